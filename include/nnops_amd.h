@@ -1,0 +1,143 @@
+/* nnops_amd.h -- C ABI of the MI355X (gfx950) quantized-matmul path.
+ *
+ * This is the drop-in boundary below nnops' operator front end. In nnops the
+ * CPU and CUDA backends are bound to `MatMul` / `Linear` through one kernel
+ * function pointer per op, `Status fn(attrs, TensorView& out, span<const
+ * TensorView> in, const ComputeContext&, void* workspace)`
+ * (src/ops/dispatch.hpp:42-43, 62-96); the CUDA side of the integer route
+ * flattens the views into a POD parameter block and launches on
+ * `ctx.cuda_stream` (src/backend/cuda/matmul/matmul.cu:34-98,
+ * src/backend/cuda/matmul/matmul_i8_common.cuh). The entry points below are
+ * that launch boundary for a `Backend::HIP`: plain device pointers, element
+ * strides taken from `TensorView::row_stride_elems()`, scalars, a
+ * caller-provided device workspace and an opaque `hipStream_t`.
+ *
+ * Contract (all entry points):
+ *   - every pointer in an args block is a DEVICE pointer (the C++ front end
+ *     stages host QuantParams tables into the workspace);
+ *   - nothing is allocated and nothing synchronises the host: work is enqueued
+ *     on `stream` and the call returns;
+ *   - `workspace` must hold at least the matching *_workspace_size() bytes
+ *     (NNOPS_NOT_INITIALIZED otherwise) and must not be shared by calls that
+ *     may run concurrently; its contents on entry are irrelevant;
+ *   - a rejected call returns a non-zero status and enqueues nothing.
+ */
+#ifndef NNOPS_AMD_H
+#define NNOPS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: nnops::Status values (include/nnops/core/status.hpp:19-33). */
+enum {
+    NNOPS_OK = 0,
+    NNOPS_INVALID_ARGUMENT = 1,
+    NNOPS_UNSUPPORTED = 2,
+    NNOPS_NOT_INITIALIZED = 3,
+    NNOPS_OUT_OF_MEMORY = 4,
+    NNOPS_INTERNAL = 5,
+};
+
+/* Destination element types (nnops' s32/s8/u8 integer destinations,
+ * MatMulAttributes::output_dtype, include/nnops/ops/matmul.hpp:53-60; f32/f16
+ * for the Q4_1 route). */
+enum {
+    NNOPS_OUT_S32 = 0,
+    NNOPS_OUT_S8 = 1,
+    NNOPS_OUT_U8 = 2,
+    NNOPS_OUT_F32 = 3,
+    NNOPS_OUT_F16 = 4,
+};
+
+/* Activations the output pass applies (a subset of EpilogueActivateType,
+ * include/nnops/core/epilogue.hpp:22-33; the integer route of nnops honours
+ * only Relu, matmul_tile_impl.h:411). */
+enum {
+    NNOPS_ACT_NONE = 0,
+    NNOPS_ACT_RELU = 1,
+    NNOPS_ACT_GELU = 2,
+};
+
+/* Integer GEMM  C[M,N] = epilogue(A[M,K] x B[K,N]).
+ * Replaces the integer route of nnops' matmul_cuda / linear_cuda
+ * (src/backend/cuda/matmul/matmul.cu:34-98, GemmI8Params) and of matmul_cpu's
+ * I8Route (src/backend/cpu/matmul/matmul_i8.cpp:55-159).
+ *
+ * A is s8 or u8 (a_u8), [M,K] row-major with row stride lda, or [K,M] with
+ * trans_a. B is s8, [K,N] (ldb) or [N,K] with trans_b (Linear's weight).
+ * Quantization tables override their scalars when non-null: s_a/zp_a per row
+ * of A (PerToken), s_b/zp_b per output column (PerChannel), s_out_rows/
+ * zp_out_rows per output row (Epilogue Requantize table).
+ *
+ * Output pass, per element, nnops order (simd_epilogue.hpp:341-467):
+ *   v = sum (a - zp_a)(b - zp_b) + bias[n];  Relu;  for s8/u8:
+ *   q = sat(round(clamp(float(v) * ((s_a / s_out) * s_b), lo - zp, hi - zp)) + zp)
+ * with round = half away from zero (round_even = 0, nnops) or half to even.
+ *
+ * float_ep (extension, no nnops counterpart): the s8/u8 destination is
+ * produced through the f32 epilogue instead:
+ *   f = float(v) * (s_a * s_b);  r = float(C_old - zp_out) * s_out (add_to);
+ *   y = act(clamp(f [+ r if residual_pre])) [+ r otherwise];
+ *   q = sat(round(clamp(y / s_out, lo - zp, hi - zp)) + zp)
+ * which is how an s8 add_to residual and a GELU on an integer destination are
+ * defined here (nnops rejects both: linear.cpp:226). */
+typedef struct NnopsGemmI8Args {
+    const void* a;
+    const int8_t* b;
+    const int32_t* bias;        /* [N] int32, or NULL */
+    void* c;
+    int64_t m, n, k;
+    int64_t lda, ldb, ldc;      /* row strides in elements */
+    int32_t trans_a, trans_b, a_u8;
+    const float* s_a; float s_a_scalar; const int32_t* zp_a; int32_t zp_a_scalar;
+    const float* s_b; float s_b_scalar; const int32_t* zp_b; int32_t zp_b_scalar;
+    const float* s_out_rows; const int32_t* zp_out_rows; float s_out; int32_t zp_out;
+    int32_t out_kind;           /* NNOPS_OUT_S32 / S8 / U8 */
+    int32_t act;                /* NNOPS_ACT_* (integer route: NONE or RELU) */
+    int32_t round_even;
+    int32_t float_ep;
+    float min_clip, max_clip;   /* float epilogue only */
+    int32_t add_to, residual_pre; /* float epilogue only */
+} NnopsGemmI8Args;
+
+size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* args);
+int nnops_hip_gemm_i8(const NnopsGemmI8Args* args, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Q4_1-weight GEMM  C[M,N] = A[M,K] x dequant(B).
+ * Replaces nnops' fp x q4_1 route: matmul_qblock_fused (small M,
+ * src/backend/cpu/matmul/matmul_qblock_fused.cpp:174-197) and FpRoute with
+ * the Q4_1 RHS pack (matmul_helper.cpp:408-497). B is a stream of llama.cpp
+ * Q4_1 blocks (20 bytes: f16 d, f16 m, 16 nibble bytes, value = d*q + m;
+ * include/nnops/detail/q4_1.hpp:5-18):
+ *   trans_b = 1: [N] rows of ceil(K/32) blocks along K (Linear / GGUF form),
+ *   trans_b = 0: [K] rows of ceil(N/32) blocks along N,
+ * consecutive rows ldb_bytes apart. A is f16 or f32 (a_f16), C is f32 or f16
+ * (out_kind NNOPS_OUT_F32 / NNOPS_OUT_F16). Accumulation is f32. */
+typedef struct NnopsGemmQ41Args {
+    const void* a;
+    const uint8_t* b;
+    void* c;
+    int64_t m, n, k;
+    int64_t lda, ldc;           /* elements */
+    int64_t ldb_bytes;
+    int32_t trans_b, a_f16;
+    int32_t out_kind;           /* NNOPS_OUT_F32 / NNOPS_OUT_F16 */
+} NnopsGemmQ41Args;
+
+size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* args);
+int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* args, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Library version and build target, for the caller's diagnostics. */
+const char* nnops_hip_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNOPS_AMD_H */

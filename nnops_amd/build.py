@@ -1,0 +1,84 @@
+"""Build libnnops_amd.so (HIP kernels for gfx950 + the C++ front end) in-tree.
+
+    python -m nnops_amd.build        # or nnops_amd.build.build()
+
+Each translation unit is compiled by hipcc for --offload-arch=gfx950 only,
+objects go to nnops_amd/_build/, the shared library to nnops_amd/. Kernel TUs
+are compiled with -ffp-contract=off (the int8 requant and the GELU epilogue
+must round every float operation on its own to match the CPU bit for bit) and
+without packed-FP32 instruction selection.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libnnops_amd.so")
+
+SOURCES = [
+    "csrc/kernels/gemm_i8.hip",
+    "csrc/kernels/q4_1.hip",
+    "csrc/host/ops.cpp",
+    "csrc/host/capi_ops.cpp",
+]
+
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm install expected under /opt/rocm)")
+
+
+def _flags(src: str) -> list[str]:
+    common = [
+        "-std=c++20", "-O3", "-fPIC", f"--offload-arch={ARCH}",
+        "-I", os.path.join(ROOT, "include"),
+        "-I", os.path.join(PKG, "include"),
+        "-Wall", "-Wno-unused-function",
+    ]
+    if src.endswith(".hip"):
+        common += [
+            "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        ]
+    else:
+        common += ["-x", "hip"]  # host C++ that calls the HIP runtime
+    return common
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    cmd = [hipcc()] + _flags(src) + ["-c", os.path.join(PKG, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source and link the shared library; returns its path."""
+    os.makedirs(BUILD, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)

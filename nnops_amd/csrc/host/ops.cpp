@@ -1,0 +1,681 @@
+// MatMul / Linear front end for Backend::HIP: descriptor rules, workspace
+// planning and the lowering of a call onto the C ABI entry points
+// (nnops_hip_gemm_i8 / nnops_hip_gemm_q4_1).
+//
+// Follows nnops' operator front end: output-descriptor rules of
+// src/ops/matmul.cpp:49-58 and src/ops/linear.cpp:29-47, validate()'s count /
+// rank / K-agreement checks (src/ops/matmul.cpp:60-94), QuantParams routing of
+// src/backend/cpu/matmul/matmul_tile_impl.h:366-421 (A per-token scale and zero
+// point, B per-channel, output per-tensor or the epilogue's per-row
+// Requantize table), batch broadcasting over the leading dims.
+#include "nnops/ops/linear.hpp"
+#include "nnops/ops/matmul.hpp"
+#include "nnops_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <cstring>
+#include <limits>
+
+namespace nnops {
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+Status from_code(int c)
+{
+    switch (c) {
+    case NNOPS_OK: return Status::ok;
+    case NNOPS_INVALID_ARGUMENT: return Status::invalid_argument;
+    case NNOPS_UNSUPPORTED: return Status::unsupported;
+    case NNOPS_NOT_INITIALIZED: return Status::not_initialized;
+    case NNOPS_OUT_OF_MEMORY: return Status::out_of_memory;
+    default: return Status::internal;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Problem geometry shared by MatMul and Linear.
+// ---------------------------------------------------------------------------
+struct Geometry {
+    int64_t m = 0, n = 0, k = 0;
+    int64_t batch = 1;
+    bool trans_a = false, trans_b = false;
+    // leading (batch) dims, broadcast
+    int64_t nd = 0;
+    int64_t out_batch[TensorDesc::kMaxRank]{};
+    int64_t a_batch[TensorDesc::kMaxRank]{};
+    int64_t b_batch[TensorDesc::kMaxRank]{};
+};
+
+/// MatMul geometry: A [..., M, K] (trans_a: [..., K, M]), B [..., K, N]
+/// (trans_b: [..., N, K]); a q4_1 B's innermost dim counts values, not blocks.
+Status matmul_geometry(const TensorDesc& a, const TensorDesc& b, bool ta, bool tb, Geometry& g)
+{
+    if (a.rank < 2 || b.rank < 2) {
+        return Status::invalid_argument;
+    }
+    const int64_t am = a.dims[static_cast<size_t>(a.rank - 2)];
+    const int64_t ak = a.dims[static_cast<size_t>(a.rank - 1)];
+    const int64_t b0 = b.dims[static_cast<size_t>(b.rank - 2)];
+    const int64_t b1 = b.dims[static_cast<size_t>(b.rank - 1)];
+    g.trans_a = ta;
+    g.trans_b = tb;
+    g.m = ta ? ak : am;
+    g.k = ta ? am : ak;
+    const int64_t kb = tb ? b1 : b0;
+    g.n = tb ? b0 : b1;
+    if (kb != g.k) {
+        return Status::invalid_argument;
+    }
+    g.nd = std::max(a.rank, b.rank) - 2;
+    g.batch = 1;
+    for (int64_t i = 0; i < g.nd; ++i) {
+        const int64_t ai = i - (g.nd - (a.rank - 2));
+        const int64_t bi = i - (g.nd - (b.rank - 2));
+        const int64_t da = ai >= 0 ? a.dims[static_cast<size_t>(ai)] : 1;
+        const int64_t db = bi >= 0 ? b.dims[static_cast<size_t>(bi)] : 1;
+        if (da != db && da != 1 && db != 1) {
+            return Status::invalid_argument;
+        }
+        g.a_batch[i] = da;
+        g.b_batch[i] = db;
+        g.out_batch[i] = std::max(da, db);
+        g.batch *= g.out_batch[i];
+    }
+    return Status::ok;
+}
+
+// ---------------------------------------------------------------------------
+// Host vs device tables. QuantParams / Epilogue tables may be host arrays
+// (staged into the workspace, as nnops' CUDA backend stages them) or device
+// arrays (read in place).
+// ---------------------------------------------------------------------------
+bool is_device_pointer(const void* p)
+{
+    if (p == nullptr) {
+        return false;
+    }
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof(attr));
+    const hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged ||
+           attr.type == hipMemoryTypeArray;
+}
+
+struct Stager {
+    char* base = nullptr;
+    size_t used = 0, cap = 0;
+    hipStream_t stream = nullptr;
+    bool ok = true;
+
+    template <class T>
+    const T* stage(const T* p, int64_t count)
+    {
+        if (p == nullptr || count <= 0 || is_device_pointer(p)) {
+            return p;
+        }
+        const size_t bytes = align_up(static_cast<size_t>(count) * sizeof(T));
+        if (base == nullptr || used + bytes > cap) {
+            ok = false;
+            return p;
+        }
+        char* dst = base + used;
+        used += bytes;
+        if (hipMemcpyAsync(dst, p, static_cast<size_t>(count) * sizeof(T), hipMemcpyHostToDevice,
+                           stream) != hipSuccess) {
+            ok = false;
+        }
+        return reinterpret_cast<const T*>(dst);
+    }
+};
+
+/// Staging bytes a call may need: per-row (A scale/zp, output scale/zp) and
+/// per-column (B scale/zp) tables.
+size_t staging_bytes(int64_t m, int64_t n)
+{
+    return 4 * align_up(static_cast<size_t>(m) * 4) + 2 * align_up(static_cast<size_t>(n) * 4);
+}
+
+/// Read a scalar that may sit in host or device memory; device memory is not
+/// read from the host (that would synchronise), so it reports failure.
+bool host_scalar(const float* p, float& out)
+{
+    if (is_device_pointer(p)) {
+        return false;
+    }
+    out = *p;
+    return true;
+}
+bool host_scalar(const int32_t* p, int32_t& out)
+{
+    if (is_device_pointer(p)) {
+        return false;
+    }
+    out = *p;
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// The quantized call, independent of MatMul vs Linear.
+// ---------------------------------------------------------------------------
+struct QuantCall {
+    bool trans_a = false, trans_b = false;
+    Epilogue ep{};
+    bool add_to = false, residual_pre = false;
+    bool round_even = false, float_ep = false;
+};
+
+int32_t out_kind_of(DataType dt)
+{
+    switch (dt) {
+    case DataType::s32: return NNOPS_OUT_S32;
+    case DataType::s8: return NNOPS_OUT_S8;
+    case DataType::u8: return NNOPS_OUT_U8;
+    case DataType::f32: return NNOPS_OUT_F32;
+    case DataType::f16: return NNOPS_OUT_F16;
+    default: return -1;
+    }
+}
+
+NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, const QuantCall& q, int32_t out_kind)
+{
+    NnopsGemmI8Args x{};
+    x.m = g.m;
+    x.n = g.n;
+    x.k = g.k;
+    x.trans_a = q.trans_a;
+    x.trans_b = q.trans_b;
+    x.lda = g.trans_a ? g.m : g.k;
+    x.ldb = g.trans_b ? g.k : g.n;
+    x.ldc = g.n;
+    x.out_kind = out_kind;
+    return x;
+}
+
+NnopsGemmQ41Args q41_args_from_geometry(const Geometry& g, const QuantCall& q, int32_t out_kind)
+{
+    NnopsGemmQ41Args x{};
+    x.m = g.m;
+    x.n = g.n;
+    x.k = g.k;
+    x.trans_b = q.trans_b;
+    x.a_f16 = 1;
+    x.lda = g.k;
+    x.ldc = g.n;
+    x.ldb_bytes = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, q.trans_b ? g.k : g.n));
+    x.out_kind = out_kind;
+    return x;
+}
+
+size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDesc* out,
+                       const QuantCall& q, DataType out_dtype)
+{
+    Geometry g;
+    if (!is_ok(matmul_geometry(a, b, q.trans_a, q.trans_b, g))) {
+        return 0;
+    }
+    if (is_int8_matmul(a.dtype, b.dtype)) {
+        const NnopsGemmI8Args x = i8_args_from_geometry(g, q, out_kind_of(out_dtype));
+        return staging_bytes(g.m, g.n) + align_up(nnops_hip_gemm_i8_workspace_size(&x));
+    }
+    if (is_q4_1_matmul(a.dtype, b.dtype)) {
+        const DataType odt = out != nullptr ? out->dtype : a.dtype;
+        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, out_kind_of(odt));
+        x.a_f16 = a.dtype == DataType::f16;
+        return align_up(nnops_hip_gemm_q4_1_workspace_size(&x));
+    }
+    return 0;
+}
+
+/// Byte offset of batch index `bi` for an operand whose leading dims are
+/// `dims` (broadcast against `out`), given its row pitch and the rows per
+/// matrix.
+int64_t batch_offset(int64_t bi, const Geometry& g, const int64_t* dims, int64_t matrix_bytes)
+{
+    int64_t off = 0, stride = matrix_bytes, rem = bi;
+    // walk dims from innermost batch axis outward
+    std::array<int64_t, TensorDesc::kMaxRank> coord{};
+    for (int64_t d = g.nd - 1; d >= 0; --d) {
+        coord[static_cast<size_t>(d)] = rem % g.out_batch[d];
+        rem /= g.out_batch[d];
+    }
+    for (int64_t d = g.nd - 1; d >= 0; --d) {
+        if (dims[d] != 1) {
+            off += coord[static_cast<size_t>(d)] * stride;
+        }
+        stride *= dims[d];
+    }
+    return off;
+}
+
+Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView> inputs,
+                 const ComputeContext& ctx, void* workspace, size_t ws_bytes)
+{
+    const TensorView& a = inputs[0];
+    const TensorView& b = inputs[1];
+    const TensorView* bias = inputs.size() > 2 ? &inputs[2] : nullptr;
+    Geometry g;
+    if (Status s = matmul_geometry(a.desc(), b.desc(), q.trans_a, q.trans_b, g); !is_ok(s)) {
+        return s;
+    }
+    // The destination must be [..., M, N] with the broadcast batch.
+    if (out.rank() < 2 || out.shape(out.rank() - 2) != g.m || out.shape(out.rank() - 1) != g.n ||
+        out.numel() != g.batch * g.m * g.n) {
+        return Status::invalid_argument;
+    }
+    if (g.m == 0 || g.n == 0 || g.batch == 0) {
+        return Status::ok;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(ctx.hip_stream);
+    const int64_t a_rows_per = g.trans_a ? g.k : g.m;
+    const int64_t b_rows_per = g.trans_b ? g.n : g.k;
+
+    if (is_int8_matmul(a.data_type(), b.data_type())) {
+        const int32_t ok = out_kind_of(out.data_type());
+        if (ok != NNOPS_OUT_S32 && ok != NNOPS_OUT_S8 && ok != NNOPS_OUT_U8) {
+            return Status::unsupported;  // dequantizing destinations: not on this backend
+        }
+        if (bias != nullptr && (bias->data_type() != DataType::s32 || bias->numel() != g.n)) {
+            return Status::invalid_argument;
+        }
+        const bool float_ep = q.float_ep || q.add_to;
+        if (q.add_to && ok == NNOPS_OUT_S32) {
+            return Status::unsupported;
+        }
+        NnopsGemmI8Args x = i8_args_from_geometry(g, q, ok);
+        x.a_u8 = a.data_type() == DataType::u8;
+        x.lda = a.row_stride_elems();
+        x.ldb = b.row_stride_elems();
+        x.ldc = out.row_stride_elems();
+        x.bias = bias != nullptr ? bias->ptr<const int32_t>() : nullptr;
+        x.round_even = q.round_even;
+        x.float_ep = float_ep && ok != NNOPS_OUT_S32;
+        x.add_to = q.add_to;
+        x.residual_pre = q.residual_pre;
+        x.min_clip = q.ep.min_clip;
+        x.max_clip = q.ep.max_clip;
+        switch (q.ep.type) {
+        case EpilogueActivateType::None: x.act = NNOPS_ACT_NONE; break;
+        case EpilogueActivateType::Relu: x.act = NNOPS_ACT_RELU; break;
+        case EpilogueActivateType::Gelu: x.act = x.float_ep ? NNOPS_ACT_GELU : NNOPS_ACT_NONE; break;
+        default:
+            // nnops' integer pass honours only Relu and ignores the rest
+            // (matmul_i8.cpp:100-103); the float epilogue has no route for them.
+            if (x.float_ep) {
+                return Status::unsupported;
+            }
+            x.act = NNOPS_ACT_NONE;
+        }
+        if (!x.float_ep) {
+            // clip bounds are not applied on an integer destination (nnops)
+            x.min_clip = -std::numeric_limits<float>::infinity();
+            x.max_clip = std::numeric_limits<float>::infinity();
+        }
+
+        Stager st;
+        st.base = static_cast<char*>(workspace);
+        st.cap = workspace != nullptr ? std::min(ws_bytes, staging_bytes(g.m, g.n)) : 0;
+        st.stream = stream;
+        const QuantParams& qa = a.quant_params();
+        const QuantParams& qb = b.quant_params();
+        const QuantParams& qc = out.quant_params();
+        x.s_a = st.stage(qa.scale_data, g.m);
+        x.s_a_scalar = qa.scale;
+        x.zp_a = st.stage(qa.zero_point_data, g.m);
+        x.zp_a_scalar = qa.zero_point;
+        x.s_b = st.stage(qb.scale_data, g.n);
+        x.s_b_scalar = qb.scale;
+        x.zp_b = st.stage(qb.zero_point_data, g.n);
+        x.zp_b_scalar = qb.zero_point;
+        x.s_out = qc.scale;
+        x.zp_out = qc.zero_point;
+        if (qc.scale_data != nullptr && !host_scalar(qc.scale_data, x.s_out)) {
+            return Status::unsupported;
+        }
+        if (qc.zero_point_data != nullptr && !host_scalar(qc.zero_point_data, x.zp_out)) {
+            return Status::unsupported;
+        }
+        if (q.ep.quant == EpilogueQuantType::Requantize && q.ep.quant_param_count > 0) {
+            if (q.ep.quant_param_count > 1) {
+                if (q.ep.quant_param_count < g.m) {
+                    return Status::invalid_argument;
+                }
+                x.s_out_rows = st.stage(q.ep.quant_scales, g.m);
+                x.zp_out_rows = st.stage(q.ep.quant_zero_points, g.m);
+            } else {
+                if (q.ep.quant_scales != nullptr && !host_scalar(q.ep.quant_scales, x.s_out)) {
+                    return Status::unsupported;
+                }
+                x.zp_out = 0;
+                if (q.ep.quant_zero_points != nullptr && !host_scalar(q.ep.quant_zero_points, x.zp_out)) {
+                    return Status::unsupported;
+                }
+            }
+        }
+        if (!st.ok) {
+            return Status::not_initialized;
+        }
+        const size_t stage_cap = staging_bytes(g.m, g.n);
+        const size_t need = nnops_hip_gemm_i8_workspace_size(&x);
+        if (need > 0 && (workspace == nullptr || ws_bytes < stage_cap + need)) {
+            return Status::not_initialized;
+        }
+        void* ws = need > 0 ? static_cast<char*>(workspace) + stage_cap : nullptr;
+
+        const int64_t a_mat = a_rows_per * a.pitch();
+        const int64_t b_mat = b_rows_per * b.pitch();
+        const int64_t c_mat = g.m * out.pitch();
+        for (int64_t bi = 0; bi < g.batch; ++bi) {
+            NnopsGemmI8Args xb = x;
+            xb.a = a.ptr<const char>() + batch_offset(bi, g, g.a_batch, a_mat);
+            xb.b = reinterpret_cast<const int8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
+            xb.c = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
+            const int rc = nnops_hip_gemm_i8(&xb, ws, need, stream);
+            if (rc != NNOPS_OK) {
+                return from_code(rc);
+            }
+        }
+        return Status::ok;
+    }
+
+    if (is_q4_1_matmul(a.data_type(), b.data_type())) {
+        if (g.trans_a || bias != nullptr || q.add_to || q.ep.type != EpilogueActivateType::None ||
+            epilogue_is_active(q.ep)) {
+            return Status::unsupported;
+        }
+        const int32_t ok = out_kind_of(out.data_type());
+        if (ok != NNOPS_OUT_F32 && !(ok == NNOPS_OUT_F16 && a.data_type() == DataType::f16)) {
+            return Status::unsupported;
+        }
+        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, ok);
+        x.a_f16 = a.data_type() == DataType::f16;
+        x.lda = a.row_stride_elems();
+        x.ldc = out.row_stride_elems();
+        x.ldb_bytes = b.pitch();
+        const size_t need = nnops_hip_gemm_q4_1_workspace_size(&x);
+        if (need > 0 && (workspace == nullptr || ws_bytes < need)) {
+            return Status::not_initialized;
+        }
+        const int64_t a_mat = a_rows_per * a.pitch();
+        const int64_t b_mat = b_rows_per * b.pitch();
+        const int64_t c_mat = g.m * out.pitch();
+        for (int64_t bi = 0; bi < g.batch; ++bi) {
+            NnopsGemmQ41Args xb = x;
+            xb.a = a.ptr<const char>() + batch_offset(bi, g, g.a_batch, a_mat);
+            xb.b = reinterpret_cast<const uint8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
+            xb.c = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
+            const int rc = nnops_hip_gemm_q4_1(&xb, workspace, need, stream);
+            if (rc != NNOPS_OK) {
+                return from_code(rc);
+            }
+        }
+        return Status::ok;
+    }
+    return Status::unsupported;
+}
+
+Status check_views(std::span<TensorView> outputs, std::span<const TensorView> inputs)
+{
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        return Status::invalid_argument;
+    }
+    for (const TensorView& v : inputs) {
+        if (v.is_empty() && v.numel() != 0) {
+            return Status::invalid_argument;
+        }
+    }
+    if (outputs[0].is_empty() && outputs[0].numel() != 0) {
+        return Status::invalid_argument;
+    }
+    return Status::ok;
+}
+
+TensorDesc output_desc(const Geometry& g, DataType dt, const TensorDesc& a, const TensorDesc& b)
+{
+    TensorDesc d;
+    d.rank = g.nd + 2;
+    for (int64_t i = 0; i < g.nd; ++i) {
+        d.dims[static_cast<size_t>(i)] = g.out_batch[i];
+    }
+    d.dims[static_cast<size_t>(g.nd)] = g.m;
+    d.dims[static_cast<size_t>(g.nd + 1)] = g.n;
+    d.dtype = dt;
+    (void)a;
+    (void)b;
+    return d;
+}
+
+}  // namespace
+
+// ===========================================================================
+// MatMul
+// ===========================================================================
+std::unique_ptr<MatMul> MatMul::create(const MatMulAttributes& attrs, Backend backend)
+{
+    return std::unique_ptr<MatMul>(new MatMul(attrs, backend));
+}
+
+std::vector<TensorDesc> MatMul::getOutputTensorDesc(std::span<const TensorDesc> inputs) const
+{
+    if (inputs.size() < 2) {
+        return {};
+    }
+    Geometry g;
+    if (!is_ok(matmul_geometry(inputs[0], inputs[1], attrs_.transpose_a, attrs_.transpose_b, g))) {
+        return {};
+    }
+    const DataType dt = is_int8_matmul(inputs[0].dtype, inputs[1].dtype) ? attrs_.output_dtype
+                                                                         : inputs[0].dtype;
+    return {output_desc(g, dt, inputs[0], inputs[1])};
+}
+
+Status MatMul::validate(std::span<const TensorDesc> inputs, std::span<const TensorDesc> outputs) const
+{
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        return Status::invalid_argument;
+    }
+    Geometry g;
+    return matmul_geometry(inputs[0], inputs[1], attrs_.transpose_a, attrs_.transpose_b, g);
+}
+
+size_t MatMul::getWorkspaceSize(std::span<const TensorDesc> inputs,
+                                std::span<const TensorDesc> outputs) const
+{
+    if (inputs.size() < 2) {
+        return 0;
+    }
+    QuantCall q;
+    q.trans_a = attrs_.transpose_a;
+    q.trans_b = attrs_.transpose_b;
+    const DataType odt = !outputs.empty() ? outputs[0].dtype : attrs_.output_dtype;
+    return quant_workspace(inputs[0], inputs[1], outputs.empty() ? nullptr : &outputs[0], q, odt);
+}
+
+Status MatMul::compute(std::span<TensorView> outputs, std::span<const TensorView> inputs,
+                       const ComputeContext& ctx, void* workspace)
+{
+    if (Status s = check_views(outputs, inputs); !is_ok(s)) {
+        return s;
+    }
+    if (backend_ != Backend::HIP) {
+        return Status::unsupported;
+    }
+    const TensorDesc descs_in[3] = {inputs[0].desc(), inputs[1].desc(),
+                                    inputs.size() > 2 ? inputs[2].desc() : TensorDesc{}};
+    const TensorDesc desc_out = outputs[0].desc();
+    if (Status s = validate(std::span<const TensorDesc>(descs_in, inputs.size()),
+                            std::span<const TensorDesc>(&desc_out, 1));
+        !is_ok(s)) {
+        return s;
+    }
+    if (is_int8_matmul(inputs[0].data_type(), inputs[1].data_type()) &&
+        outputs[0].data_type() != attrs_.output_dtype) {
+        return Status::invalid_argument;
+    }
+    QuantCall q;
+    q.trans_a = attrs_.transpose_a;
+    q.trans_b = attrs_.transpose_b;
+    q.ep = attrs_.epilogue;
+    q.residual_pre = attrs_.residual_pre_activation;
+    q.add_to = attrs_.residual_pre_activation;  // MatMul's residual is the pre-activation fold
+    q.round_even = attrs_.requant_round_even;
+    q.float_ep = attrs_.float_epilogue;
+    const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),
+                                       std::span<const TensorDesc>(&desc_out, 1));
+    return run_quant(q, outputs[0], inputs, ctx, workspace, workspace != nullptr ? ws : 0);
+}
+
+// ===========================================================================
+// Linear
+// ===========================================================================
+std::unique_ptr<Linear> Linear::create(const LinearAttributes& attrs, Backend backend)
+{
+    return std::unique_ptr<Linear>(new Linear(attrs, backend));
+}
+
+namespace {
+
+// Linear's X [..., K] flattened to [rows, K]; W [N, K] (q4_1: K in blocks).
+bool linear_descs(std::span<const TensorDesc> inputs, TensorDesc& x2, TensorDesc& w)
+{
+    if (inputs.size() < 2 || inputs[0].rank < 1 || inputs[1].rank != 2) {
+        return false;
+    }
+    const TensorDesc& x = inputs[0];
+    x2 = TensorDesc{};
+    x2.rank = 2;
+    x2.dims[0] = x.rank >= 2 ? x.rows() : 1;
+    x2.dims[1] = x.cols();
+    x2.dtype = x.dtype;
+    x2.row_stride_elems = x.row_stride_elems;
+    w = inputs[1];
+    return true;
+}
+
+DataType linear_out_dtype(const LinearAttributes& attrs, DataType x, DataType w)
+{
+    if (is_int8_matmul(x, w)) {
+        const DataType o = attrs.output_dtype;
+        const bool known = o == DataType::f16 || o == DataType::f32 || o == DataType::s32 ||
+                           o == DataType::s8 || o == DataType::u8;
+        return known ? o : DataType::f32;
+    }
+    return x;
+}
+
+}  // namespace
+
+std::vector<TensorDesc> Linear::getOutputTensorDesc(std::span<const TensorDesc> inputs) const
+{
+    TensorDesc x2, w;
+    if (!linear_descs(inputs, x2, w)) {
+        return {};
+    }
+    TensorDesc d = inputs[0];
+    d.dims[static_cast<size_t>(d.rank - 1)] = w.dims[0];
+    d.dtype = linear_out_dtype(attrs_, inputs[0].dtype, w.dtype);
+    d.row_stride_elems = 0;
+    return {d};
+}
+
+Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const TensorDesc> outputs) const
+{
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        return Status::invalid_argument;
+    }
+    if (attrs_.gated) {
+        return Status::unsupported;
+    }
+    TensorDesc x2, w;
+    if (!linear_descs(inputs, x2, w)) {
+        return Status::invalid_argument;
+    }
+    if (x2.dims[1] != w.dims[1]) {
+        return Status::invalid_argument;
+    }
+    if (inputs.size() > 2 && inputs[2].numel() != w.dims[0]) {
+        return Status::invalid_argument;
+    }
+    return Status::ok;
+}
+
+size_t Linear::getWorkspaceSize(std::span<const TensorDesc> inputs,
+                                std::span<const TensorDesc> outputs) const
+{
+    TensorDesc x2, w;
+    if (!linear_descs(inputs, x2, w)) {
+        return 0;
+    }
+    QuantCall q;
+    q.trans_b = true;
+    const DataType odt = !outputs.empty() ? outputs[0].dtype
+                                          : linear_out_dtype(attrs_, x2.dtype, w.dtype);
+    TensorDesc o;
+    o.rank = 2;
+    o.dims[0] = x2.dims[0];
+    o.dims[1] = w.dims[0];
+    o.dtype = odt;
+    return quant_workspace(x2, w, &o, q, odt);
+}
+
+Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView> inputs,
+                       const ComputeContext& ctx, void* workspace)
+{
+    if (Status s = check_views(outputs, inputs); !is_ok(s)) {
+        return s;
+    }
+    if (backend_ != Backend::HIP) {
+        return Status::unsupported;
+    }
+    const TensorDesc descs_in[3] = {inputs[0].desc(), inputs[1].desc(),
+                                    inputs.size() > 2 ? inputs[2].desc() : TensorDesc{}};
+    const TensorDesc desc_out = outputs[0].desc();
+    if (Status s = validate(std::span<const TensorDesc>(descs_in, inputs.size()),
+                            std::span<const TensorDesc>(&desc_out, 1));
+        !is_ok(s)) {
+        return s;
+    }
+    const TensorView& x = inputs[0];
+    const TensorView& wv = inputs[1];
+    TensorView& y = outputs[0];
+    if (y.data_type() != linear_out_dtype(attrs_, x.data_type(), wv.data_type()) &&
+        !(is_q4_1_matmul(x.data_type(), wv.data_type()) && y.data_type() == DataType::f32)) {
+        return Status::invalid_argument;
+    }
+    // Flatten the leading dims: [..., K] -> [rows, K], [..., N] -> [rows, N].
+    const int64_t rows = x.total_rows();
+    if (y.total_rows() != rows || y.shape(y.rank() - 1) != wv.shape(0)) {
+        return Status::invalid_argument;
+    }
+    const int64_t xs[2] = {rows, x.shape(x.rank() - 1)};
+    const int64_t ys[2] = {rows, wv.shape(0)};
+    const int64_t x_pitch = x.rank() >= 2 ? x.pitch()
+                                          : static_cast<int64_t>(data_type_row_bytes(x.data_type(), xs[1]));
+    const int64_t y_pitch = y.rank() >= 2 ? y.pitch()
+                                          : static_cast<int64_t>(data_type_row_bytes(y.data_type(), ys[1]));
+    TensorView x2(xs, x.data_type(), x.ptr<void>(), x_pitch, TensorLayout::Dense, x.quant_params());
+    TensorView y2(ys, y.data_type(), y.ptr<void>(), y_pitch, TensorLayout::Dense, y.quant_params());
+    TensorView ins[3] = {x2, wv, inputs.size() > 2 ? inputs[2] : TensorView{}};
+
+    QuantCall q;
+    q.trans_b = true;
+    q.ep = attrs_.epilogue;
+    q.add_to = attrs_.add_to;
+    q.residual_pre = attrs_.add_to && attrs_.residual_pre_activation;
+    q.round_even = attrs_.requant_round_even;
+    q.float_ep = attrs_.float_epilogue;
+    const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),
+                                       std::span<const TensorDesc>(&desc_out, 1));
+    return run_quant(q, y2, std::span<const TensorView>(ins, inputs.size()), ctx, workspace,
+                     workspace != nullptr ? ws : 0);
+}
+
+}  // namespace nnops

@@ -1,0 +1,218 @@
+// Device-side building blocks shared by the gfx950 kernels: vector types, the
+// int8 output pass (compensate -> bias -> Relu -> requant) and the float
+// epilogue, written so every float operation rounds on its own (these TUs are
+// compiled with -ffp-contract=off), which is what makes integer outputs
+// bit-identical to nnops' scalar requant.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nnops_amd.h"
+
+namespace nnops_amd {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Epilogue parameters, resolved once on the host (device pointers only).
+// ---------------------------------------------------------------------------
+struct EpiParams {
+    const int32_t* bias;       // [N] int32 (integer outputs) or nullptr
+    const int32_t* r_a;        // [M] sum_k A (true values), or nullptr
+    const int32_t* r_b;        // [N] sum_k B, or nullptr
+    const float* s_a;          // [M] or nullptr -> s_a_scalar
+    const int32_t* zp_a;       // [M] or nullptr -> zp_a_scalar
+    const float* s_b;          // [N] or nullptr -> s_b_scalar
+    const int32_t* zp_b;       // [N] or nullptr -> zp_b_scalar
+    const float* s_out_rows;   // [M] or nullptr -> s_out
+    const int32_t* zp_out_rows;
+    float s_a_scalar, s_b_scalar, s_out;
+    int32_t zp_a_scalar, zp_b_scalar, zp_out;
+    int32_t a_off;             // shift left in the accumulate: -128 for a u8 A read as s8
+    int32_t k;
+    int32_t out_kind;          // NNOPS_OUT_*
+    int32_t act;               // NNOPS_ACT_*
+    int32_t round_even;
+    int32_t float_ep;
+    float min_clip, max_clip;
+    int32_t add_to, residual_pre;
+    int32_t compensate;        // any of r_a / r_b is live
+};
+
+// Per-row constants of the output pass.
+struct EpiRow {
+    int32_t zp_a, r_a, zp_out;
+    float s_a, s_out, row_k;
+};
+
+__device__ __forceinline__ EpiRow epi_row(const EpiParams& p, int m)
+{
+    EpiRow r;
+    r.zp_a = p.zp_a ? p.zp_a[m] : p.zp_a_scalar;
+    r.r_a = p.r_a ? p.r_a[m] : 0;
+    r.s_a = p.s_a ? p.s_a[m] : p.s_a_scalar;
+    r.s_out = p.s_out_rows ? p.s_out_rows[m] : p.s_out;
+    r.zp_out = p.zp_out_rows ? p.zp_out_rows[m] : p.zp_out;
+    r.row_k = __fdiv_rn(r.s_a, r.s_out);
+    return r;
+}
+
+// Per-column constants of the output pass.
+struct EpiCol {
+    int32_t bias, zp_b, r_b;
+    float s_b;
+};
+
+__device__ __forceinline__ EpiCol epi_col(const EpiParams& p, int n)
+{
+    EpiCol c;
+    c.bias = p.bias ? p.bias[n] : 0;
+    c.zp_b = p.zp_b ? p.zp_b[n] : p.zp_b_scalar;
+    c.r_b = p.r_b ? p.r_b[n] : 0;
+    c.s_b = p.s_b ? p.s_b[n] : p.s_b_scalar;
+    return c;
+}
+
+// Recover sum_k (a - zp_a)(b - zp_b) from the raw accumulate: the same algebra
+// as nnops' matmul_int8_compensate, with a_off the shift the kernel left in.
+__device__ __forceinline__ int32_t epi_compensate(const EpiParams& p, const EpiRow& r,
+                                                  const EpiCol& c, int32_t raw)
+{
+    if (!p.compensate) {
+        return raw;
+    }
+    return raw - (p.a_off + r.zp_a) * c.r_b - c.zp_b * r.r_a + p.k * r.zp_a * c.zp_b;
+}
+
+__device__ __forceinline__ float round_half_away(float x)
+{
+    return __builtin_truncf(__fadd_rn(x, __builtin_copysignf(0.5f, x)));
+}
+
+__device__ __forceinline__ int32_t requant_clamped(float x, int32_t zp, bool u8, bool even)
+{
+    const float zpf = (float)zp;
+    const float lo = __fsub_rn(u8 ? 0.0f : -128.0f, zpf);
+    const float hi = __fsub_rn(u8 ? 255.0f : 127.0f, zpf);
+    x = x < lo ? lo : x;
+    x = hi < x ? hi : x;
+    const float rr = even ? __builtin_rintf(x) : round_half_away(x);
+    return (int32_t)rr + zp;
+}
+
+// tanh(|x|) = (1 - t)/(1 + t), t = exp(-2|x|), exp by Cody & Waite's reduction
+// (Software Manual for the Elementary Functions, 1980) and the degree-7 Taylor
+// polynomial of exp(-r) on |r| <= ln2/2 in Horner form. Built only from
+// correctly rounded +,-,*,/ and floor, so the host evaluates the same bits.
+__device__ __forceinline__ float tanh_cw(float x)
+{
+    const float ax = __builtin_fabsf(x);
+    if (!(ax < 9.0f)) {
+        return (x != x) ? x : __builtin_copysignf(1.0f, x);
+    }
+    const float y = __fadd_rn(ax, ax);
+    const float n = __builtin_floorf(__fadd_rn(__fmul_rn(y, 1.44269504088896341f), 0.5f));
+    const float r = __fsub_rn(__fsub_rn(y, __fmul_rn(n, 0.693145751953125f)),
+                              __fmul_rn(n, 1.42860682030941723e-06f));
+    const float nr = -r;
+    float q = 1.98412698412698413e-04f;
+    q = __fadd_rn(__fmul_rn(q, nr), 1.38888888888888889e-03f);
+    q = __fadd_rn(__fmul_rn(q, nr), 8.33333333333333333e-03f);
+    q = __fadd_rn(__fmul_rn(q, nr), 4.16666666666666667e-02f);
+    q = __fadd_rn(__fmul_rn(q, nr), 1.66666666666666667e-01f);
+    q = __fadd_rn(__fmul_rn(q, nr), 0.5f);
+    q = __fadd_rn(__fmul_rn(q, nr), 1.0f);
+    q = __fadd_rn(__fmul_rn(q, nr), 1.0f);
+    const int ni = (int)n;
+    const float scale = __int_as_float((127 - ni) << 23);
+    const float t = __fmul_rn(q, scale);
+    const float th = __fdiv_rn(__fsub_rn(1.0f, t), __fadd_rn(1.0f, t));
+    return __builtin_copysignf(th, x);
+}
+
+// GELU, tanh form, in nnops' operation order: 0.5x(1 + tanh(c(x + 0.044715x^3))).
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+    const float c = 0.7978845608028654f;
+    const float x3 = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
+    const float inner = __fmul_rn(c, __fadd_rn(x, x3));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanh_cw(inner)));
+}
+
+__device__ __forceinline__ float apply_act(const EpiParams& p, float x)
+{
+    x = x < p.min_clip ? p.min_clip : x;
+    x = p.max_clip < x ? p.max_clip : x;
+    if (p.act == NNOPS_ACT_RELU) {
+        return x > 0.0f ? x : 0.0f;
+    }
+    if (p.act == NNOPS_ACT_GELU) {
+        return gelu_tanh(x);
+    }
+    return x;
+}
+
+// The whole output pass for one element: raw int32 accumulate in, destination
+// written. `c` is the row base of the destination, `n` the column.
+__device__ __forceinline__ void epi_store(const EpiParams& p, const EpiRow& r, const EpiCol& col,
+                                          int32_t raw, void* crow, int n)
+{
+    int32_t v = epi_compensate(p, r, col, raw);
+    if (p.out_kind == NNOPS_OUT_S32) {
+        v += col.bias;
+        if (p.act == NNOPS_ACT_RELU) {
+            v = v < 0 ? 0 : v;
+        }
+        static_cast<int32_t*>(crow)[n] = v;
+        return;
+    }
+    const bool u8 = p.out_kind == NNOPS_OUT_U8;
+    int32_t q;
+    if (!p.float_ep) {
+        v += col.bias;
+        if (p.act == NNOPS_ACT_RELU) {
+            v = v < 0 ? 0 : v;
+        }
+        const float req = __fmul_rn(r.row_k, col.s_b);
+        q = requant_clamped(__fmul_rn((float)v, req), r.zp_out, u8, p.round_even);
+    } else {
+        v += col.bias;
+        float f = __fmul_rn((float)v, __fmul_rn(r.s_a, col.s_b));
+        float res = 0.0f;
+        if (p.add_to) {
+            const int32_t old = u8 ? (int32_t) static_cast<uint8_t*>(crow)[n]
+                                   : (int32_t) static_cast<int8_t*>(crow)[n];
+            res = __fmul_rn((float)(old - r.zp_out), r.s_out);
+            if (p.residual_pre) {
+                f = __fadd_rn(f, res);
+            }
+        }
+        f = apply_act(p, f);
+        if (p.add_to && !p.residual_pre) {
+            f = __fadd_rn(f, res);
+        }
+        q = requant_clamped(__fdiv_rn(f, r.s_out), r.zp_out, u8, p.round_even);
+    }
+    if (u8) {
+        static_cast<uint8_t*>(crow)[n] = (uint8_t)q;
+    } else {
+        static_cast<int8_t*>(crow)[n] = (int8_t)q;
+    }
+}
+
+// Bytes of the destination element for an out kind.
+__host__ __device__ __forceinline__ int out_elem_bytes(int out_kind)
+{
+    return (out_kind == NNOPS_OUT_S32 || out_kind == NNOPS_OUT_F32) ? 4
+           : (out_kind == NNOPS_OUT_F16) ? 2 : 1;
+}
+
+}  // namespace nnops_amd

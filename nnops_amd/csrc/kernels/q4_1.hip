@@ -1,0 +1,625 @@
+// Q4_1-weight GEMM / GEMV on gfx950 (llama.cpp block_q4_1: f16 d, f16 m, 16
+// nibble bytes; value j = d * q_j + m, q_j the low nibble of byte j for j < 16
+// and the high nibble of byte j-16 otherwise).
+//
+// Kernels
+//   gemv_q4_1_nk   blocks along K ([N][K/32], Linear/GGUF form), small M.
+//                  A (a K-chunk of it) is staged in LDS once per block with its
+//                  per-block sums; every lane streams whole 20-byte blocks
+//                  (one dwordx4 + one dword, 64 consecutive blocks per wave
+//                  instruction pair = 1280 contiguous bytes). f16 A: nibbles are
+//                  widened with the 0x54 exponent trick (f16 0x54qq = 64 + q/16)
+//                  and dotted with v_dot2_f32_f16; the 64*sum(a) offset comes
+//                  off with the staged block sum. Bound: HBM.
+//   gemv_q4_1_kn   blocks along N ([K][N/32]), small M: a lane owns one
+//                  32-column block, waves split K, partial planes summed by
+//                  reduce_q4_1. Bound: HBM.
+//   gemm_q4_1_mfma larger M, f16 A: B tiles decoded to f16 (d*q + m in f32,
+//                  rounded once) into LDS, A tiles staged k-contiguous,
+//                  v_mfma_f32_32x32x16_f16, f32 accumulate. Bound: MFMA.
+#include "common.hpp"
+
+namespace nnops_amd {
+namespace {
+
+typedef int v4i_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+struct Q41Kern {
+    const void* a;       // f16 or f32 [M][lda]
+    const uint8_t* b;
+    void* c;
+    float* partial;      // [splits][M][N] (kn form)
+    int m, n, k;
+    int64_t lda, ldc, ldb;   // lda/ldc in elements, ldb in bytes
+    int out_f16;
+    int splits;
+};
+
+__device__ __forceinline__ float h2f(uint32_t bits16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+template <bool AF16>
+__device__ __forceinline__ float load_a(const Q41Kern& p, int m, int k)
+{
+    if constexpr (AF16) {
+        return (float)static_cast<const _Float16*>(p.a)[(int64_t)m * p.lda + k];
+    } else {
+        return static_cast<const float*>(p.a)[(int64_t)m * p.lda + k];
+    }
+}
+
+__device__ __forceinline__ void store_out(const Q41Kern& p, int m, int n, float v)
+{
+    if (p.out_f16) {
+        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
+    } else {
+        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV, blocks along K.
+// ---------------------------------------------------------------------------
+constexpr int kNkRowsPerWave = 4;
+constexpr int kNkWaves = 4;
+constexpr int kNkChunkBlocks = 256;   // K chunk staged in LDS: 256 blocks = 8192 values
+
+template <int MT, bool AF16>
+__global__ __launch_bounds__(256) void gemv_q4_1_nk(Q41Kern p)
+{
+    // A chunk, as f16 pairs (AF16) or f32, plus per-block sums sum_j a_j.
+    __shared__ uint32_t lds_a[MT][AF16 ? kNkChunkBlocks * 16 : kNkChunkBlocks * 32];
+    __shared__ float lds_asum[MT][kNkChunkBlocks];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kNkWaves + wave) * kNkRowsPerWave;
+    const int nb = (p.k + 31) / 32;
+
+    float acc[kNkRowsPerWave][MT];
+#pragma unroll
+    for (int r = 0; r < kNkRowsPerWave; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = 0.0f;
+        }
+    }
+
+    for (int cb0 = 0; cb0 < nb; cb0 += kNkChunkBlocks) {
+        const int cbn = min(kNkChunkBlocks, nb - cb0);
+        __syncthreads();
+        // Stage A[:, cb0*32 : (cb0+cbn)*32) (zero past K) and block sums.
+        for (int i = threadIdx.x; i < MT * cbn; i += 256) {
+            const int m = i / cbn;
+            const int blk = i - m * cbn;
+            const int kb = (cb0 + blk) * 32;
+            float s = 0.0f;
+            if constexpr (AF16) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int k = kb + 2 * j;
+                    const _Float16 x0 = (m < p.m && k < p.k) ? static_cast<const _Float16*>(p.a)[(int64_t)m * p.lda + k] : (_Float16)0;
+                    const _Float16 x1 = (m < p.m && k + 1 < p.k) ? static_cast<const _Float16*>(p.a)[(int64_t)m * p.lda + k + 1] : (_Float16)0;
+                    s += (float)x0 + (float)x1;
+                    lds_a[m][blk * 16 + j] = (uint32_t)__builtin_bit_cast(uint16_t, x0) |
+                                             ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+                }
+            } else {
+#pragma unroll 8
+                for (int j = 0; j < 32; ++j) {
+                    const int k = kb + j;
+                    const float x = (m < p.m && k < p.k) ? static_cast<const float*>(p.a)[(int64_t)m * p.lda + k] : 0.0f;
+                    s += x;
+                    lds_a[m][blk * 32 + j] = __float_as_uint(x);
+                }
+            }
+            lds_asum[m][blk] = s;
+        }
+        __syncthreads();
+
+        for (int blk = lane; blk < cbn; blk += 64) {
+            uint32_t raw[kNkRowsPerWave][5];
+#pragma unroll
+            for (int r = 0; r < kNkRowsPerWave; ++r) {
+                const int n = min(row0 + r, p.n - 1);
+                const uint8_t* src = p.b + (int64_t)n * p.ldb + (int64_t)(cb0 + blk) * 20;
+                const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
+                raw[r][0] = (uint32_t)x.x;
+                raw[r][1] = (uint32_t)x.y;
+                raw[r][2] = (uint32_t)x.z;
+                raw[r][3] = (uint32_t)x.w;
+                raw[r][4] = *reinterpret_cast<const uint32_t*>(src + 16);
+            }
+#pragma unroll
+            for (int r = 0; r < kNkRowsPerWave; ++r) {
+                const float d = h2f(raw[r][0] & 0xffffu);
+                const float mn = h2f(raw[r][0] >> 16);
+                if constexpr (AF16) {
+                    // h[p] = f16 pair (64 + q_2p/16, 64 + q_2p+1/16)
+                    uint32_t h[16];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t q = raw[r][1 + i];
+                        const uint32_t lo = q & 0x0f0f0f0fu;
+                        const uint32_t hi = (q >> 4) & 0x0f0f0f0fu;
+                        h[2 * i] = (lo & 0xffu) | ((lo << 8) & 0x00ff0000u) | 0x54005400u;
+                        h[2 * i + 1] = ((lo >> 16) & 0xffu) | ((lo >> 8) & 0x00ff0000u) | 0x54005400u;
+                        h[8 + 2 * i] = (hi & 0xffu) | ((hi << 8) & 0x00ff0000u) | 0x54005400u;
+                        h[8 + 2 * i + 1] = ((hi >> 16) & 0xffu) | ((hi >> 8) & 0x00ff0000u) | 0x54005400u;
+                    }
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        float s = 0.0f;
+                        const uint32_t* ap = &lds_a[m][blk * 16];
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) {
+                            s = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ap[j]),
+                                                       __builtin_bit_cast(v2h, h[j]), s, false);
+                        }
+                        const float asum = lds_asum[m][blk];
+                        // sum_j a_j (d q_j + mn) = 16 d (s - 64 asum) + mn asum
+                        const float qsum = 16.0f * (s - 64.0f * asum);
+                        acc[r][m] = fmaf(d, qsum, fmaf(mn, asum, acc[r][m]));
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        float s = 0.0f;
+                        const float* ap = reinterpret_cast<const float*>(&lds_a[m][blk * 32]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint32_t q = raw[r][1 + i];
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) {
+                                s = fmaf(ap[4 * i + b], (float)((q >> (8 * b)) & 15u), s);
+                                s = fmaf(ap[16 + 4 * i + b], (float)((q >> (8 * b + 4)) & 15u), s);
+                            }
+                        }
+                        acc[r][m] = fmaf(d, s, fmaf(mn, lds_asum[m][blk], acc[r][m]));
+                    }
+                }
+            }
+        }
+    }
+
+    // Wave reduction of every (row, m) partial.
+#pragma unroll
+    for (int r = 0; r < kNkRowsPerWave; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                v += __shfl_xor(v, off, 64);
+            }
+            acc[r][m] = v;
+        }
+    }
+    if (lane < kNkRowsPerWave * MT) {
+        const int r = lane / MT;
+        const int m = lane - r * MT;
+        float v = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < kNkRowsPerWave; ++rr) {
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) {
+                if (rr == r && mm == m) {
+                    v = acc[rr][mm];
+                }
+            }
+        }
+        const int n = row0 + r;
+        if (n < p.n && m < p.m) {
+            store_out(p, m, n, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV, blocks along N: partial[split][m][n].
+// ---------------------------------------------------------------------------
+template <int MT, bool AF16>
+__global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
+{
+    __shared__ float red[3][MT][32][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nblocks = (p.n + 31) / 32;
+    const int bn = blockIdx.x * 64 + lane;           // this lane's n block
+    const int split = blockIdx.y;
+    const int kper = (p.k + p.splits - 1) / p.splits;
+    const int k0 = split * kper;
+    const int k1 = min(p.k, k0 + kper);
+    const bool live = bn < nblocks;
+    const uint8_t* col = p.b + (int64_t)min(bn, nblocks - 1) * 20;
+
+    float acc[MT][32];
+    float accm[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        accm[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            acc[m][j] = 0.0f;
+        }
+    }
+    for (int k = k0 + wave; k < k1; k += 4) {
+        const uint8_t* src = col + (int64_t)k * p.ldb;
+        const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
+        const uint32_t q4 = *reinterpret_cast<const uint32_t*>(src + 16);
+        const uint32_t qs[4] = {(uint32_t)x.y, (uint32_t)x.z, (uint32_t)x.w, q4};
+        const float d = h2f((uint32_t)x.x & 0xffffu);
+        const float mn = h2f((uint32_t)x.x >> 16);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float a = m < p.m ? load_a<AF16>(p, m, k) : 0.0f;
+            const float ad = a * d;
+            accm[m] = fmaf(a, mn, accm[m]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    acc[m][4 * i + b] = fmaf(ad, (float)((qs[i] >> (8 * b)) & 15u), acc[m][4 * i + b]);
+                    acc[m][16 + 4 * i + b] =
+                        fmaf(ad, (float)((qs[i] >> (8 * b + 4)) & 15u), acc[m][16 + 4 * i + b]);
+                }
+            }
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                red[wave - 1][m][j][lane] = acc[m][j] + accm[m];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0 || !live) {
+        return;
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m >= p.m) {
+            continue;
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int n = bn * 32 + j;
+            const float v = acc[m][j] + accm[m] + red[0][m][j][lane] + red[1][m][j][lane] +
+                            red[2][m][j][lane];
+            if (n < p.n) {
+                p.partial[((int64_t)split * p.m + m) * p.n + n] = v;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void reduce_q4_1(Q41Kern p)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)p.m * p.n;
+    if (i >= total) {
+        return;
+    }
+    float s = 0.0f;
+    for (int sp = 0; sp < p.splits; ++sp) {
+        s += p.partial[(int64_t)sp * total + i];
+    }
+    const int m = (int)(i / p.n);
+    const int n = (int)(i - (int64_t)m * p.n);
+    store_out(p, m, n, s);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM, f16 A.
+// ---------------------------------------------------------------------------
+constexpr int kQBK = 64;                 // k values per stage (2 Q4_1 blocks)
+constexpr int kQLdsRow = kQBK * 2 + 16;  // bytes: 64 halves + 16 pad
+
+// Decode one block (raw: d|m, then 4 dwords of nibbles) to 32 f16 values.
+__device__ __forceinline__ void decode_block_f16(const uint32_t raw[5], _Float16 out[32])
+{
+    const float d = h2f(raw[0] & 0xffffu);
+    const float mn = h2f(raw[0] >> 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t q = raw[1 + i];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            out[4 * i + b] = (_Float16)fmaf(d, (float)((q >> (8 * b)) & 15u), mn);
+            out[16 + 4 * i + b] = (_Float16)fmaf(d, (float)((q >> (8 * b + 4)) & 15u), mn);
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, bool TRANS_B>
+__global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
+{
+    constexpr int T = WM * WN * 64;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int CA = BM * (kQBK * 2 / 16) / T;    // 16-byte A chunks per thread
+    // B: TRANS_B -> BN rows x 2 blocks; else 64 k rows x BN/32 blocks.
+    constexpr int NBLK = TRANS_B ? BN * 2 : kQBK * (BN / 32);
+    constexpr int CB = NBLK / T;
+    static_assert(CA >= 1 && CB >= 1 && CA * T * 16 == BM * kQBK * 2 && CB * T == NBLK, "tile");
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][BM * kQLdsRow];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][BN * kQLdsRow];
+
+    const int tiles_n = (p.n + BN - 1) / BN;
+    const int tm = blockIdx.x / tiles_n;
+    const int tn = blockIdx.x - tm * tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave / WN) * TM, wn0 = (wave % WN) * TN;
+    const int nbk = (p.k + 31) / 32;     // blocks along K (TRANS_B)
+    const int nbn = (p.n + 31) / 32;     // blocks along N (!TRANS_B)
+    const _Float16* A = static_cast<const _Float16*>(p.a);
+
+    v4i ra[CA];
+    uint32_t rb[CB][5];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i) {
+            const int idx = tid + i * T;
+            const int r = idx >> 3, c = idx & 7;       // 8 chunks of 8 halves per row
+            const int m = min(m0 + r, p.m - 1);
+            const int k = k0 + c * 8;
+            const _Float16* src = A + (int64_t)m * p.lda + k;
+            if (k + 8 <= p.k && ((p.lda & 7) == 0) && (((uintptr_t)A & 15) == 0)) {
+                ra[i] = *reinterpret_cast<const v4i*>(src);
+            } else {
+                uint16_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    h[e] = (k + e < p.k) ? __builtin_bit_cast(uint16_t, src[e]) : (uint16_t)0;
+                }
+                ra[i] = v4i{(int)(h[0] | (h[1] << 16)), (int)(h[2] | (h[3] << 16)),
+                            (int)(h[4] | (h[5] << 16)), (int)(h[6] | (h[7] << 16))};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            const int idx = tid + i * T;
+            const uint8_t* src;
+            bool live;
+            if constexpr (TRANS_B) {
+                const int r = idx >> 1, kb = (k0 >> 5) + (idx & 1);
+                live = kb < nbk;
+                src = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb + (int64_t)min(kb, nbk - 1) * 20;
+            } else {
+                const int kr = idx / (BN / 32), bn = (n0 >> 5) + idx % (BN / 32);
+                live = (k0 + kr) < p.k;
+                src = p.b + (int64_t)min(k0 + kr, p.k - 1) * p.ldb + (int64_t)min(bn, nbn - 1) * 20;
+            }
+            const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
+            rb[i][0] = live ? (uint32_t)x.x : 0u;
+            rb[i][1] = (uint32_t)x.y;
+            rb[i][2] = (uint32_t)x.z;
+            rb[i][3] = (uint32_t)x.w;
+            rb[i][4] = *reinterpret_cast<const uint32_t*>(src + 16);
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i) {
+            const int idx = tid + i * T;
+            const int r = idx >> 3, c = idx & 7;
+            *reinterpret_cast<v4i*>(&lds_a[buf][r * kQLdsRow + c * 16]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            const int idx = tid + i * T;
+            _Float16 w[32];
+            decode_block_f16(rb[i], w);
+            if constexpr (TRANS_B) {
+                const int r = idx >> 1, kb = idx & 1;
+                uint8_t* dst = &lds_b[buf][r * kQLdsRow + kb * 64];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v4i v;
+                    v.x = (int)(__builtin_bit_cast(uint16_t, w[8 * q + 0]) | (__builtin_bit_cast(uint16_t, w[8 * q + 1]) << 16));
+                    v.y = (int)(__builtin_bit_cast(uint16_t, w[8 * q + 2]) | (__builtin_bit_cast(uint16_t, w[8 * q + 3]) << 16));
+                    v.z = (int)(__builtin_bit_cast(uint16_t, w[8 * q + 4]) | (__builtin_bit_cast(uint16_t, w[8 * q + 5]) << 16));
+                    v.w = (int)(__builtin_bit_cast(uint16_t, w[8 * q + 6]) | (__builtin_bit_cast(uint16_t, w[8 * q + 7]) << 16));
+                    *reinterpret_cast<v4i*>(dst + q * 16) = v;
+                }
+            } else {
+                const int kr = idx / (BN / 32), nb = idx % (BN / 32);
+#pragma unroll
+                for (int j = 0; j < 32; ++j) {
+                    *reinterpret_cast<_Float16*>(&lds_b[buf][(nb * 32 + j) * kQLdsRow + kr * 2]) = w[j];
+                }
+            }
+        }
+    };
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            acc[i][j] = v16f{0.0f};
+        }
+    }
+
+    const int kt = (p.k + kQBK - 1) / kQBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    const int frow = lane & 31;
+    const int fk = (lane >> 5) * 16;     // bytes: 8 halves per lane group
+    for (int t = 0; t < kt; ++t) {
+        const int cur = t & 1;
+        if (t + 1 < kt) {
+            load_stage((t + 1) * kQBK);
+        }
+#pragma unroll
+        for (int ks = 0; ks < kQBK * 2; ks += 32) {    // 16 halves per MFMA step
+            v8h fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                fa[i] = *reinterpret_cast<const v8h*>(&lds_a[cur][(wm0 + i * 32 + frow) * kQLdsRow + ks + fk]);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                fb[j] = *reinterpret_cast<const v8h*>(&lds_b[cur][(wn0 + j * 32 + frow) * kQLdsRow + ks + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < kt) {
+            store_stage(cur ^ 1);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        if (n >= p.n) {
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.m) {
+                    store_out(p, m, n, acc[i][j][r]);
+                }
+            }
+        }
+    }
+}
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+inline int kn_splits(const NnopsGemmQ41Args& g)
+{
+    // enough blocks to cover the CUs several times, at least 16 k rows per split
+    const int64_t nblk = ((g.n + 31) / 32 + 63) / 64;
+    int64_t s = (1024 + nblk - 1) / nblk;
+    s = std::min<int64_t>(s, std::max<int64_t>(1, g.k / 16));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(s, 256));
+}
+
+inline bool use_gemv(const NnopsGemmQ41Args& g)
+{
+    return g.m <= 2 || !g.a_f16;
+}
+
+}  // namespace
+}  // namespace nnops_amd
+
+using namespace nnops_amd;
+
+extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
+{
+    if (g == nullptr || !use_gemv(*g) || g->trans_b) {
+        return 0;
+    }
+    return align_up((size_t)kn_splits(*g) * (size_t)g->m * (size_t)g->n * sizeof(float));
+}
+
+extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, size_t ws_bytes, void* stream)
+{
+    if (g == nullptr || g->m < 0 || g->n < 0 || g->k < 0) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    if (g->m == 0 || g->n == 0) {
+        return NNOPS_OK;
+    }
+    if (g->a == nullptr || g->b == nullptr || g->c == nullptr) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    if (g->out_kind != NNOPS_OUT_F32 && g->out_kind != NNOPS_OUT_F16) {
+        return NNOPS_UNSUPPORTED;
+    }
+    if (g->m > INT32_MAX || g->n > INT32_MAX || g->k > INT32_MAX) {
+        return NNOPS_UNSUPPORTED;
+    }
+    const int64_t row_bytes = g->trans_b ? (g->k + 31) / 32 * 20 : (g->n + 31) / 32 * 20;
+    if (g->lda < g->k || g->ldc < g->n || g->ldb_bytes < row_bytes || (g->ldb_bytes & 3) ||
+        ((uintptr_t)g->b & 3)) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    const size_t need = nnops_hip_gemm_q4_1_workspace_size(g);
+    if (need > 0 && (workspace == nullptr || ws_bytes < need)) {
+        return NNOPS_NOT_INITIALIZED;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Q41Kern k{};
+    k.a = g->a;
+    k.b = g->b;
+    k.c = g->c;
+    k.m = (int)g->m;
+    k.n = (int)g->n;
+    k.k = (int)g->k;
+    k.lda = g->lda;
+    k.ldc = g->ldc;
+    k.ldb = g->ldb_bytes;
+    k.out_f16 = g->out_kind == NNOPS_OUT_F16;
+
+    if (use_gemv(*g)) {
+        // rows of A handled per pass: 2 (f16 pairs), 1 for f32 A
+        const int mt = g->a_f16 ? 2 : 1;
+        for (int m0 = 0; m0 < k.m; m0 += mt) {
+            Q41Kern kk = k;
+            kk.m = std::min(mt, k.m - m0);
+            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * (g->a_f16 ? 2 : 4);
+            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
+            if (g->trans_b) {
+                const unsigned blocks = (unsigned)((g->n + kNkWaves * kNkRowsPerWave - 1) / (kNkWaves * kNkRowsPerWave));
+                if (g->a_f16) {
+                    if (kk.m == 1) {
+                        hipLaunchKernelGGL((gemv_q4_1_nk<1, true>), dim3(blocks), dim3(256), 0, s, kk);
+                    } else {
+                        hipLaunchKernelGGL((gemv_q4_1_nk<2, true>), dim3(blocks), dim3(256), 0, s, kk);
+                    }
+                } else {
+                    hipLaunchKernelGGL((gemv_q4_1_nk<1, false>), dim3(blocks), dim3(256), 0, s, kk);
+                }
+            } else {
+                kk.splits = kn_splits(*g);
+                kk.partial = static_cast<float*>(workspace);
+                const unsigned bx = (unsigned)(((g->n + 31) / 32 + 63) / 64);
+                if (g->a_f16) {
+                    if (kk.m == 1) {
+                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                    } else {
+                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                    }
+                } else {
+                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                }
+                const int64_t total = (int64_t)kk.m * kk.n;
+                hipLaunchKernelGGL(reduce_q4_1, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
+            }
+        }
+    } else {
+        const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
+        if (g->trans_b) {
+            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, true>), dim3(tiles), dim3(256), 0, s, k);
+        } else {
+            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
+        }
+    }
+    return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+}
+
+extern "C" const char* nnops_hip_build_info(void)
+{
+    return "nnops_amd gfx950 (hand-written HIP: int8 MFMA GEMM/GEMV, Q4_1 GEMV/MFMA GEMM)";
+}

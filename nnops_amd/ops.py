@@ -1,0 +1,244 @@
+"""Python conveniences over the two C ABIs, for torch tensors on a HIP device.
+
+torch is used only for device memory and streams. Every compute call goes to
+libnnops_amd.so; the workspace is allocated here (by torch) only because the
+library itself never allocates.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+from . import _lib as L
+
+_TORCH_DT = None
+
+
+def _dt_code(t):
+    import torch
+    global _TORCH_DT
+    if _TORCH_DT is None:
+        _TORCH_DT = {torch.float32: L.DT_F32, torch.float16: L.DT_F16, torch.int8: L.DT_S8,
+                     torch.uint8: L.DT_U8, torch.int32: L.DT_S32}
+    return _TORCH_DT[t.dtype]
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x or None
+    return x.data_ptr()
+
+
+def tensor(t, *, dtype=None, shape=None, scale=1.0, zero_point=0, scale_data=None,
+           zero_point_data=None, granularity=None, pitch=None):
+    """An NnopsTensor over a torch tensor (device memory). The innermost dim
+    must be contiguous; the row pitch is taken from stride(-2) unless given.
+    ``dtype``/``shape`` override the torch view (q4_1: pass DT_Q4_1 and the
+    logical shape in values, the tensor being the uint8 block bytes).
+    ``scale_data``/``zero_point_data`` may be host (numpy) or device (torch)."""
+    x = L.Tensor()
+    shp = list(shape) if shape is not None else list(t.shape)
+    x.rank = len(shp)
+    for i, d in enumerate(shp):
+        x.dims[i] = int(d)
+    x.dtype = _dt_code(t) if dtype is None else dtype
+    x.data = t.data_ptr() if t is not None else None
+    if pitch is not None:
+        x.pitch = int(pitch)
+    elif t is not None and t.dim() >= 2:
+        assert t.stride(-1) == 1, "innermost dim must be contiguous"
+        x.pitch = t.stride(-2) * t.element_size()
+    x.scale = float(scale)
+    x.zero_point = int(zero_point)
+    keep = []
+    for name, arr in (("scale_data", scale_data), ("zero_point_data", zero_point_data)):
+        if arr is None:
+            continue
+        if hasattr(arr, "data_ptr"):
+            setattr(x, name, arr.data_ptr())
+        else:
+            import numpy as np
+            a = np.ascontiguousarray(arr, dtype=np.float32 if name == "scale_data" else np.int32)
+            keep.append(a)
+            setattr(x, name, a.ctypes.data)
+        x.num_scales = len(arr)
+    if granularity is not None:
+        x.granularity = granularity
+    elif scale_data is not None or zero_point_data is not None:
+        x.granularity = 1
+    x._keep = keep  # host tables must outlive the call
+    return x
+
+
+def _stream_ptr(stream):
+    if isinstance(stream, int):
+        return stream or None
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _workspace(nbytes, device):
+    import torch
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def _epilogue(ep, act=None, min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NONE,
+              quant_scales=None, quant_zero_points=None, quant_param_count=0):
+    ep.type = act or L.EP_NONE
+    ep.alpha, ep.beta = 0.0, 1.0
+    ep.min_clip, ep.max_clip = min_clip, max_clip
+    ep.quant = quant
+    ep.quant_scales = _ptr(quant_scales)
+    ep.quant_zero_points = _ptr(quant_zero_points)
+    ep.quant_param_count = quant_param_count
+
+
+class _Op:
+    def __init__(self, handle):
+        if not handle:
+            raise RuntimeError("nnops op creation failed")
+        self._h = handle
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            L.lib().nnops_op_destroy(h)
+            self._h = None
+
+    @staticmethod
+    def _arr(ts):
+        ts = list(ts)
+        arr = (L.Tensor * max(1, len(ts)))()
+        for i, t in enumerate(ts):
+            arr[i] = t
+        return arr, len(ts)
+
+    def output_desc(self, inputs):
+        arr, n = self._arr(inputs)
+        out = L.Tensor()
+        rc = L.lib().nnops_op_output_desc(self._h, arr, n, C.byref(out))
+        if rc != 0:
+            raise ValueError(f"output_desc failed: status {rc}")
+        return [out.dims[i] for i in range(out.rank)], out.dtype
+
+    def validate(self, inputs, outputs):
+        ai, ni = self._arr(inputs)
+        ao, no = self._arr(outputs)
+        return L.lib().nnops_op_validate(self._h, ai, ni, ao, no)
+
+    def workspace_size(self, inputs, outputs):
+        ai, ni = self._arr(inputs)
+        ao, no = self._arr(outputs)
+        return L.lib().nnops_op_workspace_size(self._h, ai, ni, ao, no)
+
+    def compute(self, outputs, inputs, *, stream=None, workspace=None, device="cuda"):
+        """Run compute(); allocates a workspace of workspace_size() bytes when
+        none is given. Returns the nnops Status code."""
+        ai, ni = self._arr(inputs)
+        ao, no = self._arr(outputs)
+        if workspace is None:
+            workspace = _workspace(L.lib().nnops_op_workspace_size(self._h, ai, ni, ao, no), device)
+        return L.lib().nnops_op_compute(self._h, ao, no, ai, ni, _stream_ptr(stream), _ptr(workspace))
+
+
+class MatMul(_Op):
+    def __init__(self, *, transpose_a=False, transpose_b=False, output_dtype=L.DT_S32, act=None,
+                 min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NONE, quant_scales=None,
+                 quant_zero_points=None, quant_param_count=0, residual_pre_activation=False,
+                 requant_round_even=False, float_epilogue=False, backend=L.BACKEND_HIP):
+        a = L.MatMulAttrs()
+        L.lib().nnops_matmul_attrs_init(C.byref(a))
+        a.transpose_a, a.transpose_b = int(transpose_a), int(transpose_b)
+        a.output_dtype = output_dtype
+        a.residual_pre_activation = int(residual_pre_activation)
+        a.requant_round_even = int(requant_round_even)
+        a.float_epilogue = int(float_epilogue)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, quant_scales, quant_zero_points,
+                  quant_param_count)
+        super().__init__(L.lib().nnops_matmul_create(C.byref(a), backend))
+
+
+class Linear(_Op):
+    def __init__(self, *, output_dtype=L.DT_F32, act=None, min_clip=-math.inf, max_clip=math.inf,
+                 add_to=False, residual_pre_activation=False, quant=L.EQ_NONE, quant_scales=None,
+                 quant_zero_points=None, quant_param_count=0, requant_round_even=False,
+                 float_epilogue=False, gated=False, backend=L.BACKEND_HIP):
+        a = L.LinearAttrs()
+        L.lib().nnops_linear_attrs_init(C.byref(a))
+        a.output_dtype = output_dtype
+        a.add_to = int(add_to)
+        a.residual_pre_activation = int(residual_pre_activation)
+        a.requant_round_even = int(requant_round_even)
+        a.float_epilogue = int(float_epilogue)
+        a.gated = int(gated)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, quant_scales, quant_zero_points,
+                  quant_param_count)
+        super().__init__(L.lib().nnops_linear_create(C.byref(a), backend))
+
+
+def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_S32,
+            s_a=1.0, zp_a=0, s_b=1.0, zp_b=0, s_out=1.0, zp_out=0, s_out_rows=None,
+            zp_out_rows=None, act=L.ACT_NONE, round_even=False, float_ep=False,
+            min_clip=-math.inf, max_clip=math.inf, add_to=False, residual_pre=False,
+            m=None, n=None, k=None, workspace=None, stream=None, check=True):
+    """Direct call of nnops_hip_gemm_i8 on torch device tensors. Scales/zero
+    points are python scalars or device tensors (per row / per column)."""
+    import torch
+    g = L.GemmI8Args()
+    M = m if m is not None else (a.shape[1] if trans_a else a.shape[0])
+    K = k if k is not None else (a.shape[0] if trans_a else a.shape[1])
+    N = n if n is not None else (b.shape[0] if trans_b else b.shape[1])
+    g.a, g.b, g.c, g.bias = a.data_ptr(), b.data_ptr(), c.data_ptr(), _ptr(bias)
+    g.m, g.n, g.k = M, N, K
+    g.lda, g.ldb, g.ldc = a.stride(0), b.stride(0), c.stride(0)
+    g.trans_a, g.trans_b, g.a_u8 = int(trans_a), int(trans_b), int(a.dtype == torch.uint8)
+
+    def split(v, isf):
+        if isinstance(v, torch.Tensor):
+            return v.data_ptr(), (1.0 if isf else 0)
+        return None, v
+    g.s_a, g.s_a_scalar = split(s_a, True)
+    g.zp_a, g.zp_a_scalar = split(zp_a, False)
+    g.s_b, g.s_b_scalar = split(s_b, True)
+    g.zp_b, g.zp_b_scalar = split(zp_b, False)
+    g.s_out_rows, g.zp_out_rows = _ptr(s_out_rows), _ptr(zp_out_rows)
+    g.s_out, g.zp_out = s_out, zp_out
+    g.out_kind, g.act, g.round_even = out_kind, act, int(round_even)
+    g.float_ep, g.min_clip, g.max_clip = int(float_ep), min_clip, max_clip
+    g.add_to, g.residual_pre = int(add_to), int(residual_pre)
+    lib = L.lib()
+    need = lib.nnops_hip_gemm_i8_workspace_size(C.byref(g))
+    if workspace is None:
+        workspace = _workspace(need, a.device)
+    rc = lib.nnops_hip_gemm_i8(C.byref(g), _ptr(workspace), need, _stream_ptr(stream))
+    if check and rc != 0:
+        raise RuntimeError(f"nnops_hip_gemm_i8 failed: status {rc}")
+    return rc
+
+
+def gemm_q4_1(a, b, c, *, n, trans_b=True, ldb_bytes=None, workspace=None, stream=None,
+              check=True):
+    """Direct call of nnops_hip_gemm_q4_1: ``a`` f16/f32 [M,K], ``b`` uint8 block
+    rows (2-D), ``c`` f32/f16 [M,N]."""
+    import torch
+    g = L.GemmQ41Args()
+    g.a, g.b, g.c = a.data_ptr(), b.data_ptr(), c.data_ptr()
+    g.m, g.n, g.k = a.shape[0], n, a.shape[1]
+    g.lda, g.ldc = a.stride(0), c.stride(0)
+    g.ldb_bytes = b.stride(0) if ldb_bytes is None else ldb_bytes
+    g.trans_b, g.a_f16 = int(trans_b), int(a.dtype == torch.float16)
+    g.out_kind = L.OUT_F16 if c.dtype == torch.float16 else L.OUT_F32
+    lib = L.lib()
+    need = lib.nnops_hip_gemm_q4_1_workspace_size(C.byref(g))
+    if workspace is None:
+        workspace = _workspace(need, a.device)
+    rc = lib.nnops_hip_gemm_q4_1(C.byref(g), _ptr(workspace), need, _stream_ptr(stream))
+    if check and rc != 0:
+        raise RuntimeError(f"nnops_hip_gemm_q4_1 failed: status {rc}")
+    return rc

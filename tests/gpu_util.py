@@ -1,0 +1,43 @@
+"""Helpers shared by the GPU parity tests."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+
+def dev(x, device="cuda"):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def pitched(x, pitch_elems, device="cuda"):
+    """Device copy of 2-D ``x`` inside a wider buffer (row pitch > width),
+    padding filled with a sentinel so a read past the row shows up."""
+    import torch
+    rows, cols = x.shape
+    buf = np.full((rows, pitch_elems), 0x5A if x.dtype.itemsize == 1 else 7, dtype=x.dtype)
+    buf[:, :cols] = x
+    t = torch.from_numpy(buf).to(device)
+    return t[:, :cols]
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def announce(msg):
+    """Name the case before a GPU step, flushed, so a fault can be traced."""
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def norm_err(got, want):
+    """max |got - want| / max(|want|, rms(want)), elementwise: a relative error
+    that stays meaningful at outputs that cancel to ~0 (the tolerance metric of
+    the Q4_1 routes)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rms = np.sqrt(np.mean(want * want)) if want.size else 1.0
+    den = np.maximum(np.abs(want), rms)
+    return float(np.max(np.abs(got - want) / den)) if want.size else 0.0

@@ -1,0 +1,163 @@
+"""The C ABI library without a GPU: it loads, exports every symbol the public
+headers declare, and the descriptor-only half of the operator contract
+(output descriptors, validate, workspace sizes, rejected calls) behaves like
+nnops'. No call here reaches a kernel launch."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import nnops_amd as na
+from nnops_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in ("nnops_amd.h", "nnops_amd_ops.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(nnops_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = na.lib()
+    names = declared_symbols()
+    assert len(names) >= 14
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_build_info():
+    assert b"gfx950" in na.lib().nnops_hip_build_info()
+
+
+def test_gemm_i8_rejects_before_any_launch():
+    lib = na.lib()
+    g = na.GemmI8Args()
+    assert lib.nnops_hip_gemm_i8(None, None, 0, None) == na.INVALID_ARGUMENT
+    g.m, g.n, g.k = 4, 4, 4
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT  # null data
+    g.a = g.b = g.c = 16  # never dereferenced: every rejection below happens first
+    g.lda, g.ldb, g.ldc = 4, 4, 4
+    g.out_kind = na.OUT_F32
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    g.out_kind = na.OUT_S32
+    g.float_ep = 1
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    g.float_ep = 0
+    g.lda = 3
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.lda = 4
+    g.k = 70000
+    g.lda = g.ldb = 70000
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    # a [K,N] B needs a staging workspace: missing -> not_initialized
+    g.k, g.lda, g.ldb = 4, 4, 4
+    g.trans_b = 0
+    assert lib.nnops_hip_gemm_i8_workspace_size(C.byref(g)) > 0
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.NOT_INITIALIZED
+    # empty problem: ok, nothing to do
+    g.m = 0
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.OK
+
+
+def test_gemm_q4_1_rejects_before_any_launch():
+    lib = na.lib()
+    g = na.GemmQ41Args()
+    g.m, g.n, g.k = 2, 64, 64
+    g.a = g.b = g.c = 16
+    g.lda, g.ldc = 64, 64
+    g.trans_b = 1
+    g.ldb_bytes = 40
+    g.out_kind = na.OUT_S8
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    g.out_kind = na.OUT_F32
+    g.ldb_bytes = 39  # shorter than one row of blocks
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.ldb_bytes = 42  # not a multiple of 4
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+
+
+def desc(shape, dtype):
+    t = na.Tensor()
+    t.rank = len(shape)
+    for i, d in enumerate(shape):
+        t.dims[i] = d
+    t.dtype = dtype
+    t.scale = 1.0
+    return t
+
+
+def test_matmul_output_desc_rules():
+    # int8 pair -> output_dtype (src/ops/matmul.cpp:49-58)
+    op = na.MatMul(output_dtype=na.DT_S8)
+    shape, dt = op.output_desc([desc([2, 3], na.DT_S8), desc([3, 5], na.DT_S8)])
+    assert shape == [2, 5] and dt == na.DT_S8
+    op = na.MatMul(transpose_b=True)
+    shape, dt = op.output_desc([desc([7, 9], na.DT_U8), desc([4, 9], na.DT_S8)])
+    assert shape == [7, 4] and dt == na.DT_S32
+    # batch broadcast
+    shape, _ = op.output_desc([desc([3, 1, 7, 9], na.DT_S8), desc([5, 4, 9], na.DT_S8)])
+    assert shape == [3, 5, 7, 4]
+    # fp x q4_1 follows A
+    op = na.MatMul(transpose_b=True)
+    shape, dt = op.output_desc([desc([1, 64], na.DT_F16), desc([10, 64], na.DT_Q4_1)])
+    assert shape == [1, 10] and dt == na.DT_F16
+
+
+def test_linear_output_desc_rules():
+    # int8: output_dtype when known, default f32 (src/ops/linear.cpp:29-47)
+    op = na.Linear()
+    shape, dt = op.output_desc([desc([2, 5, 8], na.DT_S8), desc([6, 8], na.DT_S8)])
+    assert shape == [2, 5, 6] and dt == na.DT_F32
+    op = na.Linear(output_dtype=na.DT_S8)
+    _, dt = op.output_desc([desc([4, 8], na.DT_S8), desc([6, 8], na.DT_S8)])
+    assert dt == na.DT_S8
+
+
+def test_validate_and_workspace():
+    op = na.MatMul(output_dtype=na.DT_S8)
+    ins = [desc([4, 8], na.DT_S8), desc([8, 6], na.DT_S8)]
+    outs = [desc([4, 6], na.DT_S8)]
+    assert op.validate(ins, outs) == na.OK
+    assert op.validate([desc([4, 8], na.DT_S8), desc([7, 6], na.DT_S8)], outs) == na.INVALID_ARGUMENT
+    assert op.validate(ins[:1], outs) == na.INVALID_ARGUMENT
+    assert op.validate([desc([8], na.DT_S8), ins[1]], outs) == na.INVALID_ARGUMENT
+    # honest, non-zero: staging for the QuantParams tables + B transpose
+    ws = op.workspace_size(ins, outs)
+    assert ws >= 8 * 6
+    op_t = na.MatMul(output_dtype=na.DT_S8, transpose_b=True)
+    ws_t = op_t.workspace_size([desc([4, 8], na.DT_S8), desc([6, 8], na.DT_S8)], outs)
+    assert 0 < ws_t < ws
+
+
+def test_compute_rejections_without_gpu():
+    ins = [desc([4, 8], na.DT_S8), desc([8, 6], na.DT_S8)]
+    ins[0].data = ins[1].data = 256
+    out = desc([4, 6], na.DT_S8)
+    out.data = 512
+    # backend with no kernels -> unsupported (dispatch.hpp:93-96 in nnops)
+    assert na.MatMul(output_dtype=na.DT_S8, backend=na.BACKEND_CPU).compute([out], ins, stream=0, workspace=0) == na.UNSUPPORTED
+    # wrong counts / empty view / K mismatch -> invalid_argument
+    op = na.MatMul(output_dtype=na.DT_S8)
+    assert op.compute([out], ins[:1], stream=0, workspace=0) == na.INVALID_ARGUMENT
+    bad = desc([9, 6], na.DT_S8)
+    bad.data = 256
+    assert op.compute([out], [ins[0], bad], stream=0, workspace=0) == na.INVALID_ARGUMENT
+    empty = desc([4, 8], na.DT_S8)
+    assert op.compute([out], [empty, ins[1]], stream=0, workspace=0) == na.INVALID_ARGUMENT
+    # output dtype disagreeing with output_dtype
+    o32 = desc([4, 6], na.DT_S32)
+    o32.data = 512
+    assert op.compute([o32], ins, stream=0, workspace=0) == na.INVALID_ARGUMENT
+    # gated Linear has no quantized route
+    assert na.Linear(gated=True).validate([desc([4, 8], na.DT_S8), desc([6, 8], na.DT_S8)],
+                                          [desc([4, 6], na.DT_F32)]) == na.UNSUPPORTED

@@ -1,0 +1,87 @@
+"""Q4_1-weight GEMV / GEMM on the GPU through the C ABI (nnops_hip_gemm_q4_1)
+against the CPU f32 dequant GEMM oracle (float64 accumulation).
+
+Tolerance (BASELINE: max relative error <= 2e-3 vs the CPU f32 dequant GEMM),
+as a normalized relative error: max_i |g_i - w_i| / max(|w_i|, rms(w)), so
+outputs that cancel to ~0 do not make the ratio meaningless."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import datagen as dg
+import nnops_amd as na
+from gpu_util import dev, host, announce, norm_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def run_gpu(a, blk, n, *, trans_b, out_f16=False):
+    import torch
+    M = a.shape[0]
+    c = torch.zeros((M, n), dtype=torch.float16 if out_f16 else torch.float32, device="cuda")
+    na.gemm_q4_1(dev(a), dev(blk), c, n=n, trans_b=trans_b)
+    torch.cuda.synchronize()
+    return host(c).astype(np.float32)
+
+
+CASES = [
+    # (M, K, N): GEMV (M <= 2) and MFMA routes; ragged K / N
+    (1, 4096, 1024), (2, 4096, 512), (1, 96, 40), (1, 1000, 77), (2, 8200, 64),
+    (3, 256, 130), (16, 4096, 256), (64, 512, 300), (130, 1000, 200),
+]
+
+
+@pytest.mark.parametrize("M,K,N", CASES)
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_q4_1_f16_a_f32_out(M, K, N, trans_b):
+    announce(f"q4_1 f16 {M}x{K}x{N} trans_b={trans_b}")
+    seed = M * 13 + K + N + int(trans_b)
+    a = dg.normal(seed, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(seed + 1, N, K) if trans_b else dg.q4_1_blocks(seed + 2, K, N)
+    got = run_gpu(a, blk, N, trans_b=trans_b)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
+    err = norm_err(got, want)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_q4_1_f32_a(trans_b):
+    announce(f"q4_1 f32 A trans_b={trans_b}")
+    M, K, N = 5, 640, 96
+    a = dg.normal(91, (M, K))
+    blk = dg.q4_1_blocks(92, N, K) if trans_b else dg.q4_1_blocks(93, K, N)
+    got = run_gpu(a, blk, N, trans_b=trans_b)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
+    assert norm_err(got, want) <= 1e-4
+
+
+@pytest.mark.parametrize("M", [1, 40])
+def test_q4_1_f16_out_nnops_semantics(M):
+    """f16 A -> f16 C (nnops' dtype rule): the oracle rounds each decoded
+    weight to f16 and the output once (test_matmul_q4_1.cpp:203-215)."""
+    announce(f"q4_1 f16 out M={M}")
+    K, N = 512, 128
+    a = dg.normal(95, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(96, N, K)
+    got = run_gpu(a, blk, N, trans_b=True, out_f16=True)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=True, w_round_f16=True, c_f16=True).astype(np.float32)
+    assert norm_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 512])
+def test_config4_full(M):
+    """BASELINE config 4 at full size: K=4096, N=14336, f16 A ~ N(0,1), f32 out;
+    M=1 fully checked, M=512 on sampled rows."""
+    announce(f"config4 M={M}")
+    K, N = 4096, 14336
+    a = dg.normal(100 + M, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(101, N, K)
+    got = run_gpu(a, blk, N, trans_b=True)
+    rows = (0, M) if M <= 4 else (200, 216)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=True, rows=rows)
+    err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
+    assert err <= TOL, err

@@ -1,0 +1,236 @@
+"""The CPU oracle pinned against nnops: known answers of the reference's own
+tests, golden vectors written by the reference's compiled oracles
+(tests/golden/golden.json), the compiled reference itself where it is present
+(oracle/_ref), and mathematics (brute force, IEEE conversions, series)."""
+from __future__ import annotations
+
+import base64
+import hashlib
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import datagen as dg
+from golden.gen_golden import build_i8_case, run_ref_i8, gelu_grid, ODT, OUTK
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "golden.json")))
+
+
+def b64(s, dt):
+    return np.frombuffer(base64.b64decode(s), dtype=dt)
+
+
+def oracle_i8_case(c, ops):
+    kw = dict(trans_b=c["trans_b"], bias=ops["bias"], out_kind=OUTK[c["out"]],
+              s_a=ops["s_a"], zp_a=ops["zp_a"], s_b=ops["s_b"], zp_b=ops["zp_b"],
+              s_out=c.get("s_out", 1.0), zp_out=c.get("zp_out", 0),
+              act=oracle.ACT_RELU if c.get("relu") else oracle.ACT_NONE)
+    return oracle.gemm_i8(ops["a"], ops["b"], **kw)
+
+
+# --- known answers: tests/test_matmul_int8.cpp -------------------------------
+
+def test_known_basic_s32():  # test_matmul_int8.cpp:106-138
+    a = np.array([[1, -2, 3], [-4, 5, -6]], np.int8)
+    b = np.array([[1, 2], [3, 4], [5, 6]], np.int8)
+    assert oracle.gemm_i8(a, b).tolist() == [[10, 12], [-19, -24]]
+
+
+def test_known_zero_points():  # :140-179
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.int8)
+    w = np.array([[7, 8, 9], [10, 11, 12]], np.int8)
+    out = oracle.gemm_i8(a, w, trans_b=True, zp_a=np.array([1, 2]), zp_b=np.array([3, 4]))
+    assert out.tolist() == [[17, 23], [47, 65]]
+
+
+def test_known_u8_zero_points():  # :181-219
+    a = np.array([[130, 128, 3], [200, 255, 0]], np.uint8)
+    b = np.array([[1, -4], [2, 5], [3, -6]], np.int8)
+    out = oracle.gemm_i8(a, b, zp_a=np.array([128, 100]), zp_b=3)
+    assert out.tolist() == [[-4, 1111], [-355, 510]]
+
+
+def test_known_requant_and_saturation():  # :221-287, :528-559
+    a = np.array([[4, 6]], np.int8)
+    w = np.ones((2, 2), np.int8)
+    out = oracle.gemm_i8(a, w, trans_b=True, out_kind=oracle.OUT_S8, s_out=2.0)
+    assert out.tolist() == [[5, 5]]
+    a = np.array([[100, 100]], np.int8)
+    w = np.full((2, 2), 100, np.int8)
+    assert oracle.gemm_i8(a, w, trans_b=True, out_kind=oracle.OUT_S8).tolist() == [[127, 127]]
+    a = np.array([[100, 100], [1, -2]], np.int8)
+    out = oracle.gemm_i8(a, w, trans_b=True, out_kind=oracle.OUT_U8, zp_out=10)
+    assert out.tolist() == [[255, 255], [0, 0]]
+
+
+def test_known_bias_s32():  # :457-488
+    a = np.array([[1, -2, 3], [-4, 5, -6]], np.int8)
+    b = np.array([[1, 2], [3, 4], [5, 6]], np.int8)
+    out = oracle.gemm_i8(a, b, bias=np.array([-5, 7], np.int32))
+    assert out.tolist() == [[5, 19], [-24, -17]]
+
+
+# --- mathematics --------------------------------------------------------------
+
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("u8", [False, True])
+def test_int_accumulate_brute_force(trans_b, u8):
+    rng = np.random.default_rng(7)
+    M, K, N = 19, 133, 27
+    a = rng.integers(0, 256, (M, K)).astype(np.uint8) if u8 else rng.integers(-128, 128, (M, K)).astype(np.int8)
+    b = rng.integers(-128, 128, (N, K) if trans_b else (K, N)).astype(np.int8)
+    zpa = rng.integers(-20, 20, M).astype(np.int32)
+    zpb = rng.integers(-5, 5, N).astype(np.int32)
+    bias = rng.integers(-1000, 1000, N).astype(np.int32)
+    got = oracle.gemm_i8(a, b, trans_b=trans_b, zp_a=zpa, zp_b=zpb, bias=bias)
+    bb = b.T if trans_b else b
+    want = (a.astype(np.int64) - zpa[:, None]) @ (bb.astype(np.int64) - zpb[None, :]) + bias
+    np.testing.assert_array_equal(got, want)
+
+
+def test_requant_round_half_away_vs_even():
+    # x = acc * req lands exactly on .5 for these; half-away and half-even differ
+    for acc, away, even in ((5, 3, 2), (-5, -3, -2), (7, 4, 4), (-7, -4, -4), (1, 1, 0)):
+        assert oracle.lib().orc_requant(acc, 0.5, 0, 0, 0) == away
+        assert oracle.lib().orc_requant(acc, 0.5, 0, 0, 1) == even
+
+
+def test_f16_conversion_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    f = np.array([oracle.lib().orc_f16_to_f32(int(h)) for h in bits[::7]], np.float32)
+    want = bits[::7].view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(np.isnan(f), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(f[ok].view(np.uint32), want[ok].view(np.uint32))
+    # narrowing: round-to-nearest-even vs numpy on a dense sweep incl. ties/subnormals
+    xs = np.concatenate([
+        dg.uniform(1, (3000,), -70000, 70000), dg.uniform(2, (3000,), -1e-4, 1e-4),
+        (np.arange(2048, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24),
+        np.float32([0.0, -0.0, np.inf, -np.inf, 65504, 65519.99, 65520, 6.1e-5, 5.96e-8, 2.98e-8])])
+    got = np.array([oracle.lib().orc_f32_to_f16(float(x)) for x in xs], np.uint16)
+    with np.errstate(over="ignore"):
+        want16 = xs.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, want16)
+
+
+def test_tanh_and_gelu_against_math():
+    x = np.linspace(-12, 12, 4801, dtype=np.float32)
+    t = np.array([oracle.lib().orc_tanhf(float(v)) for v in x])
+    assert np.max(np.abs(t - np.tanh(x.astype(np.float64)))) < 3e-7
+    g = np.array([oracle.lib().orc_gelu_tanh(float(v)) for v in x])
+    xd = x.astype(np.float64)
+    gd = 0.5 * xd * (1 + np.tanh(math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    assert np.max(np.abs(g - gd) / np.maximum(1.0, np.abs(gd))) < 1e-6
+
+
+def test_q4_1_decode_closed_form():
+    blk = dg.q4_1_blocks(5, 1, 64).ravel()
+    vals = oracle.q4_1_decode(blk, 64)
+    for b in range(2):
+        raw = blk[b * 20:(b + 1) * 20]
+        d = np.float32(raw[0:2].view(np.float16)[0])
+        m = np.float32(raw[2:4].view(np.float16)[0])
+        q = np.concatenate([raw[4:] & 15, raw[4:] >> 4]).astype(np.float32)
+        np.testing.assert_array_equal(vals[b * 32:(b + 1) * 32], d * q + m)
+
+
+def test_q4_1_single_block_known():  # tests/test_q4_1.cpp:186-201
+    q = np.arange(32) & 15
+    blk = np.zeros(20, np.uint8)
+    blk[0:2] = np.array([0.25], np.float16).view(np.uint8)
+    blk[2:4] = np.array([-1.5], np.float16).view(np.uint8)
+    blk[4:] = (q[:16] | (q[16:] << 4)).astype(np.uint8)
+    np.testing.assert_array_equal(oracle.q4_1_decode(blk, 32), 0.25 * q.astype(np.float32) - 1.5)
+
+
+def test_q4_1_gemm_oracle_brute_force():
+    M, K, N = 3, 96, 40
+    a = dg.normal(11, (M, K)).astype(np.float16)
+    for trans_b in (True, False):
+        blk = dg.q4_1_blocks(12, N, K) if trans_b else dg.q4_1_blocks(13, K, N)
+        got = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
+        if trans_b:
+            w = np.stack([oracle.q4_1_decode(blk[n], K) for n in range(N)])  # [N,K]
+        else:
+            w = np.stack([oracle.q4_1_decode(blk[k], N) for k in range(K)]).T
+        want = a.astype(np.float64) @ w.astype(np.float64).T
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+# --- golden vectors from the reference's compiled oracles ----------------------
+
+@pytest.mark.parametrize("entry", GOLD["i8"], ids=[e["case"]["name"] for e in GOLD["i8"]])
+def test_oracle_matches_golden_i8(entry):
+    c = entry["case"]
+    ops = build_i8_case(c)
+    out = oracle_i8_case(c, ops)
+    raw = np.ascontiguousarray(out).tobytes()
+    assert out.ravel()[:64].tolist() == entry["out"]["head"]
+    assert hashlib.sha256(raw).hexdigest() == entry["out"]["sha256"]
+
+
+@pytest.mark.parametrize("entry", GOLD["q4_1_quantize"], ids=lambda e: str(e["count"]))
+def test_oracle_q4_1_quantize_golden(entry):
+    x = dg.uniform(entry["seed"], (entry["count"],), -1.0, 1.0)
+    blk = oracle.q4_1_quantize(x)
+    assert hashlib.sha256(blk.tobytes()).hexdigest() == entry["out"]["sha256"]
+
+
+@pytest.mark.parametrize("entry", GOLD["q4_1_decode"], ids=lambda e: str(e["seed"]))
+def test_oracle_q4_1_decode_golden(entry):
+    blk = dg.q4_1_blocks(entry["seed"], entry["rows"], entry["cols"])
+    out = np.concatenate([oracle.q4_1_decode(blk[r], entry["cols"]) for r in range(entry["rows"])])
+    assert hashlib.sha256(out.tobytes()).hexdigest() == entry["out"]["sha256"]
+
+
+def test_oracle_requant_golden():
+    g = GOLD["requant"]
+    acc, req = b64(g["acc_b64"], np.int32), b64(g["req_b64"], np.float32)
+    s8 = np.array([oracle.lib().orc_requant(int(a), float(r), g["s8_zp"], 0, 0) for a, r in zip(acc, req)])
+    u8 = np.array([oracle.lib().orc_requant(int(a), float(r), g["u8_zp"], 1, 0) for a, r in zip(acc, req)])
+    np.testing.assert_array_equal(s8, b64(g["s8_b64"], np.int32))
+    np.testing.assert_array_equal(u8, b64(g["u8_b64"], np.int32))
+
+
+def test_oracle_gelu_close_to_reference_gelu():
+    """The GELU of the float epilogue uses its own tanh; against nnops'
+    std::tanh-based GELU it agrees to a few f32 ulps (absolute 2e-6 at |y|<=1)."""
+    x = b64(GOLD["gelu"]["x_b64"], np.float32)
+    y = b64(GOLD["gelu"]["y_b64"], np.float32)
+    g = np.array([oracle.lib().orc_gelu_tanh(float(v)) for v in x], np.float32)
+    err = np.abs(g.astype(np.float64) - y) / np.maximum(1.0, np.abs(y))
+    assert err.max() < 2e-6
+
+
+# --- the compiled reference itself (where this container has it) --------------
+
+ref_only = pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
+
+
+@ref_only
+@pytest.mark.parametrize("seed", range(6))
+def test_oracle_matches_reference_random(seed):
+    rng = np.random.default_rng(seed)
+    M, K, N = (int(v) for v in rng.integers(1, 70, 3))
+    tb = bool(seed & 1)
+    c = dict(m=M, k=K, n=N, trans_b=tb, out=["s32", "s8", "u8"][seed % 3], a_u8=bool(seed & 2),
+             seed_a=1000 + seed, seed_b=2000 + seed, seed_sa=3000 + seed, sa_range=(0.01, 0.1),
+             seed_sb=4000 + seed, sb_range=(0.001, 0.02), seed_zpa=5000 + seed,
+             zpa_range=(-9, 9), seed_zpb=6000 + seed, zpb_range=(-4, 4),
+             seed_bias=7000 + seed, bias_amp=3000, relu=bool(seed & 4), s_out=0.37, zp_out=5)
+    ops = build_i8_case(c)
+    np.testing.assert_array_equal(oracle_i8_case(c, ops), run_ref_i8(c, ops))
+
+
+@ref_only
+def test_oracle_q4_1_quantize_matches_reference_partial_blocks():
+    for count in (1, 7, 31, 33, 63, 71):
+        x = dg.uniform(88 + count, (count,), -2, 2)
+        nb = (count + 31) // 32
+        want = np.zeros(nb * 20, np.uint8)
+        oracle.ref_lib().ref_q4_1_quantize(x.ctypes.data, count, want.ctypes.data)
+        np.testing.assert_array_equal(oracle.q4_1_quantize(x), want)
