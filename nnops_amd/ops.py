@@ -28,7 +28,9 @@ def _ptr(x):
         return None
     if isinstance(x, int):
         return x or None
-    return x.data_ptr()
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    return x.ctypes.data  # host (numpy) table: the caller keeps it alive
 
 
 def tensor(t, *, dtype=None, shape=None, scale=1.0, zero_point=0, scale_data=None,
@@ -68,7 +70,7 @@ def tensor(t, *, dtype=None, shape=None, scale=1.0, zero_point=0, scale_data=Non
         x.granularity = granularity
     elif scale_data is not None or zero_point_data is not None:
         x.granularity = 1
-    x._keep = keep  # host tables must outlive the call
+    x._keep = keep + [t]  # the buffers (device tensor, host tables) must outlive the call
     return x
 
 
@@ -97,6 +99,19 @@ def _epilogue(ep, act=None, min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NO
     ep.quant_scales = _ptr(quant_scales)
     ep.quant_zero_points = _ptr(quant_zero_points)
     ep.quant_param_count = quant_param_count
+
+
+def _host_tables(scales, zps):
+    """Epilogue tables: device tensors pass through; host arrays are made
+    contiguous f32/int32 and kept alive by the op (the op stores the pointer)."""
+    import numpy as np
+    out = []
+    for arr, dt in ((scales, np.float32), (zps, np.int32)):
+        if arr is None or hasattr(arr, "data_ptr"):
+            out.append(arr)
+        else:
+            out.append(np.ascontiguousarray(arr, dtype=dt))
+    return out
 
 
 class _Op:
@@ -159,8 +174,8 @@ class MatMul(_Op):
         a.residual_pre_activation = int(residual_pre_activation)
         a.requant_round_even = int(requant_round_even)
         a.float_epilogue = int(float_epilogue)
-        _epilogue(a.epilogue, act, min_clip, max_clip, quant, quant_scales, quant_zero_points,
-                  quant_param_count)
+        self._keep = _host_tables(quant_scales, quant_zero_points)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count)
         super().__init__(L.lib().nnops_matmul_create(C.byref(a), backend))
 
 
@@ -177,8 +192,8 @@ class Linear(_Op):
         a.requant_round_even = int(requant_round_even)
         a.float_epilogue = int(float_epilogue)
         a.gated = int(gated)
-        _epilogue(a.epilogue, act, min_clip, max_clip, quant, quant_scales, quant_zero_points,
-                  quant_param_count)
+        self._keep = _host_tables(quant_scales, quant_zero_points)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count)
         super().__init__(L.lib().nnops_linear_create(C.byref(a), backend))
 
 
