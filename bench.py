@@ -106,7 +106,7 @@ def run_cfg2(args, torch, dg, na, stream):
                    "weight_layout": "[N,K]"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": tops / PEAK_INT8_TOPS, "traffic": None,
-                     "kernel": "gemm_i8_mfma<256,256,2,2>", "algorithmic_ops_per_launch": ops},
+                     "kernel": "gemm_i8_ring<256,256,2,4,4,EPI_S8>", "algorithmic_ops_per_launch": ops},
         "dtype": "int8 (s32 accumulate)",
     }
 

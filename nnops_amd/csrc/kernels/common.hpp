@@ -160,49 +160,55 @@ __device__ __forceinline__ float apply_act(const EpiParams& p, float x)
     return x;
 }
 
-// The whole output pass for one element: raw int32 accumulate in, destination
-// written. `c` is the row base of the destination, `n` the column.
-__device__ __forceinline__ void epi_store(const EpiParams& p, const EpiRow& r, const EpiCol& col,
-                                          int32_t raw, void* crow, int n)
+// The output pass for one element: raw int32 accumulate in, the value to store
+// out (int32 for s32, the s8/u8 code otherwise). `old` is the destination's
+// current value, read only when add_to.
+__device__ __forceinline__ int32_t epi_value(const EpiParams& p, const EpiRow& r, const EpiCol& col,
+                                             int32_t raw, int32_t old)
 {
-    int32_t v = epi_compensate(p, r, col, raw);
+    int32_t v = epi_compensate(p, r, col, raw) + col.bias;
     if (p.out_kind == NNOPS_OUT_S32) {
-        v += col.bias;
-        if (p.act == NNOPS_ACT_RELU) {
-            v = v < 0 ? 0 : v;
-        }
-        static_cast<int32_t*>(crow)[n] = v;
-        return;
+        return (p.act == NNOPS_ACT_RELU && v < 0) ? 0 : v;
     }
     const bool u8 = p.out_kind == NNOPS_OUT_U8;
-    int32_t q;
     if (!p.float_ep) {
-        v += col.bias;
         if (p.act == NNOPS_ACT_RELU) {
             v = v < 0 ? 0 : v;
         }
         const float req = __fmul_rn(r.row_k, col.s_b);
-        q = requant_clamped(__fmul_rn((float)v, req), r.zp_out, u8, p.round_even);
-    } else {
-        v += col.bias;
-        float f = __fmul_rn((float)v, __fmul_rn(r.s_a, col.s_b));
-        float res = 0.0f;
-        if (p.add_to) {
-            const int32_t old = u8 ? (int32_t) static_cast<uint8_t*>(crow)[n]
-                                   : (int32_t) static_cast<int8_t*>(crow)[n];
-            res = __fmul_rn((float)(old - r.zp_out), r.s_out);
-            if (p.residual_pre) {
-                f = __fadd_rn(f, res);
-            }
-        }
-        f = apply_act(p, f);
-        if (p.add_to && !p.residual_pre) {
+        return requant_clamped(__fmul_rn((float)v, req), r.zp_out, u8, p.round_even);
+    }
+    float f = __fmul_rn((float)v, __fmul_rn(r.s_a, col.s_b));
+    float res = 0.0f;
+    if (p.add_to) {
+        res = __fmul_rn((float)(old - r.zp_out), r.s_out);
+        if (p.residual_pre) {
             f = __fadd_rn(f, res);
         }
-        q = requant_clamped(__fdiv_rn(f, r.s_out), r.zp_out, u8, p.round_even);
     }
-    if (u8) {
-        static_cast<uint8_t*>(crow)[n] = (uint8_t)q;
+    f = apply_act(p, f);
+    if (p.add_to && !p.residual_pre) {
+        f = __fadd_rn(f, res);
+    }
+    return requant_clamped(__fdiv_rn(f, r.s_out), r.zp_out, u8, p.round_even);
+}
+
+__device__ __forceinline__ int32_t epi_load_old(const EpiParams& p, const void* crow, int n)
+{
+    if (!p.add_to) {
+        return 0;
+    }
+    return p.out_kind == NNOPS_OUT_U8 ? (int32_t) static_cast<const uint8_t*>(crow)[n]
+                                      : (int32_t) static_cast<const int8_t*>(crow)[n];
+}
+
+// Single-element store of the output pass.
+__device__ __forceinline__ void epi_store(const EpiParams& p, const EpiRow& r, const EpiCol& col,
+                                          int32_t raw, void* crow, int n)
+{
+    const int32_t q = epi_value(p, r, col, raw, epi_load_old(p, crow, n));
+    if (p.out_kind == NNOPS_OUT_S32) {
+        static_cast<int32_t*>(crow)[n] = q;
     } else {
         static_cast<int8_t*>(crow)[n] = (int8_t)q;
     }

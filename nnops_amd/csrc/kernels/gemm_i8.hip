@@ -127,8 +127,285 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     tn = in_group / gsize;
 }
 
-template <int BM, int BN, int WM, int WN, bool ALIGNED>
-__global__ __launch_bounds__(WM * WN * 64, 1) void gemm_i8_mfma(GemmI8Kern p)
+// Stage loader: CA/CB 16-byte chunks per thread per 64-byte k stage. FULLK:
+// K is a multiple of 64 and every row is 16-byte aligned, so no load needs a
+// bound; otherwise chunks past K read as zero (ALIGNED or per byte).
+template <int C, bool FULLK, bool ALIGNED, bool FLIP>
+__device__ __forceinline__ void load_chunks(v4i (&r)[C], const int8_t* const (&src)[C],
+                                            const int (&kc)[C], int k0, int K, uint32_t x)
+{
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        if constexpr (FULLK) {
+            r[i] = *reinterpret_cast<const v4i*>(src[i] + k0 + kc[i]);
+            if constexpr (FLIP) {
+                r[i] = flip_u8(r[i], x, true);
+            }
+        } else if constexpr (FLIP) {
+            r[i] = load16_a<ALIGNED>(src[i], k0 + kc[i], K, x);
+        } else {
+            r[i] = load16<ALIGNED>(src[i], k0 + kc[i], K);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Output pass shared by the MFMA kernels. One 32-row slab of the wave tile at a
+// time goes through LDS (32x32 accumulator layout: lane holds column lane & 31,
+// rows 8*(r/4) + 4*(lane/32) + (r%4)); then every lane owns 4 consecutive
+// columns and walks the slab's rows, so the destination is written with packed
+// 4-byte (s8/u8) or 16-byte (s32) stores, 4 rows in flight per lane.
+//   EPI_S8   integer requant with row-uniform scales (no zero points, no
+//            per-row tables): req = (s_a / s_out) * s_b[n] hoisted per column;
+//   EPI_S32  raw accumulate + bias (+ Relu), no zero points;
+//   EPI_GENERIC  everything else (compensation, per-row tables, float epilogue).
+// The fast modes evaluate exactly the float operations epi_value does.
+// ---------------------------------------------------------------------------
+enum { EPI_GENERIC = 0, EPI_S8 = 1, EPI_S32 = 2 };
+
+template <int FM, int FN, int TN, int EPI, int PROBE = 0>
+__device__ __forceinline__ void output_pass(const GemmI8Kern& p, v16i (&acc)[FM][FN], int32_t* slab,
+                                            int row0, int col0, int lane)
+{
+    constexpr int kEpiPitch = TN + 4;
+    constexpr int kColGroups = TN / 4;                   // 4-column groups per slab row
+    constexpr int kRowStep = 64 / kColGroups;            // rows covered per pass of the wave
+    constexpr int kRowsPerLane = 32 / kRowStep;
+    static_assert(kColGroups * kRowStep == 64 && kRowsPerLane * kRowStep == 32, "slab walk");
+    const EpiParams& ep = p.ep;
+    const int cg = lane % kColGroups;
+    const int rsub = lane / kColGroups;
+    const int nb = col0 + cg * 4;                        // first of this lane's 4 columns
+    EpiCol cols[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        cols[e] = epi_col(ep, min(nb + e, p.n - 1));
+    }
+    float req[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI == EPI_S8) {
+        const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            req[e] = __fmul_rn(row_k, cols[e].s_b);
+        }
+    }
+    const bool relu = ep.act == NNOPS_ACT_RELU;
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    const bool s32 = ep.out_kind == NNOPS_OUT_S32;
+    const bool packed = (nb + 3 < p.n) && (((uintptr_t)p.c & 15) == 0) &&
+                        (s32 ? (p.ldc_bytes % 16 == 0) : (p.ldc_bytes % 4 == 0));
+    // Fast modes (host-checked: N % 4 == 0, 16-byte-aligned C, pitch multiple
+    // of the packed store, half-away rounding): branch-free per element.
+    const int32_t relu_floor = relu ? 0 : INT32_MIN;
+    const float zpf = (float)ep.zp_out;
+    const float lo = __fsub_rn(u8 ? 0.0f : -128.0f, zpf);
+    const float hi = __fsub_rn(u8 ? 255.0f : 127.0f, zpf);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                slab[row * kEpiPitch + j * 32 + (lane & 31)] = acc[i][j][r];
+            }
+        }
+        __syncthreads();
+        const int mbase = row0 + i * 32 + rsub;
+        char* cbase = static_cast<char*>(p.c) + (int64_t)mbase * p.ldc_bytes +
+                      (int64_t)nb * (s32 ? 4 : 1);
+        const int64_t cstep = (int64_t)kRowStep * p.ldc_bytes;
+#pragma unroll 4
+        for (int t = 0; t < kRowsPerLane; ++t) {
+            const int rr = rsub + t * kRowStep;
+            const int m = mbase + t * kRowStep;
+            char* cptr = cbase + t * cstep;
+            if (m >= p.m || nb >= p.n) {
+                continue;
+            }
+            const v4i raw = *reinterpret_cast<const v4i*>(&slab[rr * kEpiPitch + cg * 4]);
+            if constexpr (EPI == EPI_S8) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int32_t v = max(raw[e] + cols[e].bias, relu_floor);
+                    float x = __fmul_rn((float)v, req[e]);
+                    x = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
+                    const int32_t q = (int32_t)round_half_away(x) + ep.zp_out;
+                    w |= ((uint32_t)q & 0xffu) << (8 * e);
+                }
+                if constexpr (PROBE == 3) {  // timing probe: no stores
+                    if (w == 0x12345678u) {
+                        *reinterpret_cast<uint32_t*>(cptr) = w;
+                    }
+                } else if constexpr (PROBE == 4) {  // timing probe: stores, no math
+                    *reinterpret_cast<uint32_t*>(cptr) = (uint32_t)raw[0];
+                } else {
+                    *reinterpret_cast<uint32_t*>(cptr) = w;
+                }
+            } else if constexpr (EPI == EPI_S32) {
+                v4i q;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    q[e] = max(raw[e] + cols[e].bias, relu_floor);
+                }
+                *reinterpret_cast<v4i*>(cptr) = q;
+            } else {
+                char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+                const EpiRow row = epi_row(ep, m);
+                if (packed && s32) {
+                    int32_t q[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        q[e] = epi_value(ep, row, cols[e], raw[e], 0);
+                    }
+                    *reinterpret_cast<v4i*>(crow + (int64_t)nb * 4) = v4i{q[0], q[1], q[2], q[3]};
+                } else if (packed) {
+                    uint32_t old = 0;
+                    if (ep.add_to) {
+                        old = *reinterpret_cast<const uint32_t*>(crow + nb);
+                    }
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t ob = (old >> (8 * e)) & 0xffu;
+                        const int32_t o = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
+                        w |= ((uint32_t)epi_value(ep, row, cols[e], raw[e], o) & 0xffu) << (8 * e);
+                    }
+                    *reinterpret_cast<uint32_t*>(crow + nb) = w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (nb + e < p.n) {
+                            epi_store(ep, row, cols[e], raw[e], crow, nb + e);
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Register output pass (EPI_S8 / EPI_S32): the element math runs in the MFMA
+// accumulator layout (lane = one column, 4 consecutive rows per register
+// group), then each 4x4 block is transposed across the lane quad with DPP so a
+// lane holds 4 consecutive columns of one row and writes them with one packed
+// store. No LDS round trip and no block barrier.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int quad_bcast(int v, int k)
+{
+    // quad_perm(k, k, k, k): every lane of the quad reads lane k
+    switch (k) {
+    case 0: return __builtin_amdgcn_mov_dpp(v, 0x00, 0xf, 0xf, true);
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0x55, 0xf, 0xf, true);
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0xaa, 0xf, 0xf, true);
+    default: return __builtin_amdgcn_mov_dpp(v, 0xff, 0xf, 0xf, true);
+    }
+}
+
+// Lane qi holds bytes (row 0..3) of column qi; returns (column 0..3) of row qi.
+__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t w, int qi)
+{
+    const uint32_t w0 = (uint32_t)quad_bcast((int)w, 0);
+    const uint32_t w1 = (uint32_t)quad_bcast((int)w, 1);
+    const uint32_t w2 = (uint32_t)quad_bcast((int)w, 2);
+    const uint32_t w3 = (uint32_t)quad_bcast((int)w, 3);
+    // v_perm_b32(hi, lo, sel): selector byte b picks lo.byte[b] (b < 4) or hi.byte[b-4]
+    const uint32_t sel = (uint32_t)qi | ((uint32_t)(4 + qi) << 8) | 0x0c0c0000u;
+    const uint32_t t01 = __builtin_amdgcn_perm(w1, w0, sel);
+    const uint32_t t23 = __builtin_amdgcn_perm(w3, w2, sel);
+    return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+}
+
+// 4x4 dword transpose across the quad: v[r] = (row r, column qi) in,
+// v[c] = (row qi, column c) out. Two exchange stages (lane xor 1, xor 2).
+__device__ __forceinline__ void quad_transpose_dwords(int32_t (&v)[4], int qi)
+{
+    const bool odd = qi & 1;
+#pragma unroll
+    for (int a = 0; a < 4; a += 2) {
+        const int send = odd ? v[a] : v[a + 1];
+        const int recv = __builtin_amdgcn_mov_dpp(send, 0xb1, 0xf, 0xf, true);  // quad_perm(1,0,3,2)
+        if (odd) {
+            v[a] = recv;
+        } else {
+            v[a + 1] = recv;
+        }
+    }
+    const bool hi = qi & 2;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int send = hi ? v[a] : v[a + 2];
+        const int recv = __builtin_amdgcn_mov_dpp(send, 0x4e, 0xf, 0xf, true);  // quad_perm(2,3,0,1)
+        if (hi) {
+            v[a] = recv;
+        } else {
+            v[a + 2] = recv;
+        }
+    }
+}
+
+template <int FM, int FN, int EPI>
+__device__ __forceinline__ void output_pass_regs(const GemmI8Kern& p, v16i (&acc)[FM][FN], int row0,
+                                                 int col0, int lane)
+{
+    static_assert(EPI == EPI_S8 || EPI == EPI_S32, "register pass: fast modes only");
+    const EpiParams& ep = p.ep;
+    const int qi = lane & 3;
+    const int colq = (lane & 31) & ~3;
+    const int32_t relu_floor = ep.act == NNOPS_ACT_RELU ? 0 : INT32_MIN;
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    const float zpf = (float)ep.zp_out;
+    const float lo = __fsub_rn(u8 ? 0.0f : -128.0f, zpf);
+    const float hi = __fsub_rn(u8 ? 255.0f : 127.0f, zpf);
+    const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n_own = col0 + j * 32 + (lane & 31);       // column held before the transpose
+        const EpiCol col = epi_col(ep, min(n_own, p.n - 1));
+        const float req = __fmul_rn(row_k, col.s_b);
+        const int n_st = col0 + j * 32 + colq;               // first column stored by this lane
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int m = row0 + i * 32 + 8 * g + 4 * (lane >> 5) + qi;
+                char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+                if constexpr (EPI == EPI_S8) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int32_t v = max(acc[i][j][4 * g + e] + col.bias, relu_floor);
+                        float x = __fmul_rn((float)v, req);
+                        x = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
+                        const int32_t q = (int32_t)round_half_away(x) + ep.zp_out;
+                        w |= ((uint32_t)q & 0xffu) << (8 * e);
+                    }
+                    w = quad_transpose_bytes(w, qi);
+                    if (m < p.m && n_st < p.n) {
+                        *reinterpret_cast<uint32_t*>(cptr + n_st) = w;
+                    }
+                } else {
+                    int32_t v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = max(acc[i][j][4 * g + e] + col.bias, relu_floor);
+                    }
+                    quad_transpose_dwords(v, qi);
+                    if (m < p.m && n_st < p.n) {
+                        *reinterpret_cast<v4i*>(cptr + (int64_t)n_st * 4) = v4i{v[0], v[1], v[2], v[3]};
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int WPE, bool FULLK, bool ALIGNED, bool FLIP, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void gemm_i8_mfma(GemmI8Kern p)
 {
     constexpr int T = WM * WN * 64;
     constexpr int TM = BM / WM;           // wave tile rows
@@ -139,8 +416,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_i8_mfma(GemmI8Kern p)
     constexpr int CB = BN * (kBK / 16) / T;
     static_assert(CA >= 1 && CB >= 1 && CA * T == BM * 4 && CB * T == BN * 4, "tile/threads");
 
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) int8_t lds_b[2][BN * kLdsRow];
+    constexpr int kStageBytes = 2 * (BM + BN) * kLdsRow;
+    constexpr int kEpiPitch = TN + 4;                      // int32 per staged output row
+    constexpr int kEpiBytes = WM * WN * 32 * kEpiPitch * 4;
+    static_assert(kEpiBytes <= kStageBytes, "epilogue staging must fit the stage buffers");
+    __shared__ __attribute__((aligned(16))) int8_t lds_raw[kStageBytes];
+    int8_t (*lds_a)[BM * kLdsRow] = reinterpret_cast<int8_t (*)[BM * kLdsRow]>(lds_raw);
+    int8_t (*lds_b)[BN * kLdsRow] = reinterpret_cast<int8_t (*)[BN * kLdsRow]>(lds_raw + 2 * BM * kLdsRow);
 
     int tm, tn;
     tile_coords((p.m + BM - 1) / BM, (p.n + BN - 1) / BN, tm, tn);
@@ -152,8 +434,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_i8_mfma(GemmI8Kern p)
     const int wm0 = (wave / WN) * TM;
     const int wn0 = (wave % WN) * TN;
 
-    // Per-thread global source rows for the stage loads (clamped into range:
-    // rows past M/N are computed but never stored).
+    // Per-thread stage chunks (rows past M/N are clamped: computed, never stored).
     const int8_t* a_src[CA];
     const int8_t* b_src[CB];
     int a_lds[CA], b_lds[CB], a_kc[CA], b_kc[CB];
@@ -175,24 +456,166 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_i8_mfma(GemmI8Kern p)
     }
 
     v4i ra[CA], rb[CB];
-    auto load_stage = [&](int k0) {
+    v16i acc[FM][FN];
 #pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            ra[i] = load16_a<ALIGNED>(a_src[i], k0 + a_kc[i], p.k, p.a_xor);
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            acc[i][j] = v16i{0};
+        }
+    }
+
+    const int frag_row = lane & 31;
+    const int frag_k = (lane >> 5) * 16;
+    const int kt = (p.k + kBK - 1) / kBK;
+
+    load_chunks<CA, FULLK, ALIGNED, FLIP>(ra, a_src, a_kc, 0, p.k, p.a_xor);
+    load_chunks<CB, FULLK, ALIGNED, false>(rb, b_src, b_kc, 0, p.k, 0u);
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+        *reinterpret_cast<v4i*>(&lds_a[0][a_lds[i]]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        *reinterpret_cast<v4i*>(&lds_b[0][b_lds[i]]) = rb[i];
+    }
+    __syncthreads();
+
+    for (int t = 0; t < kt; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < kt;
+        if (more) {
+            load_chunks<CA, FULLK, ALIGNED, FLIP>(ra, a_src, a_kc, (t + 1) * kBK, p.k, p.a_xor);
+            load_chunks<CB, FULLK, ALIGNED, false>(rb, b_src, b_kc, (t + 1) * kBK, p.k, 0u);
+        }
+        const int8_t* la = &lds_a[cur][(wm0 + frag_row) * kLdsRow + frag_k];
+        const int8_t* lb = &lds_b[cur][(wn0 + frag_row) * kLdsRow + frag_k];
+#pragma unroll
+        for (int ks = 0; ks < kBK; ks += 32) {
+            v4i fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                fa[i] = *reinterpret_cast<const v4i*>(la + i * 32 * kLdsRow + ks);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                fb[j] = *reinterpret_cast<const v4i*>(lb + j * 32 * kLdsRow + ks);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < CA; ++i) {
+                *reinterpret_cast<v4i*>(&lds_a[cur ^ 1][a_lds[i]]) = ra[i];
+            }
+#pragma unroll
+            for (int i = 0; i < CB; ++i) {
+                *reinterpret_cast<v4i*>(&lds_b[cur ^ 1][b_lds[i]]) = rb[i];
+            }
+        }
+        __syncthreads();
+    }
+
+    if constexpr (EPI == EPI_GENERIC) {
+        output_pass<FM, FN, TN, EPI>(p, acc, reinterpret_cast<int32_t*>(lds_raw) + wave * 32 * kEpiPitch,
+                                     m0 + wm0, n0 + wn0, lane);
+    } else {
+        output_pass_regs<FM, FN, EPI>(p, acc, m0 + wm0, n0 + wn0, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Large-tile kernel with an asynchronous LDS ring (full-K, 16-byte-aligned
+// operands). Stages are filled by global_load_lds_dwordx4: each wave
+// instruction writes 1 KiB of LDS contiguously (lane l -> bytes 16l..16l+15),
+// i.e. 16 tile rows of 64 bytes, so the 16-byte chunk a lane fetches from HBM
+// is chosen to land in a swizzled slot: row r's logical chunk c lives in slot
+// c ^ ((r >> 2) & 3). A fragment read serves 16 lanes (16 consecutive rows,
+// one logical chunk) per LDS cycle; with 64 four-byte banks (256 bytes per
+// cycle) those 16 reads land on 16 distinct 16-byte bank groups, so the read
+// is conflict-free with no padding. NS stages are in flight, so each load has NS-1 k-steps of MFMA
+// work (~3K cycles at 256x256) to land before it is needed.
+// ---------------------------------------------------------------------------
+#define NNOPS_GPTR(x) ((const __attribute__((address_space(1))) void*)(x))
+#define NNOPS_LPTR(x) ((__attribute__((address_space(3))) void*)(x))
+
+// s_waitcnt immediate: wait until at most n vector-memory ops are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void block_barrier()
+{
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS access moves across the barrier
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int EPI, int PROBE = 0>
+__global__ __launch_bounds__(WM * WN * 64)
+__attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+void gemm_i8_ring(GemmI8Kern p)
+{
+    constexpr int W = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int QA = BM / 16 / W;              // 1 KiB load instructions per wave per stage (A)
+    constexpr int QB = BN / 16 / W;
+    constexpr int L = QA + QB;                    // vector-memory ops per wave per stage
+    constexpr int kStage = (BM + BN) * 64;
+    constexpr int kEpiPitch = TN + 4;
+    static_assert(QA * W * 16 == BM && QB * W * 16 == BN, "rows per stage");
+    static_assert((EPI != EPI_GENERIC && PROBE == 0) || W * 32 * kEpiPitch * 4 <= NS * kStage,
+                  "epilogue staging fits the ring");
+    static_assert((NS - 1) * L < 64, "vmcnt range");
+
+    __shared__ __attribute__((aligned(1024))) int8_t ring[NS * kStage];
+    long long probe_c0 = 0, probe_r0 = 0;
+    if constexpr (PROBE == 5) {  // timing probe: shader clock vs real time
+        probe_c0 = clock64();
+        probe_r0 = (long long)__builtin_amdgcn_s_memrealtime();
+    }
+
+    int tm, tn;
+    tile_coords((p.m + BM - 1) / BM, (p.n + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / WN) * TM, wn0 = (wave % WN) * TN;
+
+    // This lane's source offsets for its QA + QB load instructions.
+    int64_t a_off[QA], b_off[QB];
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+        const int r = (wave * QA + q) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        a_off[q] = (int64_t)min(m0 + r, p.m - 1) * p.lda + c * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+        const int r = (wave * QB + q) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        b_off[q] = (int64_t)min(n0 + r, p.n - 1) * p.ldb + c * 16;
+    }
+    auto issue = [&](int stage_k, int slot) {
+        int8_t* base = ring + slot * kStage;
+#pragma unroll
+        for (int q = 0; q < QA; ++q) {
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(p.a + a_off[q] + stage_k),
+                                             NNOPS_LPTR(base + (wave * QA + q) * 1024), 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            rb[i] = load16<ALIGNED>(b_src[i], k0 + b_kc[i], p.k);
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            *reinterpret_cast<v4i*>(&lds_a[buf][a_lds[i]]) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            *reinterpret_cast<v4i*>(&lds_b[buf][b_lds[i]]) = rb[i];
+        for (int q = 0; q < QB; ++q) {
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(p.b + b_off[q] + stage_k),
+                                             NNOPS_LPTR(base + BM * 64 + (wave * QB + q) * 1024), 16, 0, 0);
         }
     };
 
@@ -205,68 +628,165 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_i8_mfma(GemmI8Kern p)
         }
     }
 
-    const int kt = (p.k + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
+    const int kt = p.k / 64;
+    // Fragment read offsets: row (lane & 31) of each 32-row fragment, logical
+    // chunk ks/16 + lane/32 in slot (chunk ^ swz), swz = ((lane & 31) >> 2) & 3.
+    const int swz = ((lane & 31) >> 2) & 3;
+    const int c0 = ((lane >> 5) ^ swz) * 16;          // k half 0
+    const int c1 = ((2 + (lane >> 5)) ^ swz) * 16;    // k half 1
+    const int a_row = (wm0 + (lane & 31)) * 64;
+    const int b_row = BM * 64 + (wn0 + (lane & 31)) * 64;
 
-    const int frag_row = lane & 31;
-    const int frag_k = (lane >> 5) * 16;
-    for (int t = 0; t < kt; ++t) {
-        const int cur = t & 1;
-        if (t + 1 < kt) {
-            load_stage((t + 1) * kBK);
+    auto read_frags = [&](const int8_t* st, int cc, v4i (&fa)[FM], v4i (&fb)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
         }
 #pragma unroll
-        for (int ks = 0; ks < kBK; ks += 32) {
-            v4i fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                fa[i] = *reinterpret_cast<const v4i*>(
-                    &lds_a[cur][(wm0 + i * 32 + frag_row) * kLdsRow + ks + frag_k]);
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                fb[j] = *reinterpret_cast<const v4i*>(
-                    &lds_b[cur][(wn0 + j * 32 + frag_row) * kLdsRow + ks + frag_k]);
-            }
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-                }
-            }
+        for (int j = 0; j < FN; ++j) {
+            fb[j] = *reinterpret_cast<const v4i*>(st + b_row + j * 32 * 64 + cc);
         }
-        if (t + 1 < kt) {
-            store_stage(cur ^ 1);
-        }
-        __syncthreads();
-    }
-
-    // Output pass. 32x32 accumulator layout: lane holds column (lane & 31) and
-    // rows 8*(r/4) + 4*(lane/32) + (r%4) for r in 0..15.
-    const int ebytes = out_elem_bytes(p.ep.out_kind);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn0 + j * 32 + (lane & 31);
-        if (n >= p.n) {
-            continue;
-        }
-        const EpiCol col = epi_col(p.ep, n);
+    };
+    auto mfma_all = [&](const v4i (&fa)[FM], const v4i (&fb)[FN]) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.m) {
-                    const EpiRow row = epi_row(p.ep, m);
-                    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
-                    (void)ebytes;
-                    epi_store(p.ep, row, col, acc[i][j][r], crow, n);
+            for (int j = 0; j < FN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+    // Interleave the next fragment reads with this half's MFMAs: one
+    // ds_read_b128 after each of the first FM + FN MFMAs, so every read has at
+    // least half a phase of matrix work to land before it is needed.
+    auto schedule = [&]() {
+#pragma unroll
+        for (int q = 0; q < FM + FN; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
+    };
+
+    // Ring: stage s goes to slot s % NS; nothing is issued past the last k
+    // step, so the vmcnt waits below count only the stages really in flight.
+    auto issue_stage = [&](int s) {
+        if (s < kt) {
+            issue(s * 64, s % NS);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        issue_stage(s);
+    }
+    if (kt >= NS) {
+        wait_vmcnt<(NS - 1) * L>();   // stage 0 landed, stages 1..NS-1 may be in flight
+    } else {
+        wait_vmcnt<0>();
+    }
+    block_barrier();
+
+    v4i f0a[FM], f0b[FN], f1a[FM], f1b[FN];
+    read_frags(ring, c0, f0a, f0b);
+    // One k step: half 0 of stage t on the matrix cores while half 1's
+    // fragments load; barrier (stage t+1 landed everywhere, stage t's slot free);
+    // half 1 of stage t while half 0 of stage t+1 loads and stage t+NS is
+    // issued into stage t's slot. STEADY: every stage up to t+NS-1 was issued,
+    // so exactly NS-2 stages may stay in flight.
+    auto step = [&](int t, bool steady) {
+        const int8_t* st = ring + (t % NS) * kStage;
+        if constexpr (PROBE != 7) {
+            read_frags(st, c1, f1a, f1b);
+        }
+        mfma_all(f0a, f0b);
+        schedule();
+        if constexpr (PROBE != 6) {  // timing probe 6: no barrier, no loads
+            if (steady) {
+                wait_vmcnt<(NS - 2) * L>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            block_barrier();
+        }
+        if constexpr (PROBE != 7) {
+            read_frags(ring + ((t + 1) % NS) * kStage, c0, f0a, f0b);
+        }
+        if constexpr (PROBE != 2 && PROBE != 6) {  // timing probe 2: no loads inside the loop
+            if (steady) {
+                issue((t + NS) * 64, t % NS);
+            }
+        }
+        mfma_all(f1a, f1b);
+        if (steady && FM * FN >= L + FM + FN) {
+            // loads first (one per MFMA), then the fragment reads, then the rest
+#pragma unroll
+            for (int q = 0; q < L; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+#pragma unroll
+            for (int q = 0; q < FM + FN; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            if constexpr (FM * FN > L + FM + FN) {
+                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - L - (FM + FN), 0);
+            }
+        } else if (steady) {
+            // fewer MFMAs than loads + reads: each MFMA carries a load (while
+            // any remain) and a fragment read (while any remain)
+#pragma unroll
+            for (int q = 0; q < FM * FN; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (q < L) {
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+                if (q < FM + FN) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+        } else {
+            schedule();
+        }
+    };
+    int t = 0;
+    for (; t + NS < kt; ++t) {
+        step(t, true);
+    }
+    for (; t < kt; ++t) {
+        step(t, false);
+    }
+    __syncthreads();
+
+    if constexpr (PROBE == 5) {
+        if (threadIdx.x == 0) {
+            long long* d = reinterpret_cast<long long*>(p.c) + 2 * blockIdx.x;
+            d[0] = clock64() - probe_c0;
+            d[1] = (long long)__builtin_amdgcn_s_memrealtime() - probe_r0;
+        }
+    }
+    if constexpr (PROBE == 1 || PROBE >= 5) {  // timing probe: no output pass (every accumulator consumed)
+        int32_t x = 0;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    x ^= acc[i][j][r];
                 }
             }
         }
+        if (x == 0x7fffffff) {
+            static_cast<int32_t*>(p.c)[threadIdx.x] = x;
+        }
+        return;
+    }
+    if constexpr (EPI == EPI_GENERIC || PROBE != 0) {
+        output_pass<FM, FN, TN, EPI, PROBE>(p, acc, reinterpret_cast<int32_t*>(ring) + wave * 32 * kEpiPitch,
+                                            m0 + wm0, n0 + wn0, lane);
+    } else {
+        output_pass_regs<FM, FN, EPI>(p, acc, m0 + wm0, n0 + wn0, lane);
     }
 }
 
@@ -414,15 +934,59 @@ WsPlan plan_workspace(const NnopsGemmI8Args& g)
 
 inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 0) && (ld % 16 == 0); }
 
-template <int BM, int BN, int WM, int WN>
-void launch_gemm(const GemmI8Kern& k, bool aligned, hipStream_t s)
+template <int BM, int BN, int WM, int WN, int WPE, bool FULLK, bool ALIGNED>
+void launch_gemm_epi(const GemmI8Kern& k, int epi, hipStream_t s)
 {
     const int tiles = ((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN);
-    if (aligned) {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, true>), dim3(tiles), dim3(WM * WN * 64), 0, s, k);
+    const dim3 grid(tiles), block(WM * WN * 64);
+    if (k.a_xor != 0u) {
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, true, EPI_GENERIC>), grid, block, 0, s, k);
+    } else if (epi == EPI_S8) {
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S8>), grid, block, 0, s, k);
+    } else if (epi == EPI_S32) {
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S32>), grid, block, 0, s, k);
     } else {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, false>), dim3(tiles), dim3(WM * WN * 64), 0, s, k);
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_GENERIC>), grid, block, 0, s, k);
     }
+}
+
+template <int BM, int BN, int WM, int WN, int WPE>
+void launch_gemm(const GemmI8Kern& k, bool aligned, bool fullk, int epi, hipStream_t s)
+{
+    if (fullk) {
+        launch_gemm_epi<BM, BN, WM, WN, WPE, true, true>(k, epi, s);
+    } else if (aligned) {
+        launch_gemm_epi<BM, BN, WM, WN, WPE, false, true>(k, epi, s);
+    } else {
+        launch_gemm_epi<BM, BN, WM, WN, WPE, false, false>(k, epi, s);
+    }
+}
+
+void launch_ring(const GemmI8Kern& k, int epi, hipStream_t s)
+{
+    const int tiles = ((k.m + 255) / 256) * ((k.n + 255) / 256);
+    if (epi == EPI_S8) {
+        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_S8>), dim3(tiles), dim3(512), 0, s, k);
+    } else if (epi == EPI_S32) {
+        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_S32>), dim3(tiles), dim3(512), 0, s, k);
+    } else {
+        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_GENERIC>), dim3(tiles), dim3(512), 0, s, k);
+    }
+}
+
+// Which output-pass specialisation a call can take: the fast modes need
+// row-uniform parameters, no zero-point terms, half-away rounding, and a
+// destination that takes packed stores for every 4-column group.
+int choose_epi(const NnopsGemmI8Args& g, const EpiParams& e)
+{
+    if (e.compensate || g.s_out_rows != nullptr || g.zp_out_rows != nullptr || g.float_ep ||
+        g.round_even || (g.n % 4) != 0 || ((uintptr_t)g.c & 15) != 0) {
+        return EPI_GENERIC;
+    }
+    if (g.out_kind == NNOPS_OUT_S32) {
+        return (g.ldc * 4) % 16 == 0 ? EPI_S32 : EPI_GENERIC;
+    }
+    return (g.s_a == nullptr && g.ldc % 4 == 0) ? EPI_S8 : EPI_GENERIC;
 }
 
 }  // namespace
@@ -539,6 +1103,8 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     }
 
     const bool aligned = aligned16(k.a, k.lda) && aligned16(k.b, k.ldb) && (g->k % 16 == 0);
+    const bool fullk = aligned && (g->k % 64 == 0);
+    const int epi = choose_epi(*g, e);
     if (g->m <= 16) {
         const unsigned blocks = (unsigned)((g->n + 15) / 16);
         if (aligned) {
@@ -546,12 +1112,14 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         } else {
             hipLaunchKernelGGL((gemv_i8_mfma<4, false>), dim3(blocks), dim3(256), 0, s, k);
         }
+    } else if (g->m >= 1024 && g->n >= 1024 && fullk && !g->a_u8) {
+        launch_ring(k, epi, s);
     } else if (g->m >= 1024 && g->n >= 1024) {
-        launch_gemm<256, 256, 2, 2>(k, aligned, s);
+        launch_gemm<256, 256, 2, 2, 1>(k, aligned, fullk, epi, s);
     } else if (g->m >= 64) {
-        launch_gemm<128, 128, 2, 2>(k, aligned, s);
+        launch_gemm<128, 128, 2, 2, 2>(k, aligned, fullk, epi, s);
     } else {
-        launch_gemm<32, 64, 1, 2>(k, aligned, s);
+        launch_gemm<32, 64, 1, 2, 4>(k, aligned, fullk, epi, s);
     }
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
