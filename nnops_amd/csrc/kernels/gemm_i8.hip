@@ -856,6 +856,122 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma(GemmI8Kern p)
 }
 
 // ---------------------------------------------------------------------------
+// Row GEMV, M <= 4, B k-contiguous ([N][K]). A wave owns R consecutive rows of
+// B; lane l reads the 16-byte chunks k = 16*(l + 64c), so every wave load
+// instruction streams 1 KiB of one row contiguously (non-temporal: the
+// weights are read once). Dots on v_dot4_i32_i8, A kept in registers per
+// 4 KiB k block, cross-lane sum at the end. Bound: HBM.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_sum(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off, 64);
+    }
+    return v;
+}
+
+template <int MT, int R, bool FLIP, int WPB = 4, int SPLIT = 1>
+__global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
+{
+    // SPLIT > 1: SPLIT consecutive waves share one row (R = 1), each taking an
+    // interleaved 1/SPLIT of its 1 KiB k chunks; partial sums meet in LDS.
+    static_assert(SPLIT == 1 || R == 1, "split rows are single rows");
+    static_assert(WPB % SPLIT == 0, "a row's waves share a block");
+    constexpr int C = 4;                       // 16-byte chunks per lane per row per k block
+    __shared__ int part[SPLIT > 1 ? WPB : 1][R * MT];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = wave % SPLIT;
+    const int n0 = ((blockIdx.x * WPB + wave) / SPLIT) * R;
+    const bool row_live = n0 < p.n;
+    const int8_t* brow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        brow[r] = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb;
+    }
+    int acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = 0;
+        }
+    }
+    for (int kb = 0; kb < p.k; kb += 64 * 16 * C) {
+        v4i w[R][C], a[MT][C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int k = kb + (lane + 64 * c) * 16;
+            const bool live = row_live && (c % SPLIT == sub) && k < p.k;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                w[r][c] = live ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(brow[r] + k))
+                               : v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int mm = min(m, p.m - 1);
+                v4i x = live ? *reinterpret_cast<const v4i*>(p.a + (int64_t)mm * p.lda + k) : v4i{0, 0, 0, 0};
+                if constexpr (FLIP) {
+                    x = flip_u8(x, p.a_xor, live);
+                }
+                a[m][c] = x;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    int s = acc[r][m];
+                    s = __builtin_amdgcn_sdot4(a[m][c].x, w[r][c].x, s, false);
+                    s = __builtin_amdgcn_sdot4(a[m][c].y, w[r][c].y, s, false);
+                    s = __builtin_amdgcn_sdot4(a[m][c].z, w[r][c].z, s, false);
+                    s = __builtin_amdgcn_sdot4(a[m][c].w, w[r][c].w, s, false);
+                    acc[r][m] = s;
+                }
+            }
+        }
+    }
+    int mine = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int v = wave_sum(acc[r][m]);
+            if (lane == r * MT + m) {
+                mine = v;
+            }
+        }
+    }
+    if constexpr (SPLIT > 1) {
+        if (lane < R * MT) {
+            part[wave][lane] = mine;
+        }
+        __syncthreads();
+        if (sub != 0) {
+            return;
+        }
+        if (lane < R * MT) {
+#pragma unroll
+            for (int q = 1; q < SPLIT; ++q) {
+                mine += part[wave + q][lane];
+            }
+        }
+    }
+    if (row_live && lane < R * MT) {
+        const int r = lane / MT, m = lane % MT;
+        const int n = n0 + r;
+        if (n < p.n && m < p.m) {
+            char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+            epi_store(p.ep, epi_row(p.ep, m), epi_col(p.ep, n), mine, crow, n);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prepasses
 // ---------------------------------------------------------------------------
 // dst[c][r] = src[r][c] for r < R, c < C; dst columns r in [R, Rp) are zeroed.
@@ -1105,7 +1221,25 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     const bool aligned = aligned16(k.a, k.lda) && aligned16(k.b, k.ldb) && (g->k % 16 == 0);
     const bool fullk = aligned && (g->k % 64 == 0);
     const int epi = choose_epi(*g, e);
-    if (g->m <= 16) {
+    if (g->m <= 4 && aligned) {
+        constexpr int R = 1;
+        const unsigned blocks = (unsigned)((g->n + 4 * R - 1) / (4 * R));
+        const bool flip = k.a_xor != 0u;
+#define NNOPS_ROWS(MT)                                                                              \
+        if (flip) {                                                                                 \
+            hipLaunchKernelGGL((gemv_i8_rows<MT, R, true>), dim3(blocks), dim3(256), 0, s, k);      \
+        } else {                                                                                    \
+            hipLaunchKernelGGL((gemv_i8_rows<MT, R, false>), dim3(blocks), dim3(256), 0, s, k);     \
+        }
+        if (g->m == 1) {
+            NNOPS_ROWS(1)
+        } else if (g->m == 2) {
+            NNOPS_ROWS(2)
+        } else {
+            NNOPS_ROWS(4)
+        }
+#undef NNOPS_ROWS
+    } else if (g->m <= 16) {
         const unsigned blocks = (unsigned)((g->n + 15) / 16);
         if (aligned) {
             hipLaunchKernelGGL((gemv_i8_mfma<4, true>), dim3(blocks), dim3(256), 0, s, k);

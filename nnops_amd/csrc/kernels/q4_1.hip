@@ -125,12 +125,12 @@ __global__ __launch_bounds__(256) void gemv_q4_1_nk(Q41Kern p)
             for (int r = 0; r < kNkRowsPerWave; ++r) {
                 const int n = min(row0 + r, p.n - 1);
                 const uint8_t* src = p.b + (int64_t)n * p.ldb + (int64_t)(cb0 + blk) * 20;
-                const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
+                const v4i_a4 x = __builtin_nontemporal_load(reinterpret_cast<const v4i_a4*>(src));
                 raw[r][0] = (uint32_t)x.x;
                 raw[r][1] = (uint32_t)x.y;
                 raw[r][2] = (uint32_t)x.z;
                 raw[r][3] = (uint32_t)x.w;
-                raw[r][4] = *reinterpret_cast<const uint32_t*>(src + 16);
+                raw[r][4] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + 16));
             }
 #pragma unroll
             for (int r = 0; r < kNkRowsPerWave; ++r) {
@@ -213,6 +213,327 @@ __global__ __launch_bounds__(256) void gemv_q4_1_nk(Q41Kern p)
         const int n = row0 + r;
         if (n < p.n && m < p.m) {
             store_out(p, m, n, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV v2, blocks along K, f16 A, M <= 2: no LDS. A wave owns R rows; lane l
+// owns blocks l, l+64, ... of every row, reads those blocks' A values straight
+// from global memory (L1/L2-resident: A is K*2 bytes), widens them to f16
+// pairs and forms the block sums once, then streams its R rows' blocks
+// (non-temporal dwordx4 + dword per block) and dots them on v_dot2_f32_f16.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t nib_pair(uint32_t nibs, uint32_t sel)
+{
+    // two nibble bytes -> f16 pair (0x54qq = 64 + q/16) via v_perm_b32
+    return __builtin_amdgcn_perm(0x54545454u, nibs, sel);
+}
+
+template <int MT, int R>
+__global__ __launch_bounds__(256) void gemv_q4_1_rows(Q41Kern p)
+{
+    constexpr int NB = 2;                    // blocks per lane per pass, all loads issued up front
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * 4 + wave) * R;
+    if (n0 >= p.n) {
+        return;
+    }
+    const int nb = (p.k + 31) / 32;
+    const _Float16* A = static_cast<const _Float16*>(p.a);
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = 0.0f;
+        }
+    }
+    const bool a_vec = ((p.lda & 7) == 0) && (((uintptr_t)A & 15) == 0);
+    const uint8_t* rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rows[r] = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb;
+    }
+    for (int b0 = 0; b0 < nb; b0 += 64 * NB) {
+        uint32_t raw[NB][R][5];
+        uint32_t ah[NB][MT][16];
+        // weights first (the HBM stream), then this lane's A values (L1/L2)
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int blk = b0 + lane + 64 * u;
+            const bool live = blk < nb;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint8_t* src = rows[r] + (int64_t)(live ? blk : 0) * 20;
+                const v4i_a4 x = __builtin_nontemporal_load(reinterpret_cast<const v4i_a4*>(src));
+                raw[u][r][0] = live ? (uint32_t)x.x : 0u;   // d = m = 0: a dead block adds 0
+                raw[u][r][1] = (uint32_t)x.y;
+                raw[u][r][2] = (uint32_t)x.z;
+                raw[u][r][3] = (uint32_t)x.w;
+                raw[u][r][4] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + 16));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int blk = b0 + lane + 64 * u;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int mm = min(m, p.m - 1);
+                const _Float16* arow = A + (int64_t)mm * p.lda + (int64_t)blk * 32;
+                if (a_vec && blk * 32 + 32 <= p.k) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const v4i x = *reinterpret_cast<const v4i*>(arow + 8 * q);
+                        ah[u][m][4 * q + 0] = (uint32_t)x.x;
+                        ah[u][m][4 * q + 1] = (uint32_t)x.y;
+                        ah[u][m][4 * q + 2] = (uint32_t)x.z;
+                        ah[u][m][4 * q + 3] = (uint32_t)x.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const int k = blk * 32 + 2 * j;
+                        const uint32_t lo = k < p.k ? __builtin_bit_cast(uint16_t, arow[2 * j]) : 0u;
+                        const uint32_t hi = k + 1 < p.k ? __builtin_bit_cast(uint16_t, arow[2 * j + 1]) : 0u;
+                        ah[u][m][j] = lo | (hi << 16);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            float asum[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float sa = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    sa = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[u][m][j]),
+                                                __builtin_bit_cast(v2h, 0x3c003c00u), sa, false);
+                }
+                asum[m] = sa;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float d = h2f(raw[u][r][0] & 0xffffu);
+                const float mn = h2f(raw[u][r][0] >> 16);
+                uint32_t h[16];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lo = raw[u][r][1 + i] & 0x0f0f0f0fu;
+                    const uint32_t hi = (raw[u][r][1 + i] >> 4) & 0x0f0f0f0fu;
+                    h[2 * i] = nib_pair(lo, 0x04010400u);
+                    h[2 * i + 1] = nib_pair(lo, 0x04030402u);
+                    h[8 + 2 * i] = nib_pair(hi, 0x04010400u);
+                    h[8 + 2 * i + 1] = nib_pair(hi, 0x04030402u);
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float sq = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        sq = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[u][m][j]),
+                                                    __builtin_bit_cast(v2h, h[j]), sq, false);
+                    }
+                    // sum_j a_j (d q_j + mn) = 16 d (sq - 64 asum) + mn asum
+                    const float qsum = 16.0f * (sq - 64.0f * asum[m]);
+                    acc[r][m] = fmaf(d, qsum, fmaf(mn, asum[m], acc[r][m]));
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                v += __shfl_xor(v, off, 64);
+            }
+            acc[r][m] = v;
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (n0 + r < p.n && m < p.m) {
+                    store_out(p, m, n0 + r, acc[r][m]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV v3, blocks along K, f16 A, M <= 2, rows of up to 128 blocks (K <= 4096
+// per pass): each wave pulls its R rows into a private LDS region with
+// global_load_lds_dwordx4 (1 KiB contiguous per instruction, so the HBM stream
+// is perfectly coalesced), then every lane reads its own 20-byte blocks back
+// from LDS. A wave only reads what it loaded itself: no block barrier.
+// ---------------------------------------------------------------------------
+#define NNOPS_GPTR(x) ((const __attribute__((address_space(1))) void*)(x))
+#define NNOPS_LPTR(x) ((__attribute__((address_space(3))) void*)(x))
+
+template <int MT, int R, int PROBE = 0>
+__global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
+{
+    constexpr int kRowBytes = 3072;                    // >= 128 blocks * 20 bytes, 3 DMA instructions
+    __shared__ __attribute__((aligned(16))) uint8_t stage[4][R][kRowBytes];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * 4 + wave) * R;
+    if (n0 >= p.n) {
+        return;
+    }
+    const int nb = (p.k + 31) / 32;                     // host guarantees nb <= 128
+    const int row_bytes = nb * 20;
+    const _Float16* A = static_cast<const _Float16*>(p.a);
+    if (PROBE == 2 && p.ldb == row_bytes && n0 + R <= p.n) {
+        // adjacent rows are one contiguous span: no over-read
+        const uint8_t* span = p.b + (int64_t)n0 * p.ldb;
+        const int span_bytes = R * row_bytes;
+        for (int q = 0; q * 1024 < span_bytes; ++q) {
+            const int off = q * 1024 + lane * 16;
+            const uint8_t* src = span + (off + 16 <= span_bytes ? off : 0);
+            const int r = off / row_bytes;
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(src), NNOPS_LPTR(&stage[wave][0][0] + q * 1024), 16, 0, 2);
+            (void)r;
+        }
+    } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint8_t* row = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb;
+#pragma unroll
+        for (int q = 0; q < kRowBytes / 1024; ++q) {
+            const int off = q * 1024 + lane * 16;
+            // chunks past the row re-read its start (kept in bounds, never used)
+            const uint8_t* src = row + (off + 16 <= row_bytes ? off : 0);
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(src), NNOPS_LPTR(&stage[wave][r][q * 1024]), 16, 0, 2);
+        }
+    }
+    }
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = 0.0f;
+        }
+    }
+    // A for this lane's blocks while the weights land
+    constexpr int NB = 2;
+    uint32_t ah[NB][MT][16];
+    const bool a_vec = ((p.lda & 7) == 0) && (((uintptr_t)A & 15) == 0);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int blk = lane + 64 * u;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int mm = min(m, p.m - 1);
+            const _Float16* arow = A + (int64_t)mm * p.lda + (int64_t)blk * 32;
+            if (a_vec && blk * 32 + 32 <= p.k) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const v4i x = *reinterpret_cast<const v4i*>(arow + 8 * q);
+                    ah[u][m][4 * q + 0] = (uint32_t)x.x;
+                    ah[u][m][4 * q + 1] = (uint32_t)x.y;
+                    ah[u][m][4 * q + 2] = (uint32_t)x.z;
+                    ah[u][m][4 * q + 3] = (uint32_t)x.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int k = blk * 32 + 2 * j;
+                    const uint32_t lo = k < p.k ? __builtin_bit_cast(uint16_t, arow[2 * j]) : 0u;
+                    const uint32_t hi = k + 1 < p.k ? __builtin_bit_cast(uint16_t, arow[2 * j + 1]) : 0u;
+                    ah[u][m][j] = lo | (hi << 16);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070 | (15 << 8));   // vmcnt(0): the wave's DMA landed
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int blk = lane + 64 * u;
+        if (blk >= nb) {
+            continue;
+        }
+        float asum[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float sa = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                sa = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[u][m][j]),
+                                            __builtin_bit_cast(v2h, 0x3c003c00u), sa, false);
+            }
+            asum[m] = sa;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t* bp = PROBE == 2 ? reinterpret_cast<const uint32_t*>(&stage[wave][0][0] + r * row_bytes + blk * 20)
+                                            : reinterpret_cast<const uint32_t*>(&stage[wave][r][blk * 20]);
+            uint32_t raw[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                raw[i] = bp[i];
+            }
+            if constexpr (PROBE == 1) {  // timing probe: no dequant / dot
+                acc[r][0] += __uint_as_float(raw[0] ^ raw[1] ^ raw[2] ^ raw[3] ^ raw[4]) + asum[0];
+                continue;
+            }
+            const float d = h2f(raw[0] & 0xffffu);
+            const float mn = h2f(raw[0] >> 16);
+            uint32_t h[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = raw[1 + i] & 0x0f0f0f0fu;
+                const uint32_t hi = (raw[1 + i] >> 4) & 0x0f0f0f0fu;
+                h[2 * i] = nib_pair(lo, 0x04010400u);
+                h[2 * i + 1] = nib_pair(lo, 0x04030402u);
+                h[8 + 2 * i] = nib_pair(hi, 0x04010400u);
+                h[8 + 2 * i + 1] = nib_pair(hi, 0x04030402u);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float sq = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    sq = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[u][m][j]),
+                                                __builtin_bit_cast(v2h, h[j]), sq, false);
+                }
+                const float qsum = 16.0f * (sq - 64.0f * asum[m]);
+                acc[r][m] = fmaf(d, qsum, fmaf(mn, asum[m], acc[r][m]));
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                v += __shfl_xor(v, off, 64);
+            }
+            acc[r][m] = v;
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (n0 + r < p.n && m < p.m) {
+                    store_out(p, m, n0 + r, acc[r][m]);
+                }
+            }
         }
     }
 }
@@ -583,10 +904,22 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             if (g->trans_b) {
                 const unsigned blocks = (unsigned)((g->n + kNkWaves * kNkRowsPerWave - 1) / (kNkWaves * kNkRowsPerWave));
                 if (g->a_f16) {
-                    if (kk.m == 1) {
-                        hipLaunchKernelGGL((gemv_q4_1_nk<1, true>), dim3(blocks), dim3(256), 0, s, kk);
+                    constexpr int R = 2;
+                    const unsigned rb = (unsigned)((g->n + 4 * R - 1) / (4 * R));
+                    const int64_t nbk = (g->k + 31) / 32;
+                    // LDS-staged rows: whole 16-byte chunks per row, <= 128 blocks
+                    const bool staged = nbk <= 128 && (nbk % 4) == 0 && (g->ldb_bytes % 16) == 0 &&
+                                        ((uintptr_t)g->b & 15) == 0;
+                    if (staged) {
+                        if (kk.m == 1) {
+                            hipLaunchKernelGGL((gemv_q4_1_lds<1, R>), dim3(rb), dim3(256), 0, s, kk);
+                        } else {
+                            hipLaunchKernelGGL((gemv_q4_1_lds<2, R>), dim3(rb), dim3(256), 0, s, kk);
+                        }
+                    } else if (kk.m == 1) {
+                        hipLaunchKernelGGL((gemv_q4_1_rows<1, R>), dim3(rb), dim3(256), 0, s, kk);
                     } else {
-                        hipLaunchKernelGGL((gemv_q4_1_nk<2, true>), dim3(blocks), dim3(256), 0, s, kk);
+                        hipLaunchKernelGGL((gemv_q4_1_rows<2, R>), dim3(rb), dim3(256), 0, s, kk);
                     }
                 } else {
                     hipLaunchKernelGGL((gemv_q4_1_nk<1, false>), dim3(blocks), dim3(256), 0, s, kk);
