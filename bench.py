@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5"])
+    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -136,7 +136,7 @@ def run_cfg2(args, torch, dg, na, stream):
                                "relu, requant (half away from zero)", "M": M, "N": N, "K": K,
                    "weight_layout": "[N,K]"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": tops / PEAK_INT8_TOPS, "traffic": None,
+                     "frac": tops / PEAK_INT8_TOPS, "traffic": measured_traffic("gemm_i8_ring_cfg2"),
                      "kernel": "gemm_i8_ring<256,256,2,4,4,EPI_S8>", "algorithmic_ops_per_launch": ops},
         "dtype": "int8 (s32 accumulate)",
     }
@@ -233,6 +233,29 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
             "M": M, "K": K, "N": N, "a_pitch": 14400, "c_pitch": 4160, "weight_layout": "[N,K]"}
 
 
+def measured_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed counter summary
+    (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by the same
+    counters' reading of a plain copy of known size); None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_counters.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        line = line.strip()
+        if line.startswith("#") or "=" not in line:
+            continue
+        k, v = line.split("=", 1)
+        vals[k.strip()] = v.strip()
+    try:
+        fs, ws = float(vals["fetch_scale"]), float(vals["write_scale"])
+        f = float(vals[f"{kernel_key}.fetch_kib"]) * fs
+        w = float(vals[f"{kernel_key}.write_kib"]) * ws
+    except (KeyError, ValueError):
+        return None
+    return (f + w) * 1024.0
+
+
 def cpu_baseline(seconds):
     """The CPU oracle on a bounded sample of config 2: rows of the same
     4096^3 problem, split over this host's cores with one oracle call per row
@@ -293,6 +316,17 @@ def main():
     na.load()
     stream = torch.cuda.Stream()
 
+    if args.workload == "copy":
+        # plain device copy of 256 MiB, the reference for scaling FETCH_SIZE /
+        # WRITE_SIZE readings (profiles/traffic_counters.txt)
+        x = torch.empty(2 ** 28, dtype=torch.uint8, device="cuda")
+        x.fill_(1)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "copy", "bytes_per_copy": 2 ** 28, "copies": 3}))
+        return
     if args.workload != "cfg2":
         res = {"cfg1": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=128, K=1024, N=1024,
                                             nbuf=1),
