@@ -21,6 +21,15 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they retire in issue order, global_load_lds included).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // ---------------------------------------------------------------------------
 // Epilogue parameters, resolved once on the host (device pointers only).
 // ---------------------------------------------------------------------------

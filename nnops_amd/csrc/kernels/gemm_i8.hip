@@ -546,13 +546,6 @@ void gemm_i8_mfma(GemmI8Kern p)
 #define NNOPS_LPTR(x) ((__attribute__((address_space(3))) void*)(x))
 
 // s_waitcnt immediate: wait until at most n vector-memory ops are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 __device__ __forceinline__ void block_barrier()
 {
     __builtin_amdgcn_s_barrier();
@@ -900,6 +893,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
     }
     for (int kb = 0; kb < p.k; kb += 64 * 16 * C) {
         v4i w[R][C], a[MT][C];
+        // weights first (the HBM stream is the long pole), then A from cache
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             const int k = kb + (lane + 64 * c) * 16;
@@ -909,6 +903,11 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
                 w[r][c] = live ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(brow[r] + k))
                                : v4i{0, 0, 0, 0};
             }
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int k = kb + (lane + 64 * c) * 16;
+            const bool live = row_live && (c % SPLIT == sub) && k < p.k;
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const int mm = min(m, p.m - 1);

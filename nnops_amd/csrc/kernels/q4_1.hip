@@ -19,6 +19,8 @@
 //                  v_mfma_f32_32x32x16_f16, f32 accumulate. Bound: MFMA.
 #include "common.hpp"
 
+#include <utility>
+
 namespace nnops_amd {
 namespace {
 
@@ -379,7 +381,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_rows(Q41Kern p)
 #define NNOPS_GPTR(x) ((const __attribute__((address_space(1))) void*)(x))
 #define NNOPS_LPTR(x) ((__attribute__((address_space(3))) void*)(x))
 
-template <int MT, int R, int PROBE = 0>
+template <int MT, int R>
 __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
 {
     constexpr int kRowBytes = 3072;                    // >= 128 blocks * 20 bytes, 3 DMA instructions
@@ -393,18 +395,6 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
     const int nb = (p.k + 31) / 32;                     // host guarantees nb <= 128
     const int row_bytes = nb * 20;
     const _Float16* A = static_cast<const _Float16*>(p.a);
-    if (PROBE == 2 && p.ldb == row_bytes && n0 + R <= p.n) {
-        // adjacent rows are one contiguous span: no over-read
-        const uint8_t* span = p.b + (int64_t)n0 * p.ldb;
-        const int span_bytes = R * row_bytes;
-        for (int q = 0; q * 1024 < span_bytes; ++q) {
-            const int off = q * 1024 + lane * 16;
-            const uint8_t* src = span + (off + 16 <= span_bytes ? off : 0);
-            const int r = off / row_bytes;
-            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(src), NNOPS_LPTR(&stage[wave][0][0] + q * 1024), 16, 0, 2);
-            (void)r;
-        }
-    } else {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint8_t* row = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb;
@@ -415,7 +405,6 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
             const uint8_t* src = row + (off + 16 <= row_bytes ? off : 0);
             __builtin_amdgcn_global_load_lds(NNOPS_GPTR(src), NNOPS_LPTR(&stage[wave][r][q * 1024]), 16, 0, 2);
         }
-    }
     }
     float acc[R][MT];
 #pragma unroll
@@ -477,16 +466,11 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t* bp = PROBE == 2 ? reinterpret_cast<const uint32_t*>(&stage[wave][0][0] + r * row_bytes + blk * 20)
-                                            : reinterpret_cast<const uint32_t*>(&stage[wave][r][blk * 20]);
+            const uint32_t* bp = reinterpret_cast<const uint32_t*>(&stage[wave][r][blk * 20]);
             uint32_t raw[5];
 #pragma unroll
             for (int i = 0; i < 5; ++i) {
                 raw[i] = bp[i];
-            }
-            if constexpr (PROBE == 1) {  // timing probe: no dequant / dot
-                acc[r][0] += __uint_as_float(raw[0] ^ raw[1] ^ raw[2] ^ raw[3] ^ raw[4]) + asum[0];
-                continue;
             }
             const float d = h2f(raw[0] & 0xffffu);
             const float mn = h2f(raw[0] >> 16);
@@ -513,6 +497,140 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
             }
         }
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                v += __shfl_xor(v, off, 64);
+            }
+            acc[r][m] = v;
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (n0 + r < p.n && m < p.m) {
+                    store_out(p, m, n0 + r, acc[r][m]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV, blocks along K, K = 4096 (128 blocks, 2560-byte rows), rows stored
+// back to back: the pipelined form. A wave first loads its lanes' A (two
+// blocks per lane, from L2), then DMAs its R rows as one contiguous span of
+// 1 KiB pieces into LDS, and decodes each (row, block half) as soon as the
+// pieces it needs have landed, so the decode ALU work overlaps the HBM stream
+// instead of following it (every wave of the launch is resident at once).
+// ---------------------------------------------------------------------------
+template <int MT, int R>
+__global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
+{
+    constexpr int kRow = 128 * 20;
+    constexpr int C = (R * kRow + 1023) / 1024;      // DMA pieces per wave
+    __shared__ __attribute__((aligned(16))) uint8_t stage[4][C * 1024];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * 4 + wave) * R;
+    if (n0 >= p.n) {
+        return;
+    }
+    // A first: its loads retire before the DMA pieces queued behind them
+    const uint32_t* A = static_cast<const uint32_t*>(p.a);   // f16 pairs
+    uint32_t ah[2][MT][16];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const v4i* src = reinterpret_cast<const v4i*>(A + (int64_t)min(m, p.m - 1) * (p.lda / 2) +
+                                                          (lane + 64 * u) * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4i x = src[q];
+                ah[u][m][4 * q + 0] = (uint32_t)x.x;
+                ah[u][m][4 * q + 1] = (uint32_t)x.y;
+                ah[u][m][4 * q + 2] = (uint32_t)x.z;
+                ah[u][m][4 * q + 3] = (uint32_t)x.w;
+            }
+        }
+    }
+    // every lane issues every piece (past the last row: a re-read of the
+    // span's start), so the piece count, and the waits below, are static
+    const uint8_t* first = p.b + (int64_t)n0 * kRow;
+    const int valid = min(R, p.n - n0) * kRow;
+#pragma unroll
+    for (int q = 0; q < C; ++q) {
+        const int off = q * 1024 + lane * 16;
+        __builtin_amdgcn_global_load_lds(NNOPS_GPTR(first + (off + 16 <= valid ? off : 0)),
+                                         NNOPS_LPTR(&stage[wave][q * 1024]), 16, 0, 2);
+    }
+    const v2h one = __builtin_bit_cast(v2h, 0x3c003c00u);
+    float asum[2][MT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[u][m][j]), one, t, false);
+            }
+            asum[u][m] = t;
+        }
+    }
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = 0.0f;
+        }
+    }
+    auto phase = [&]<int RR, int U>() {
+        // last byte this (row, half) needs, and the piece holding it
+        constexpr int last = RR * kRow + (64 * U + 63) * 20 + 19;
+        wait_vmcnt<C - 1 - last / 1024>();
+        asm volatile("" ::: "memory");
+        const uint32_t* bp = reinterpret_cast<const uint32_t*>(&stage[wave][RR * kRow + (lane + 64 * U) * 20]);
+        uint32_t raw[5];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            raw[i] = bp[i];
+        }
+        const float d = h2f(raw[0] & 0xffffu);
+        const float mn = h2f(raw[0] >> 16);
+        uint32_t h[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = raw[1 + i] & 0x0f0f0f0fu;
+            const uint32_t hi = (raw[1 + i] >> 4) & 0x0f0f0f0fu;
+            h[2 * i] = nib_pair(lo, 0x04010400u);
+            h[2 * i + 1] = nib_pair(lo, 0x04030402u);
+            h[8 + 2 * i] = nib_pair(hi, 0x04010400u);
+            h[8 + 2 * i + 1] = nib_pair(hi, 0x04030402u);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                sq = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ah[U][m][j]), __builtin_bit_cast(v2h, h[j]), sq,
+                                            false);
+            }
+            const float qsum = 16.0f * (sq - 64.0f * asum[U][m]);
+            acc[RR][m] = fmaf(d, qsum, fmaf(mn, asum[U][m], acc[RR][m]));
+        }
+    };
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (phase.template operator()<I / 2, I % 2>(), ...);
+    }(std::make_integer_sequence<int, 2 * R>{});
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -910,7 +1028,16 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     // LDS-staged rows: whole 16-byte chunks per row, <= 128 blocks
                     const bool staged = nbk <= 128 && (nbk % 4) == 0 && (g->ldb_bytes % 16) == 0 &&
                                         ((uintptr_t)g->b & 15) == 0;
-                    if (staged) {
+                    // K = 4096 rows stored back to back, aligned A: the pipelined form
+                    const bool pipe = g->k == 128 * 32 && g->ldb_bytes == 128 * 20 && ((uintptr_t)g->b & 15) == 0 &&
+                                      (g->lda % 8) == 0 && ((uintptr_t)kk.a & 15) == 0;
+                    if (pipe) {
+                        if (kk.m == 1) {
+                            hipLaunchKernelGGL((gemv_q4_1_pipe<1, R>), dim3(rb), dim3(256), 0, s, kk);
+                        } else {
+                            hipLaunchKernelGGL((gemv_q4_1_pipe<2, R>), dim3(rb), dim3(256), 0, s, kk);
+                        }
+                    } else if (staged) {
                         if (kk.m == 1) {
                             hipLaunchKernelGGL((gemv_q4_1_lds<1, R>), dim3(rb), dim3(256), 0, s, kk);
                         } else {

@@ -32,6 +32,7 @@ CASES = [
     # (M, K, N): GEMV (M <= 2) and MFMA routes; ragged K / N
     (1, 4096, 1024), (2, 4096, 512), (1, 96, 40), (1, 1000, 77), (2, 8200, 64),
     (3, 256, 130), (16, 4096, 256), (64, 512, 300), (130, 1000, 200),
+    (1, 4096, 1003), (2, 4096, 77),
 ]
 
 
