@@ -20,6 +20,8 @@
 // is associative), so both kernels are bit-exact whatever the k split.
 #include "common.hpp"
 
+#include <utility>
+
 #include <algorithm>
 
 namespace nnops_amd {
@@ -306,17 +308,35 @@ __device__ __forceinline__ int quad_bcast(int v, int k)
 }
 
 // Lane qi holds bytes (row 0..3) of column qi; returns (column 0..3) of row qi.
-__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t w, int qi)
+// Two exchange stages: with lane xor 1 (swapping lane bit 0 with byte bit 0),
+// then with lane xor 2 (bit 1 with bit 1); each is one DPP move and one
+// v_perm whose per-lane byte selectors (sel1, sel2) come from quad_sel.
+// min(max(x, lo), hi) for lo <= hi in one v_med3_i32 (the compiler only forms
+// it when it can prove lo <= hi).
+__device__ __forceinline__ int32_t med3_i32(int32_t x, int32_t lo, int32_t hi)
 {
-    const uint32_t w0 = (uint32_t)quad_bcast((int)w, 0);
-    const uint32_t w1 = (uint32_t)quad_bcast((int)w, 1);
-    const uint32_t w2 = (uint32_t)quad_bcast((int)w, 2);
-    const uint32_t w3 = (uint32_t)quad_bcast((int)w, 3);
-    // v_perm_b32(hi, lo, sel): selector byte b picks lo.byte[b] (b < 4) or hi.byte[b-4]
-    const uint32_t sel = (uint32_t)qi | ((uint32_t)(4 + qi) << 8) | 0x0c0c0000u;
-    const uint32_t t01 = __builtin_amdgcn_perm(w1, w0, sel);
-    const uint32_t t23 = __builtin_amdgcn_perm(w3, w2, sel);
-    return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+    int32_t r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
+struct QuadSel {
+    uint32_t s1, s2;
+};
+
+__device__ __forceinline__ QuadSel quad_sel(int qi)
+{
+    // v_perm_b32(hi = partner, lo = own, sel): selector byte b picks own.byte[b]
+    // (b < 4) or partner.byte[b - 4]
+    return QuadSel{(qi & 1) ? 0x03070105u : 0x06020400u, (qi & 2) ? 0x03020706u : 0x05040100u};
+}
+
+__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t w, const QuadSel& qs)
+{
+    const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xb1, 0xf, 0xf, true);   // quad_perm(1,0,3,2)
+    w = __builtin_amdgcn_perm(p1, w, qs.s1);
+    const uint32_t p2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4e, 0xf, 0xf, true);   // quad_perm(2,3,0,1)
+    return __builtin_amdgcn_perm(p2, w, qs.s2);
 }
 
 // 4x4 dword transpose across the quad: v[r] = (row r, column qi) in,
@@ -347,19 +367,21 @@ __device__ __forceinline__ void quad_transpose_dwords(int32_t (&v)[4], int qi)
     }
 }
 
-template <int FM, int FN, int EPI>
+// BIAS_IN_ACC: the accumulators started from bias[n], so it is not added again.
+template <int FM, int FN, int EPI, bool BIAS_IN_ACC = false>
 __device__ __forceinline__ void output_pass_regs(const GemmI8Kern& p, v16i (&acc)[FM][FN], int row0,
                                                  int col0, int lane)
 {
     static_assert(EPI == EPI_S8 || EPI == EPI_S32, "register pass: fast modes only");
     const EpiParams& ep = p.ep;
     const int qi = lane & 3;
+    const QuadSel qs = quad_sel(qi);
     const int colq = (lane & 31) & ~3;
-    const int32_t relu_floor = ep.act == NNOPS_ACT_RELU ? 0 : INT32_MIN;
+    int32_t relu_floor = ep.act == NNOPS_ACT_RELU ? 0 : INT32_MIN;
+    asm("" : "+s"(relu_floor));   // one max per element, not max + select on the flag
     const bool u8 = ep.out_kind == NNOPS_OUT_U8;
-    const float zpf = (float)ep.zp_out;
-    const float lo = __fsub_rn(u8 ? 0.0f : -128.0f, zpf);
-    const float hi = __fsub_rn(u8 ? 255.0f : 127.0f, zpf);
+    const int32_t lo_i = (u8 ? 0 : -128) - ep.zp_out;
+    const int32_t hi_i = (u8 ? 255 : 127) - ep.zp_out;
     const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -374,16 +396,22 @@ __device__ __forceinline__ void output_pass_regs(const GemmI8Kern& p, v16i (&acc
                 const int m = row0 + i * 32 + 8 * g + 4 * (lane >> 5) + qi;
                 char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
                 if constexpr (EPI == EPI_S8) {
-                    uint32_t w = 0;
+                    uint32_t q[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const int32_t v = max(acc[i][j][4 * g + e] + col.bias, relu_floor);
-                        float x = __fmul_rn((float)v, req);
-                        x = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
-                        const int32_t q = (int32_t)round_half_away(x) + ep.zp_out;
-                        w |= ((uint32_t)q & 0xffu) << (8 * e);
+                        const int32_t v = max(acc[i][j][4 * g + e] + (BIAS_IN_ACC ? 0 : col.bias), relu_floor);
+                        const float x = __fmul_rn((float)v, req);
+                        // round half away from zero (the conversion truncates, as
+                        // trunc() would), then clamp in the integer domain: lo and
+                        // hi are integers and rounding is monotonic, so this equals
+                        // clamping x first; |x| past 2^31 saturates the conversion.
+                        const int32_t r = (int32_t)__fadd_rn(x, __builtin_copysignf(0.5f, x));
+                        q[e] = (uint32_t)(med3_i32(r, lo_i, hi_i) + ep.zp_out);
                     }
-                    w = quad_transpose_bytes(w, qi);
+                    // low bytes of q[0..3] -> one word (0x0c selects a zero byte)
+                    const uint32_t w01 = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);
+                    const uint32_t w23 = __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
+                    const uint32_t w = quad_transpose_bytes(w01 | w23, qs);
                     if (m < p.m && n_st < p.n) {
                         *reinterpret_cast<uint32_t*>(cptr + n_st) = w;
                     }
@@ -391,7 +419,7 @@ __device__ __forceinline__ void output_pass_regs(const GemmI8Kern& p, v16i (&acc
                     int32_t v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        v[e] = max(acc[i][j][4 * g + e] + col.bias, relu_floor);
+                        v[e] = max(acc[i][j][4 * g + e] + (BIAS_IN_ACC ? 0 : col.bias), relu_floor);
                     }
                     quad_transpose_dwords(v, qi);
                     if (m < p.m && n_st < p.n) {
@@ -612,12 +640,21 @@ void gemm_i8_ring(GemmI8Kern p)
         }
     };
 
+    // fast output modes: the accumulators start from this lane's column bias
     v16i acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+    for (int j = 0; j < FN; ++j) {
+        int32_t b0 = 0;
+        if constexpr (EPI != EPI_GENERIC && PROBE == 0) {
+            const int n = n0 + wn0 + j * 32 + (lane & 31);
+            b0 = p.ep.bias ? p.ep.bias[min(n, p.n - 1)] : 0;
+        }
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            acc[i][j] = v16i{0};
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = b0;
+            }
         }
     }
 
@@ -630,14 +667,17 @@ void gemm_i8_ring(GemmI8Kern p)
     const int a_row = (wm0 + (lane & 31)) * 64;
     const int b_row = BM * 64 + (wn0 + (lane & 31)) * 64;
 
+    // Read order fa[0], fb[*], fa[1..]: the MFMAs (i-major) can start while
+    // the later A fragments are still in flight (LDS returns in order).
     auto read_frags = [&](const int8_t* st, int cc, v4i (&fa)[FM], v4i (&fb)[FN]) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
-        }
+        fa[0] = *reinterpret_cast<const v4i*>(st + a_row + cc);
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             fb[j] = *reinterpret_cast<const v4i*>(st + b_row + j * 32 * 64 + cc);
+        }
+#pragma unroll
+        for (int i = 1; i < FM; ++i) {
+            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
         }
     };
     auto mfma_all = [&](const v4i (&fa)[FM], const v4i (&fb)[FN]) {
@@ -779,7 +819,7 @@ void gemm_i8_ring(GemmI8Kern p)
         output_pass<FM, FN, TN, EPI, PROBE>(p, acc, reinterpret_cast<int32_t*>(ring) + wave * 32 * kEpiPitch,
                                             m0 + wm0, n0 + wn0, lane);
     } else {
-        output_pass_regs<FM, FN, EPI>(p, acc, m0 + wm0, n0 + wn0, lane);
+        output_pass_regs<FM, FN, EPI, true>(p, acc, m0 + wm0, n0 + wn0, lane);
     }
 }
 
