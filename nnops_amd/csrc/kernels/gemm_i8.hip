@@ -165,7 +165,7 @@ __device__ __forceinline__ void load_chunks(v4i (&r)[C], const int8_t* const (&s
 // ---------------------------------------------------------------------------
 enum { EPI_GENERIC = 0, EPI_S8 = 1, EPI_S32 = 2 };
 
-template <int FM, int FN, int TN, int EPI, int PROBE = 0>
+template <int FM, int FN, int TN, int EPI>
 __device__ __forceinline__ void output_pass(const GemmI8Kern& p, v16i (&acc)[FM][FN], int32_t* slab,
                                             int row0, int col0, int lane)
 {
@@ -236,15 +236,7 @@ __device__ __forceinline__ void output_pass(const GemmI8Kern& p, v16i (&acc)[FM]
                     const int32_t q = (int32_t)round_half_away(x) + ep.zp_out;
                     w |= ((uint32_t)q & 0xffu) << (8 * e);
                 }
-                if constexpr (PROBE == 3) {  // timing probe: no stores
-                    if (w == 0x12345678u) {
-                        *reinterpret_cast<uint32_t*>(cptr) = w;
-                    }
-                } else if constexpr (PROBE == 4) {  // timing probe: stores, no math
-                    *reinterpret_cast<uint32_t*>(cptr) = (uint32_t)raw[0];
-                } else {
-                    *reinterpret_cast<uint32_t*>(cptr) = w;
-                }
+                *reinterpret_cast<uint32_t*>(cptr) = w;
             } else if constexpr (EPI == EPI_S32) {
                 v4i q;
 #pragma unroll
@@ -559,31 +551,103 @@ void gemm_i8_mfma(GemmI8Kern p)
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile kernel with an asynchronous LDS ring (full-K, 16-byte-aligned
-// operands). Stages are filled by global_load_lds_dwordx4: each wave
+// Large-tile kernel with an asynchronous LDS ring (K % 64 == 0, 16-byte-aligned
+// operands). Stages are filled by buffer_load_dwordx4 ... lds: each wave
 // instruction writes 1 KiB of LDS contiguously (lane l -> bytes 16l..16l+15),
 // i.e. 16 tile rows of 64 bytes, so the 16-byte chunk a lane fetches from HBM
 // is chosen to land in a swizzled slot: row r's logical chunk c lives in slot
 // c ^ ((r >> 2) & 3). A fragment read serves 16 lanes (16 consecutive rows,
-// one logical chunk) per LDS cycle; with 64 four-byte banks (256 bytes per
-// cycle) those 16 reads land on 16 distinct 16-byte bank groups, so the read
-// is conflict-free with no padding. NS stages are in flight, so each load has NS-1 k-steps of MFMA
-// work (~3K cycles at 256x256) to land before it is needed.
+// one logical chunk) per LDS cycle; with 64 four-byte banks those 16 reads land
+// on 16 distinct 16-byte bank groups, so the read is conflict-free with no
+// padding. NS stages are in flight, so each load has NS-1 k-steps of MFMA work
+// to land before it is needed. The buffer form (32-bit offsets against a
+// per-tile descriptor) costs fewer issue cycles than the 64-bit-address form.
+//
+// The MFMA takes the B fragment as its first operand, so the 32x32 accumulator
+// holds C transposed: lane l owns output row (l & 31) and, in register group g,
+// the 4 consecutive columns 8g + 4(l >> 5) + 0..3. Each lane therefore packs
+// 4 output bytes (or one 16-byte int32 group) with no cross-lane transpose.
+//
+// Output modes:
+//   RING_S8    fused requant (row-uniform s_a/s_out, per-column s_b, bias in
+//              the accumulator init, Relu folded into the integer clamp);
+//              bytes are staged per wave in LDS and written as 16-byte rows.
+//   RING_S32   fused bias + Relu, int32 written straight from the accumulators.
+//   RING_PART  raw int32 accumulators of this K split to a workspace slab;
+//              gemm_i8_reduce sums the splits and runs the full output pass.
 // ---------------------------------------------------------------------------
-#define NNOPS_GPTR(x) ((const __attribute__((address_space(1))) void*)(x))
 #define NNOPS_LPTR(x) ((__attribute__((address_space(3))) void*)(x))
 
-// s_waitcnt immediate: wait until at most n vector-memory ops are outstanding.
+// Buffer resource over [base, base + 2 GiB) with raw 32-bit offsets. The
+// buffer builtins exist only in the device pass; the host pass sees a
+// placeholder (kernels are never compiled for the host).
+#if __HIP_DEVICE_COMPILE__
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+#else
+struct BufRsrc {
+    int w[4];
+};
+#endif
+
+__device__ __forceinline__ BufRsrc buffer_rsrc(const void* base)
+{
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+#else
+    return BufRsrc{};
+#endif
+}
+
+// 16 bytes per lane from base + voff + soff into LDS at lds + 16 * lane.
+__device__ __forceinline__ void buffer_load_lds16(BufRsrc r, int8_t* lds, int voff, int soff)
+{
+#if __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+#endif
+}
+
+enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2 };
+
+struct RingSplit {
+    int splits;        // K ranges per output tile
+    int kt_per;        // 64-byte k steps per split (the last split takes the rest)
+    int32_t* part;     // RING_PART: [splits][M][N] raw accumulators
+};
+
 __device__ __forceinline__ void block_barrier()
 {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves across the barrier
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int EPI, int PROBE = 0>
+// Logical order: the hardware deals workgroups round-robin over the 8 XCDs,
+// so consecutive logical ids are gathered on one XCD. Splits are outermost (a
+// band of one XCD shares one K range of A), then tiles grouped 4 along M
+// (neighbours share B column panels in that XCD's L2).
+__device__ __forceinline__ void ring_coords(int tiles_m, int tiles_n, int& tm, int& tn, int& sp)
+{
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) {
+        bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    }
+    const int tiles = tiles_m * tiles_n;
+    sp = bid / tiles;
+    bid -= sp * tiles;
+    constexpr int G = 4;
+    const int per_group = G * tiles_n;
+    const int group = bid / per_group;
+    const int first_m = group * G;
+    const int gsize = min(tiles_m - first_m, G);
+    const int in_group = bid - group * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int MODE, bool FLIP>
 __global__ __launch_bounds__(WM * WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
-void gemm_i8_ring(GemmI8Kern p)
+void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 {
     constexpr int W = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
@@ -592,73 +656,81 @@ void gemm_i8_ring(GemmI8Kern p)
     constexpr int QB = BN / 16 / W;
     constexpr int L = QA + QB;                    // vector-memory ops per wave per stage
     constexpr int kStage = (BM + BN) * 64;
-    constexpr int kEpiPitch = TN + 4;
     static_assert(QA * W * 16 == BM && QB * W * 16 == BN, "rows per stage");
-    static_assert((EPI != EPI_GENERIC && PROBE == 0) || W * 32 * kEpiPitch * 4 <= NS * kStage,
-                  "epilogue staging fits the ring");
+    static_assert(FM * 32 == TM && FN * 32 == TN, "wave tile");
+    constexpr int kPitch8 = TN + 16;             // staged byte row pitch: 2-way bank conflicts at most
+    static_assert(W * TM * kPitch8 <= NS * kStage, "byte staging fits the ring");
     static_assert((NS - 1) * L < 64, "vmcnt range");
+    static_assert(MODE == RING_PART || !FLIP, "u8 A needs the compensating output pass");
 
     __shared__ __attribute__((aligned(1024))) int8_t ring[NS * kStage];
-    long long probe_c0 = 0, probe_r0 = 0;
-    if constexpr (PROBE == 5) {  // timing probe: shader clock vs real time
-        probe_c0 = clock64();
-        probe_r0 = (long long)__builtin_amdgcn_s_memrealtime();
-    }
 
-    int tm, tn;
-    tile_coords((p.m + BM - 1) / BM, (p.n + BN - 1) / BN, tm, tn);
+    int tm, tn, sp;
+    ring_coords(ceil_div(p.m, BM), ceil_div(p.n, BN), tm, tn, sp);
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm0 = (wave / WN) * TM, wn0 = (wave % WN) * TN;
+    const int kt0 = sp * sk.kt_per;
+    const int kt = (sp == sk.splits - 1) ? p.k / 64 - kt0 : sk.kt_per;
 
-    // This lane's source offsets for its QA + QB load instructions.
-    int64_t a_off[QA], b_off[QB];
+    // Descriptors over this tile's row panels from this split's first k; rows
+    // past M/N are clamped to the last row (computed, never stored).
+    const BufRsrc rsa = buffer_rsrc(p.a + (int64_t)m0 * p.lda + kt0 * 64);
+    const BufRsrc rsb = buffer_rsrc(p.b + (int64_t)n0 * p.ldb + kt0 * 64);
+    int a_off[QA], b_off[QB];
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
         const int r = (wave * QA + q) * 16 + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        a_off[q] = (int64_t)min(m0 + r, p.m - 1) * p.lda + c * 16;
+        a_off[q] = min(r, p.m - 1 - m0) * (int)p.lda + c * 16;
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
         const int r = (wave * QB + q) * 16 + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        b_off[q] = (int64_t)min(n0 + r, p.n - 1) * p.ldb + c * 16;
+        b_off[q] = min(r, p.n - 1 - n0) * (int)p.ldb + c * 16;
     }
     auto issue = [&](int stage_k, int slot) {
         int8_t* base = ring + slot * kStage;
 #pragma unroll
         for (int q = 0; q < QA; ++q) {
-            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(p.a + a_off[q] + stage_k),
-                                             NNOPS_LPTR(base + (wave * QA + q) * 1024), 16, 0, 0);
+            buffer_load_lds16(rsa, base + (wave * QA + q) * 1024, a_off[q], stage_k);
         }
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(p.b + b_off[q] + stage_k),
-                                             NNOPS_LPTR(base + BM * 64 + (wave * QB + q) * 1024), 16, 0, 0);
+            buffer_load_lds16(rsb, base + BM * 64 + (wave * QB + q) * 1024, b_off[q], stage_k);
         }
     };
 
-    // fast output modes: the accumulators start from this lane's column bias
+    // Accumulators (transposed layout); the fused modes start from bias[n].
     v16i acc[FM][FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        int32_t b0 = 0;
-        if constexpr (EPI != EPI_GENERIC && PROBE == 0) {
-            const int n = n0 + wn0 + j * 32 + (lane & 31);
-            b0 = p.ep.bias ? p.ep.bias[min(n, p.n - 1)] : 0;
+        int32_t b0[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i bv = v4i{0, 0, 0, 0};
+            if constexpr (MODE != RING_PART) {
+                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                if (p.ep.bias != nullptr && n < p.n) {
+                    bv = *reinterpret_cast<const v4i*>(p.ep.bias + n);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b0[4 * g + e] = bv[e];
+            }
         }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                acc[i][j][r] = b0;
+                acc[i][j][r] = b0[r];
             }
         }
     }
 
-    const int kt = p.k / 64;
     // Fragment read offsets: row (lane & 31) of each 32-row fragment, logical
     // chunk ks/16 + lane/32 in slot (chunk ^ swz), swz = ((lane & 31) >> 2) & 3.
     const int swz = ((lane & 31) >> 2) & 3;
@@ -666,51 +738,54 @@ void gemm_i8_ring(GemmI8Kern p)
     const int c1 = ((2 + (lane >> 5)) ^ swz) * 16;    // k half 1
     const int a_row = (wm0 + (lane & 31)) * 64;
     const int b_row = BM * 64 + (wn0 + (lane & 31)) * 64;
-
-    // Read order fa[0], fb[*], fa[1..]: the MFMAs (i-major) can start while
-    // the later A fragments are still in flight (LDS returns in order).
     auto read_frags = [&](const int8_t* st, int cc, v4i (&fa)[FM], v4i (&fb)[FN]) {
-        fa[0] = *reinterpret_cast<const v4i*>(st + a_row + cc);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            fb[j] = *reinterpret_cast<const v4i*>(st + b_row + j * 32 * 64 + cc);
-        }
-#pragma unroll
-        for (int i = 1; i < FM; ++i) {
-            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
-        }
-    };
-    auto mfma_all = [&](const v4i (&fa)[FM], const v4i (&fb)[FN]) {
+        fb[0] = *reinterpret_cast<const v4i*>(st + b_row + cc);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
+            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
+        }
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 1; j < FN; ++j) {
+            fb[j] = *reinterpret_cast<const v4i*>(st + b_row + j * 32 * 64 + cc);
+        }
+    };
+    auto mfma_all = [&](v4i (&fa)[FM], const v4i (&fb)[FN]) {
+        if constexpr (FLIP) {  // u8 A enters the signed MFMA as a - 128
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                fa[i] ^= v4i{(int)0x80808080u, (int)0x80808080u, (int)0x80808080u, (int)0x80808080u};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
             }
         }
     };
-    // Interleave the next fragment reads with this half's MFMAs: one
-    // ds_read_b128 after each of the first FM + FN MFMAs, so every read has at
-    // least half a phase of matrix work to land before it is needed.
-    auto schedule = [&]() {
+    // One fragment read after each of the first FM + FN MFMAs, so every read
+    // has part of a phase of matrix work to land before it is needed.
+    auto schedule = [&](bool loads) {
 #pragma unroll
-        for (int q = 0; q < FM + FN; ++q) {
+        for (int q = 0; q < FM * FN; ++q) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (q < FM + FN) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            if (loads && q >= FM * FN - L) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
     };
 
-    // Ring: stage s goes to slot s % NS; nothing is issued past the last k
-    // step, so the vmcnt waits below count only the stages really in flight.
-    auto issue_stage = [&](int s) {
-        if (s < kt) {
-            issue(s * 64, s % NS);
-        }
-    };
+    // Ring: stage s goes to slot s % NS; nothing is issued past this split's
+    // last k step, so the vmcnt waits count only the stages really in flight.
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        issue_stage(s);
+        if (s < kt) {
+            issue(s * 64, s);
+        }
     }
     if (kt >= NS) {
         wait_vmcnt<(NS - 1) * L>();   // stage 0 landed, stages 1..NS-1 may be in flight
@@ -722,65 +797,28 @@ void gemm_i8_ring(GemmI8Kern p)
     v4i f0a[FM], f0b[FN], f1a[FM], f1b[FN];
     read_frags(ring, c0, f0a, f0b);
     // One k step: half 0 of stage t on the matrix cores while half 1's
-    // fragments load; barrier (stage t+1 landed everywhere, stage t's slot free);
-    // half 1 of stage t while half 0 of stage t+1 loads and stage t+NS is
-    // issued into stage t's slot. STEADY: every stage up to t+NS-1 was issued,
-    // so exactly NS-2 stages may stay in flight.
+    // fragments load; wait for stage t+1 and for every wave's reads of stage t
+    // (the barrier), then half 1 of stage t while half 0 of stage t+1 loads and
+    // stage t+NS is issued into stage t's slot. STEADY: every stage up to
+    // t+NS-1 was issued, so exactly NS-2 stages may stay in flight.
     auto step = [&](int t, bool steady) {
         const int8_t* st = ring + (t % NS) * kStage;
-        if constexpr (PROBE != 7) {
-            read_frags(st, c1, f1a, f1b);
-        }
+        read_frags(st, c1, f1a, f1b);
         mfma_all(f0a, f0b);
-        schedule();
-        if constexpr (PROBE != 6) {  // timing probe 6: no barrier, no loads
-            if (steady) {
-                wait_vmcnt<(NS - 2) * L>();
-            } else {
-                wait_vmcnt<0>();
-            }
-            block_barrier();
+        schedule(false);
+        if (steady) {
+            wait_vmcnt<(NS - 2) * L>();
+        } else {
+            wait_vmcnt<0>();
         }
-        if constexpr (PROBE != 7) {
-            read_frags(ring + ((t + 1) % NS) * kStage, c0, f0a, f0b);
-        }
-        if constexpr (PROBE != 2 && PROBE != 6) {  // timing probe 2: no loads inside the loop
-            if (steady) {
-                issue((t + NS) * 64, t % NS);
-            }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's reads of stage t are done
+        block_barrier();
+        read_frags(ring + ((t + 1) % NS) * kStage, c0, f0a, f0b);
+        if (steady) {
+            issue((t + NS) * 64, t % NS);
         }
         mfma_all(f1a, f1b);
-        if (steady && FM * FN >= L + FM + FN) {
-            // loads first (one per MFMA), then the fragment reads, then the rest
-#pragma unroll
-            for (int q = 0; q < L; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            }
-#pragma unroll
-            for (int q = 0; q < FM + FN; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            if constexpr (FM * FN > L + FM + FN) {
-                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - L - (FM + FN), 0);
-            }
-        } else if (steady) {
-            // fewer MFMAs than loads + reads: each MFMA carries a load (while
-            // any remain) and a fragment read (while any remain)
-#pragma unroll
-            for (int q = 0; q < FM * FN; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (q < L) {
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                }
-                if (q < FM + FN) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-            }
-        } else {
-            schedule();
-        }
+        schedule(steady);
     };
     int t = 0;
     for (; t + NS < kt; ++t) {
@@ -789,37 +827,145 @@ void gemm_i8_ring(GemmI8Kern p)
     for (; t < kt; ++t) {
         step(t, false);
     }
-    __syncthreads();
+    __syncthreads();   // every wave is done with the ring before it is reused for staging
 
-    if constexpr (PROBE == 5) {
-        if (threadIdx.x == 0) {
-            long long* d = reinterpret_cast<long long*>(p.c) + 2 * blockIdx.x;
-            d[0] = clock64() - probe_c0;
-            d[1] = (long long)__builtin_amdgcn_s_memrealtime() - probe_r0;
-        }
-    }
-    if constexpr (PROBE == 1 || PROBE >= 5) {  // timing probe: no output pass (every accumulator consumed)
-        int32_t x = 0;
+    const EpiParams& ep = p.ep;
+    if constexpr (MODE == RING_S8) {
+        // Requant in the transposed layout: per lane 4 consecutive columns of
+        // one row per register group. Relu is folded into the clamp: with
+        // req >= 0 a negative v gives r <= 0 and Relu's 0 gives r = 0, so
+        // raising the low bound to 0 yields the same code; with req < 0 the high
+        // bound drops to 0 instead. The integer clamp equals nnops' float clamp
+        // before rounding (the bounds are integers and rounding is monotonic).
+        const bool relu = ep.act == NNOPS_ACT_RELU;
+        const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+        const int32_t lo_i = (u8 ? 0 : -128) - ep.zp_out;
+        const int32_t hi_i = (u8 ? 255 : 127) - ep.zp_out;
+        const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
+        int8_t* stage8 = ring + wave * (TM * kPitch8);   // this wave's [TM][TN] byte tile
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
+            for (int g = 0; g < 4; ++g) {
+                const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+                const int n = n0 + wn0 + nl;
+                v4f sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+                if (ep.s_b != nullptr && n < p.n) {
+                    sb = *reinterpret_cast<const v4f*>(ep.s_b + n);
+                }
+                float req[4];
+                int32_t lo[4], hi[4];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    x ^= acc[i][j][r];
+                for (int e = 0; e < 4; ++e) {
+                    req[e] = __fmul_rn(row_k, sb[e]);
+                    lo[e] = (relu && req[e] >= 0.0f) ? max(lo_i, 0) : lo_i;
+                    hi[e] = (relu && !(req[e] >= 0.0f)) ? min(hi_i, 0) : hi_i;
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    uint32_t q[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = __fmul_rn((float)acc[i][j][4 * g + e], req[e]);
+                        // round half away from zero: the conversion truncates as trunc() does
+                        const int32_t r = (int32_t)__fadd_rn(x, __builtin_copysignf(0.5f, x));
+                        q[e] = (uint32_t)(med3_i32(r, lo[e], hi[e]) + ep.zp_out);
+                    }
+                    const uint32_t w = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
+                                       __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
+                    *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kPitch8 + nl) = w;
                 }
             }
         }
-        if (x == 0x7fffffff) {
-            static_cast<int32_t*>(p.c)[threadIdx.x] = x;
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // 16-byte row chunks of the wave tile (host-checked: N % 16 == 0,
+        // 16-byte-aligned C and pitch)
+        constexpr int CPR = TN / 16;
+#pragma unroll
+        for (int q = 0; q < TM * CPR / 64; ++q) {
+            const int idx = q * 64 + lane, r = idx / CPR, c = idx % CPR;
+            const int m = m0 + wm0 + r, n = n0 + wn0 + c * 16;
+            const v4i v = *reinterpret_cast<const v4i*>(stage8 + r * kPitch8 + c * 16);
+            if (m < p.m && n < p.n) {
+                char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + n;
+                __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(cptr));
+            }
+        }
+    } else {
+        // int32 groups straight from the accumulators (host-checked: N % 4 == 0)
+        const int32_t floor_v = (MODE == RING_S32 && ep.act == NNOPS_ACT_RELU) ? 0 : INT32_MIN;
+        char* cbase;
+        int64_t ld;
+        if constexpr (MODE == RING_S32) {
+            cbase = static_cast<char*>(p.c);
+            ld = p.ldc_bytes;
+        } else {
+            cbase = reinterpret_cast<char*>(sk.part + (int64_t)sp * p.m * p.n);
+            ld = (int64_t)p.n * 4;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int m = m0 + wm0 + i * 32 + (lane & 31);
+            if (m >= p.m) {
+                continue;
+            }
+            char* crow = cbase + (int64_t)m * ld;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                    if (n < p.n) {
+                        v4i v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            v[e] = max(acc[i][j][4 * g + e], floor_v);
+                        }
+                        *reinterpret_cast<v4i*>(crow + (int64_t)n * 4) = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Sum of the K-split partial accumulators and the full output pass
+// (compensation, bias, Relu, requant or the float epilogue, add_to): one
+// thread per 4 consecutive columns of a row (N % 4 == 0).
+__global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk)
+{
+    const int groups = p.n / 4;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (int64_t)p.m * groups) {
+        return;
+    }
+    const int m = (int)(gid / groups);
+    const int nb = (int)(gid - (int64_t)m * groups) * 4;
+    const int64_t slab = (int64_t)p.m * p.n;
+    const int32_t* src = sk.part + (int64_t)m * p.n + nb;
+    v4i raw = *reinterpret_cast<const v4i*>(src);
+    for (int s = 1; s < sk.splits; ++s) {
+        raw += *reinterpret_cast<const v4i*>(src + s * slab);
+    }
+    const EpiParams& ep = p.ep;
+    const EpiRow row = epi_row(ep, m);
+    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+    const bool s32 = ep.out_kind == NNOPS_OUT_S32;
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    if (s32) {
+        int32_t* c32 = reinterpret_cast<int32_t*>(crow) + nb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            c32[e] = epi_value(ep, row, epi_col(ep, nb + e), raw[e], 0);
         }
         return;
     }
-    if constexpr (EPI == EPI_GENERIC || PROBE != 0) {
-        output_pass<FM, FN, TN, EPI, PROBE>(p, acc, reinterpret_cast<int32_t*>(ring) + wave * 32 * kEpiPitch,
-                                            m0 + wm0, n0 + wn0, lane);
-    } else {
-        output_pass_regs<FM, FN, EPI, true>(p, acc, m0 + wm0, n0 + wn0, lane);
+    int8_t* c8 = reinterpret_cast<int8_t*>(crow) + nb;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int32_t old = ep.add_to ? (u8 ? (int32_t)((const uint8_t*)c8)[e] : (int32_t)c8[e]) : 0;
+        c8[e] = (int8_t)epi_value(ep, row, epi_col(ep, nb + e), raw[e], old);
     }
 }
 
@@ -1011,6 +1157,124 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
 }
 
 // ---------------------------------------------------------------------------
+// Column GEMV, M <= 16, B n-contiguous ([K][N], the MatMul weight without
+// transpose_b), consumed in place. Lane l of a wave owns CPL consecutive
+// columns (CPL = 16: one 16-byte load per row; CPL = 4: one 4-byte load per
+// row), so every wave load streams 64 * CPL contiguous bytes of one row. Four
+// rows k..k+3 are transposed in registers (two v_perm per column) into one
+// dword of 4 k-bytes per column, which v_dot4 multiplies with A[m][k..k+3]
+// read through the scalar cache (A is uniform across the wave). The 8 waves of
+// a workgroup take consecutive row ranges of the same columns and are summed
+// through LDS (W = 4 when the sum buffer would exceed 64 KiB, so two
+// workgroups fit a CU); workgroups of different row ranges write raw int32 partials
+// that gemm_i8_reduce sums and passes through the output pass. Bound: HBM.
+// ---------------------------------------------------------------------------
+typedef const __attribute__((address_space(4))) int32_t* ScalarI32Ptr;
+
+struct KnSplit {
+    int chunks;       // column chunks of 64 * CPL
+    int rows;         // rows per wave (multiple of 16)
+};
+
+// 4 rows (one dword each, byte c = column c) -> 4 column dwords (byte i = row i)
+__device__ __forceinline__ void transpose4x4_bytes(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
+                                                   uint32_t (&col)[4])
+{
+    const uint32_t t0 = __builtin_amdgcn_perm(r1, r0, 0x05010400u);   // r0b0 r1b0 r0b1 r1b1
+    const uint32_t t1 = __builtin_amdgcn_perm(r3, r2, 0x05010400u);   // r2b0 r3b0 r2b1 r3b1
+    const uint32_t t2 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);   // r0b2 r1b2 r0b3 r1b3
+    const uint32_t t3 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+    col[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+    col[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+    col[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+    col[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
+template <int MT, int CPL, int W>
+__global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk, KnSplit ks)
+{
+    constexpr int D = CPL / 4;                   // dwords per lane per row
+    constexpr int U = 4;                         // k-quads per batch (16 rows in flight)
+    __shared__ int32_t red[W][MT * CPL][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int chunk = blockIdx.x % ks.chunks;
+    const int split = blockIdx.x / ks.chunks;
+    const int n = chunk * 64 * CPL + lane * CPL;
+    const bool live = n < p.n;
+    const int k0 = (split * W + wave) * ks.rows;
+    const int k1 = min(p.k, k0 + ks.rows);
+
+    int32_t acc[MT][CPL];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            acc[m][c] = 0;
+        }
+    }
+    const int8_t* bcol = p.b + (live ? n : 0);
+    for (int k = k0; k < k1; k += 4 * U) {
+        uint32_t rows[4 * U][D];
+#pragma unroll
+        for (int r = 0; r < 4 * U; ++r) {
+            const int8_t* src = bcol + (int64_t)(k + r) * p.ldb;
+            if constexpr (D == 4) {
+                const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src));
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    rows[r][d] = (uint32_t)v[d];
+                }
+            } else {
+                rows[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            int32_t aq[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int mm = m < p.m ? m : 0;
+                aq[m] = *reinterpret_cast<ScalarI32Ptr>((uintptr_t)(p.a + (int64_t)mm * p.lda + k + 4 * u));
+            }
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                uint32_t col[4];
+                transpose4x4_bytes(rows[4 * u][d], rows[4 * u + 1][d], rows[4 * u + 2][d], rows[4 * u + 3][d], col);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        acc[m][4 * d + c] = __builtin_amdgcn_sdot4(aq[m], (int)col[c], acc[m][4 * d + c], false);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            red[wave][m * CPL + c][lane] = acc[m][c];
+        }
+    }
+    __syncthreads();
+    // sum over the waves; thread t handles (element e = t / 64 .., lane t % 64)
+    int32_t* part = sk.part + (int64_t)split * p.m * p.n;
+    for (int e = threadIdx.x >> 6; e < MT * CPL; e += W) {
+        int32_t s = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            s += red[w][e][lane];
+        }
+        const int m = e / CPL, c = e % CPL;
+        if (m < p.m && live) {
+            part[(int64_t)m * p.n + n + c] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prepasses
 // ---------------------------------------------------------------------------
 // dst[c][r] = src[r][c] for r < R, c < C; dst columns r in [R, Rp) are zeroed.
@@ -1065,10 +1329,99 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 inline int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
 
-struct WsPlan {
-    size_t r_a = 0, r_b = 0, a_t = 0, b_t = 0, total = 0;
-    int64_t kp = 0;
+// Which ring-kernel configuration a call takes (all zero: another kernel).
+struct RingPlan {
+    int bm = 0, bn = 0;     // block tile
+    int splits = 0;         // K splits (1: no split)
+    int mode = -1;          // RING_S8 / RING_S32 / RING_PART
 };
+
+// Column GEMV plan ([K,N] B consumed in place, M <= 16).
+struct KnPlan {
+    int cpl = 0;            // columns per lane (0: not taken)
+    int w = 0;              // waves per workgroup
+    int chunks = 0, rows = 0, splits = 0;
+};
+
+struct WsPlan {
+    size_t r_a = 0, r_b = 0, a_t = 0, b_t = 0, part = 0, total = 0;
+    int64_t kp = 0;
+    RingPlan ring;
+    KnPlan kn;
+};
+
+// M <= 16 with a [K,N] B: 16-byte (M <= 2) or 4-byte column groups per lane,
+// K % 16 == 0, dword-aligned A rows (scalar loads), no term that needs the
+// column sums of B (u8 A, A zero points). About 512 workgroups of 8 (or 4)
+// waves, row ranges a multiple of 16.
+KnPlan plan_kn(const NnopsGemmI8Args& g)
+{
+    KnPlan r;
+    if (g.trans_b || g.trans_a || g.m > 16 || g.k % 16 != 0 || g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0) {
+        return r;
+    }
+    const int cpl = g.m <= 2 ? 16 : 4;
+    if (g.n % cpl != 0 || g.n % 4 != 0 || ((uintptr_t)g.b % cpl) != 0 || (g.ldb % cpl) != 0 ||
+        ((uintptr_t)g.a % 4) != 0 || (g.lda % 4) != 0) {
+        return r;
+    }
+    const int mt = g.m <= 1 ? 1 : g.m <= 2 ? 2 : g.m <= 4 ? 4 : g.m <= 8 ? 8 : 16;
+    r.cpl = cpl;
+    r.w = (mt * cpl >= 64) ? 4 : 8;
+    r.chunks = (int)((g.n + 64 * cpl - 1) / (64 * cpl));
+    const int ks_target = std::max(1, 512 / r.chunks);
+    r.rows = std::max<int>(16, (int)(g.k / ((int64_t)ks_target * r.w)) / 16 * 16);
+    r.splits = (int)((g.k + (int64_t)r.rows * r.w - 1) / ((int64_t)r.rows * r.w));
+    return r;
+}
+
+inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 0) && (ld % 16 == 0); }
+
+// The ring kernel needs 64-byte k steps, 16-byte-aligned k-contiguous rows,
+// N % 4 == 0 (int32 groups), and 32-bit buffer offsets within a row panel.
+// Tile shape by M: 384x128 covers a 257..384-row problem in one M tile,
+// 128x256 and 256x128 the small ones, 256x256 the rest. K is split when the
+// tiles alone do not fill the 256 CUs (at least 8 k steps per split). The
+// fused output modes need row-uniform parameters, no zero-point terms,
+// half-away rounding, 16-byte-aligned tables and destination, and no split;
+// everything else writes raw partials and runs gemm_i8_reduce.
+RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb)
+{
+    RingPlan r;
+    if (g.m <= 16 || g.k % 64 != 0 || g.n % 4 != 0 || g.m < 64 || !aligned16(a, lda) || !aligned16(b, ldb)) {
+        return r;
+    }
+    if (g.m > 256 && g.m <= 384) {
+        r.bm = 384; r.bn = 128;
+    } else if (g.m <= 128) {
+        r.bm = 128; r.bn = 256;
+    } else if (g.m <= 256) {
+        r.bm = 256; r.bn = 128;
+    } else {
+        r.bm = 256; r.bn = 256;
+    }
+    if ((int64_t)r.bm * lda >= (int64_t)INT32_MAX || (int64_t)r.bn * ldb >= (int64_t)INT32_MAX) {
+        r = RingPlan{};
+        return r;
+    }
+    const int64_t tiles = ((g.m + r.bm - 1) / r.bm) * ((g.n + r.bn - 1) / r.bn);
+    const int kt = (int)(g.k / 64);
+    r.splits = (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / 8));
+    const bool compensate = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0 || g.zp_b != nullptr ||
+                            g.zp_b_scalar != 0;
+    const bool tables16 = ((uintptr_t)g.bias % 16 == 0) && ((uintptr_t)g.s_b % 16 == 0);
+    const bool plain = !compensate && g.s_out_rows == nullptr && g.zp_out_rows == nullptr && !g.float_ep &&
+                       !g.round_even && tables16 && ((uintptr_t)g.c % 16 == 0);
+    r.mode = RING_PART;
+    if (r.splits == 1 && plain) {
+        if (g.out_kind == NNOPS_OUT_S32 && (g.ldc * 4) % 16 == 0) {
+            r.mode = RING_S32;
+        } else if (g.out_kind != NNOPS_OUT_S32 && g.s_a == nullptr && g.ldc % 16 == 0 && g.n % 16 == 0) {
+            r.mode = RING_S8;
+        }
+    }
+    return r;
+}
 
 WsPlan plan_workspace(const NnopsGemmI8Args& g)
 {
@@ -1077,17 +1430,32 @@ WsPlan plan_workspace(const NnopsGemmI8Args& g)
     w.kp = round16(g.k);
     w.r_a = off; off += align_up((size_t)g.m * 4);
     w.r_b = off; off += align_up((size_t)g.n * 4);
+    const int8_t* a = static_cast<const int8_t*>(g.a);
+    const int8_t* b = g.b;
+    int64_t lda = g.lda, ldb = g.ldb;
     if (g.trans_a) {
         w.a_t = off; off += align_up((size_t)g.m * (size_t)w.kp);
+        a = nullptr;      // staged copies are 256-byte aligned with a 16-byte pitch
+        lda = w.kp;
+    }
+    w.kn = plan_kn(g);
+    if (w.kn.cpl != 0) {
+        w.part = off; off += align_up((size_t)w.kn.splits * (size_t)g.m * (size_t)g.n * 4);
+        w.total = off;
+        return w;
     }
     if (!g.trans_b) {
         w.b_t = off; off += align_up((size_t)g.n * (size_t)w.kp);
+        b = nullptr;
+        ldb = w.kp;
+    }
+    w.ring = plan_ring(g, a, lda, b, ldb);
+    if (w.ring.mode == RING_PART) {
+        w.part = off; off += align_up((size_t)w.ring.splits * (size_t)g.m * (size_t)g.n * 4);
     }
     w.total = off;
     return w;
 }
-
-inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 0) && (ld % 16 == 0); }
 
 template <int BM, int BN, int WM, int WN, int WPE, bool FULLK, bool ALIGNED>
 void launch_gemm_epi(const GemmI8Kern& k, int epi, hipStream_t s)
@@ -1117,15 +1485,76 @@ void launch_gemm(const GemmI8Kern& k, bool aligned, bool fullk, int epi, hipStre
     }
 }
 
-void launch_ring(const GemmI8Kern& k, int epi, hipStream_t s)
+template <int BM, int BN, int WM, int WN>
+void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, hipStream_t s)
 {
-    const int tiles = ((k.m + 255) / 256) * ((k.n + 255) / 256);
-    if (epi == EPI_S8) {
-        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_S8>), dim3(tiles), dim3(512), 0, s, k);
-    } else if (epi == EPI_S32) {
-        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_S32>), dim3(tiles), dim3(512), 0, s, k);
+    const unsigned blocks = (unsigned)(((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN) * sk.splits);
+    const dim3 block(WM * WN * 64);
+    if (flip) {
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
+    } else if (mode == RING_S8) {
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
+    } else if (mode == RING_S32) {
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
     } else {
-        hipLaunchKernelGGL((gemm_i8_ring<256, 256, 2, 4, 4, EPI_GENERIC>), dim3(tiles), dim3(512), 0, s, k);
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
+    }
+}
+
+template <int MT>
+void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, int cpl, int w, hipStream_t s)
+{
+    const dim3 grid((unsigned)(ks.chunks * sk.splits));
+    if (cpl == 16) {
+        if constexpr (MT <= 2) {
+            hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 8>), grid, dim3(512), 0, s, k, sk, ks);
+        }
+    } else if (w == 4) {
+        hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
+    } else {
+        hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 8>), grid, dim3(512), 0, s, k, sk, ks);
+    }
+}
+
+void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t s)
+{
+    RingSplit sk;
+    sk.splits = r.splits;
+    sk.kt_per = 0;
+    sk.part = part;
+    KnSplit ks;
+    ks.chunks = r.chunks;
+    ks.rows = r.rows;
+    switch (k.m) {
+    case 1: launch_kn_mt<1>(k, sk, ks, r.cpl, r.w, s); break;
+    case 2: launch_kn_mt<2>(k, sk, ks, r.cpl, r.w, s); break;
+    case 3: case 4: launch_kn_mt<4>(k, sk, ks, r.cpl, r.w, s); break;
+    case 5: case 6: case 7: case 8: launch_kn_mt<8>(k, sk, ks, r.cpl, r.w, s); break;
+    default: launch_kn_mt<16>(k, sk, ks, r.cpl, r.w, s); break;
+    }
+    const int64_t groups = (int64_t)k.m * (k.n / 4);
+    hipLaunchKernelGGL(gemm_i8_reduce, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
+}
+
+void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStream_t s)
+{
+    RingSplit sk;
+    sk.splits = r.splits;
+    sk.kt_per = (k.k / 64) / r.splits;
+    sk.part = part;
+    const bool flip = k.a_xor != 0u;
+    if (r.bm == 384) {
+        launch_ring_cfg<384, 128, 4, 2>(k, sk, r.mode, flip, s);
+    } else if (r.bm == 128) {
+        launch_ring_cfg<128, 256, 2, 4>(k, sk, r.mode, flip, s);
+    } else if (r.bn == 128) {
+        launch_ring_cfg<256, 128, 4, 2>(k, sk, r.mode, flip, s);
+    } else {
+        launch_ring_cfg<256, 256, 2, 4>(k, sk, r.mode, flip, s);
+    }
+    if (r.mode == RING_PART) {
+        const int64_t groups = (int64_t)k.m * (k.n / 4);
+        hipLaunchKernelGGL(gemm_i8_reduce, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
     }
 }
 
@@ -1187,6 +1616,9 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     if (w.total > 0 && (workspace == nullptr || ws_bytes < w.total)) {
         return NNOPS_NOT_INITIALIZED;
     }
+    if ((uintptr_t)workspace % 16 != 0) {
+        return NNOPS_INVALID_ARGUMENT;   // staged operands and partials are 16-byte vectors
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
 
@@ -1210,7 +1642,10 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         k.a = static_cast<const int8_t*>(g->a);
         k.lda = g->lda;
     }
-    if (!g->trans_b) {
+    if (w.kn.cpl != 0) {
+        k.b = g->b;               // [K,N], consumed in place by the column GEMV
+        k.ldb = g->ldb;
+    } else if (!g->trans_b) {
         int8_t* bt = reinterpret_cast<int8_t*>(ws + w.b_t);
         dim3 grid((unsigned)((g->n + 63) / 64), (unsigned)((w.kp + 63) / 64));
         hipLaunchKernelGGL(transpose_i8, grid, dim3(256), 0, s, g->b, g->ldb, (int)g->k, (int)g->n, bt,
@@ -1260,7 +1695,9 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     const bool aligned = aligned16(k.a, k.lda) && aligned16(k.b, k.ldb) && (g->k % 16 == 0);
     const bool fullk = aligned && (g->k % 64 == 0);
     const int epi = choose_epi(*g, e);
-    if (g->m <= 4 && aligned) {
+    if (w.kn.cpl != 0) {
+        launch_kn(k, w.kn, reinterpret_cast<int32_t*>(ws + w.part), s);
+    } else if (g->m <= 4 && aligned) {
         constexpr int R = 1;
         const unsigned blocks = (unsigned)((g->n + 4 * R - 1) / (4 * R));
         const bool flip = k.a_xor != 0u;
@@ -1285,8 +1722,8 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         } else {
             hipLaunchKernelGGL((gemv_i8_mfma<4, false>), dim3(blocks), dim3(256), 0, s, k);
         }
-    } else if (g->m >= 1024 && g->n >= 1024 && fullk && !g->a_u8) {
-        launch_ring(k, epi, s);
+    } else if (w.ring.mode >= 0) {
+        launch_ring(k, w.ring, reinterpret_cast<int32_t*>(ws + w.part), s);
     } else if (g->m >= 1024 && g->n >= 1024) {
         launch_gemm<256, 256, 2, 2, 1>(k, aligned, fullk, epi, s);
     } else if (g->m >= 64) {

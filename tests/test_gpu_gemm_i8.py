@@ -72,6 +72,10 @@ SHAPES = [
     (1, 64, 16), (1, 4096, 1000), (3, 100, 37), (16, 512, 130), (17, 96, 65),
     (33, 208, 70), (64, 4096, 64), (100, 1000, 333), (130, 64, 1030), (300, 512, 257),
     (1024, 256, 1024), (1100, 160, 1050),
+    # ring-kernel tile shapes, K splits and the fused / partial output modes
+    (96, 512, 512), (200, 1024, 256), (333, 2048, 512), (1024, 512, 4096),
+    # column GEMV on a [K,N] B (16- and 4-column lane groups, K splits)
+    (2, 4096, 1008), (5, 256, 100), (12, 1024, 2048), (16, 512, 4096),
 ]
 
 
@@ -94,7 +98,7 @@ def test_random_shapes_s32_and_s8(M, K, N, trans_b):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("M,K,N", [(5, 77, 9), (40, 300, 33), (200, 130, 90)])
+@pytest.mark.parametrize("M,K,N", [(5, 77, 9), (40, 300, 33), (200, 130, 90), (300, 640, 256)])
 def test_u8_zero_points_trans_a_round_even(M, K, N):
     announce(f"u8/zp/trans_a {M}x{K}x{N}")
     seed = 77 + M
@@ -194,3 +198,24 @@ def test_config2_full_sampled_rows():
                               s_out=0.05, act=oracle.ACT_RELU, rows=(r0, r0 + 16))
         np.testing.assert_array_equal(got[r0:r0 + 16], want[r0:r0 + 16])
     assert len(rows) == 48
+
+
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_kn_gemv_weight_zero_point_and_tables(M):
+    """[K,N] weights consumed in place: weight zero points (row sums of A),
+    per-column scales, per-row output tables."""
+    announce(f"[K,N] GEMV zp_b M={M}")
+    K, N = 2048, 1536
+    a = dg.act_s8(90 + M, (M, K))
+    b = dg.ints(91, (K, N), -127, 127)
+    zpb = dg.ints(92, (N,), -4, 4, np.int32)
+    sb = dg.uniform(93, (N,), 0.005, 0.02)
+    so = dg.uniform(94, (M,), 0.5, 2.0)
+    bias = dg.ints(95, (N,), -5000, 5000, np.int32)
+    got = run_gpu(a, b, na.OUT_S8, trans_b=False, bias=bias, s_a=0.02, s_b=sb, zp_b=zpb, s_out_rows=so, relu=True)
+    want = oracle.gemm_i8(a, b, bias=bias, out_kind=oracle.OUT_S8, s_a=0.02, s_b=sb, zp_b=zpb,
+                          s_out_rows=so, act=oracle.ACT_RELU)
+    assert np.unique(want).size > 50
+    np.testing.assert_array_equal(got, want)
+    got = run_gpu(a, b, na.OUT_S32, trans_b=False, zp_b=zpb)
+    np.testing.assert_array_equal(got, oracle.gemm_i8(a, b, zp_b=zpb))
