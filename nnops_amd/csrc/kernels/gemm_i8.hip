@@ -931,22 +931,45 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 }
 
 // Sum of the K-split partial accumulators and the full output pass
-// (compensation, bias, Relu, requant or the float epilogue, add_to): one
-// thread per 4 consecutive columns of a row (N % 4 == 0).
+// (compensation, bias, Relu, requant or the float epilogue, add_to). TPG
+// threads share a group of 4 consecutive columns of a row (N % 4 == 0), each
+// summing every TPG-th split with its loads in flight together, then combine
+// with lane shuffles; the first of them runs the output pass. TPG = 4 suits
+// many splits of a small output, TPG = 1 a few splits of a large one.
+template <int TPG>
 __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk)
 {
     const int groups = p.n / 4;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= (int64_t)p.m * groups) {
-        return;
-    }
-    const int m = (int)(gid / groups);
-    const int nb = (int)(gid - (int64_t)m * groups) * 4;
+    const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) / TPG;
+    const int j = threadIdx.x % TPG;
+    const bool in = gid < (int64_t)p.m * groups;
+    const int m = in ? (int)(gid / groups) : 0;
+    const int nb = in ? (int)(gid - (int64_t)m * groups) * 4 : 0;
     const int64_t slab = (int64_t)p.m * p.n;
     const int32_t* src = sk.part + (int64_t)m * p.n + nb;
-    v4i raw = *reinterpret_cast<const v4i*>(src);
-    for (int s = 1; s < sk.splits; ++s) {
-        raw += *reinterpret_cast<const v4i*>(src + s * slab);
+    v4i raw = v4i{0, 0, 0, 0};
+    if (in) {
+        int s = j;
+        for (; s + 3 * TPG < sk.splits; s += 4 * TPG) {
+            const v4i x0 = *reinterpret_cast<const v4i*>(src + s * slab);
+            const v4i x1 = *reinterpret_cast<const v4i*>(src + (s + TPG) * slab);
+            const v4i x2 = *reinterpret_cast<const v4i*>(src + (s + 2 * TPG) * slab);
+            const v4i x3 = *reinterpret_cast<const v4i*>(src + (s + 3 * TPG) * slab);
+            raw += (x0 + x1) + (x2 + x3);
+        }
+        for (; s < sk.splits; s += TPG) {
+            raw += *reinterpret_cast<const v4i*>(src + s * slab);
+        }
+    }
+    if constexpr (TPG > 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            raw[e] += __shfl_xor(raw[e], 1);
+            raw[e] += __shfl_xor(raw[e], 2);
+        }
+    }
+    if (!in || j != 0) {
+        return;
     }
     const EpiParams& ep = p.ep;
     const EpiRow row = epi_row(ep, m);
@@ -1165,8 +1188,8 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
 // dword of 4 k-bytes per column, which v_dot4 multiplies with A[m][k..k+3]
 // read through the scalar cache (A is uniform across the wave). The 8 waves of
 // a workgroup take consecutive row ranges of the same columns and are summed
-// through LDS (W = 4 when the sum buffer would exceed 64 KiB, so two
-// workgroups fit a CU); workgroups of different row ranges write raw int32 partials
+// through LDS (W = 16 for 16-column groups; W = 4 when a 4-column-group sum
+// buffer would exceed 64 KiB, so two workgroups fit a CU); workgroups of different row ranges write raw int32 partials
 // that gemm_i8_reduce sums and passes through the output pass. Bound: HBM.
 // ---------------------------------------------------------------------------
 typedef const __attribute__((address_space(4))) int32_t* ScalarI32Ptr;
@@ -1343,6 +1366,8 @@ struct KnPlan {
     int chunks = 0, rows = 0, splits = 0;
 };
 
+inline int kn_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
+
 struct WsPlan {
     size_t r_a = 0, r_b = 0, a_t = 0, b_t = 0, part = 0, total = 0;
     int64_t kp = 0;
@@ -1365,12 +1390,19 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
         ((uintptr_t)g.a % 4) != 0 || (g.lda % 4) != 0) {
         return r;
     }
-    const int mt = g.m <= 1 ? 1 : g.m <= 2 ? 2 : g.m <= 4 ? 4 : g.m <= 8 ? 8 : 16;
+    const int mt = kn_mt(g.m);
     r.cpl = cpl;
-    r.w = (mt * cpl >= 64) ? 4 : 8;
     r.chunks = (int)((g.n + 64 * cpl - 1) / (64 * cpl));
-    const int ks_target = std::max(1, 512 / r.chunks);
-    r.rows = std::max<int>(16, (int)(g.k / ((int64_t)ks_target * r.w)) / 16 * 16);
+    if (cpl == 16) {
+        // 1024-column x 256-row tiles: 16 waves of 16 rows, every load a full
+        // 1 KiB row segment (the shape that streams HBM at full rate)
+        r.w = 16;
+        r.rows = 16;
+    } else {
+        r.w = (mt * cpl >= 64) ? 4 : 8;
+        const int ks_target = std::max(1, 512 / r.chunks);
+        r.rows = std::max<int>(16, (int)(g.k / ((int64_t)ks_target * r.w)) / 16 * 16);
+    }
     r.splits = (int)((g.k + (int64_t)r.rows * r.w - 1) / ((int64_t)r.rows * r.w));
     return r;
 }
@@ -1507,12 +1539,22 @@ void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, i
     const dim3 grid((unsigned)(ks.chunks * sk.splits));
     if (cpl == 16) {
         if constexpr (MT <= 2) {
-            hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 8>), grid, dim3(512), 0, s, k, sk, ks);
+            hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 16>), grid, dim3(1024), 0, s, k, sk, ks);
         }
     } else if (w == 4) {
         hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
     } else {
         hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 8>), grid, dim3(512), 0, s, k, sk, ks);
+    }
+}
+
+void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
+{
+    const int64_t groups = (int64_t)k.m * (k.n / 4);
+    if (sk.splits > 8) {
+        hipLaunchKernelGGL(gemm_i8_reduce<4>, dim3((unsigned)((groups * 4 + 255) / 256)), dim3(256), 0, s, k, sk);
+    } else {
+        hipLaunchKernelGGL(gemm_i8_reduce<1>, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
     }
 }
 
@@ -1532,8 +1574,7 @@ void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t 
     case 5: case 6: case 7: case 8: launch_kn_mt<8>(k, sk, ks, r.cpl, r.w, s); break;
     default: launch_kn_mt<16>(k, sk, ks, r.cpl, r.w, s); break;
     }
-    const int64_t groups = (int64_t)k.m * (k.n / 4);
-    hipLaunchKernelGGL(gemm_i8_reduce, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
+    launch_reduce(k, sk, s);
 }
 
 void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStream_t s)
@@ -1553,8 +1594,7 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
         launch_ring_cfg<256, 256, 2, 4>(k, sk, r.mode, flip, s);
     }
     if (r.mode == RING_PART) {
-        const int64_t groups = (int64_t)k.m * (k.n / 4);
-        hipLaunchKernelGGL(gemm_i8_reduce, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
+        launch_reduce(k, sk, s);
     }
 }
 

@@ -14,9 +14,12 @@
 //   gemv_q4_1_kn   blocks along N ([K][N/32]), small M: a lane owns one
 //                  32-column block, waves split K, partial planes summed by
 //                  reduce_q4_1. Bound: HBM.
-//   gemm_q4_1_mfma larger M, f16 A: B tiles decoded to f16 (d*q + m in f32,
-//                  rounded once) into LDS, A tiles staged k-contiguous,
+//   gemm_q4_1_ring larger M, f16 A, blocks along K, K % 64 == 0: a 5-stage
+//                  LDS ring filled by DMA (A and the raw Q4_1 bytes), B decoded
+//                  per lane into MFMA operands with packed f16 math,
 //                  v_mfma_f32_32x32x16_f16, f32 accumulate. Bound: MFMA.
+//   gemm_q4_1_mfma the other GEMM shapes: B tiles decoded to f16 (d*q + m in
+//                  f32, rounded once) into LDS, A tiles staged k-contiguous.
 #include "common.hpp"
 
 #include <utility>
@@ -942,6 +945,239 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA GEMM, f16 A, B blocks along K ([N][K/32], 2 blocks = 40 bytes per row
+// per 64-k stage), K % 64 == 0. 128 x 256 tiles, 4 waves, each 128 x 64 of
+// 32x32 fragments (v_mfma_f32_32x32x16_f16), a 3-stage LDS ring filled only
+// by buffer_load ... lds (so every wait below is an explicit vmcnt):
+//   A     128 rows x 128 bytes; 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7)
+//   Braw  256 rows x 64 bytes (the row's 40 stage bytes + 24 not used); chunk
+//         c of row r in slot c ^ ((r >> 2) & 3)
+// Both swizzles make the 16- and 4-byte fragment reads of 32 consecutive rows
+// conflict-free (A) or at most 2-way (Braw). Each lane decodes its own B
+// operand in registers: 8 nibbles of one row (a dword pair) and the block's
+// d | m dword become 8 f16 d * q + m: the byte permute with exponent byte 0x64
+// makes (1024 + q, 1024 + q'), v_pk_add_f16 removes 1024 exactly and
+// v_pk_fma_f16 rounds d * q + m once. Stage s + NS - 1 is issued at the top of
+// step s and has NS - 2 steps to land. Bound: MFMA.
+// ---------------------------------------------------------------------------
+#if __HIP_DEVICE_COMPILE__
+typedef __amdgpu_buffer_rsrc_t QBufRsrc;
+#else
+struct QBufRsrc {
+    int w[4];
+};
+#endif
+
+__device__ __forceinline__ QBufRsrc q_buffer_rsrc(const void* base, uint32_t bytes)
+{
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+#else
+    return QBufRsrc{};
+#endif
+}
+
+__device__ __forceinline__ void q_buffer_load_lds16(QBufRsrc r, uint8_t* lds, int voff, int soff)
+{
+#if __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+#endif
+}
+
+// 8 nibble values (low nibble of each byte of lo0, lo1) -> 8 f16 d * q + m
+__device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v2h m2)
+{
+    const v2h k1024 = __builtin_bit_cast(v2h, 0x64006400u);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t src = i ? lo1 : lo0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t pr = __builtin_amdgcn_perm(0x64646464u, src, h ? 0x04030402u : 0x04010400u);
+            const v2h q = __builtin_bit_cast(v2h, pr) - k1024;
+            w[2 * i + h] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, d2, m2));
+        }
+    }
+    return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+}
+
+template <bool OUT16, int NS>
+__global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
+{
+    static_assert(NS >= 3 && (NS - 2) * 8 < 64, "stages");
+    constexpr int BM = 128, BN = 256;
+    constexpr int TN = 64, FM = 4, FN = 2;
+    constexpr int kA = BM * 128, kB = BN * 64, kStage = kA + kB;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
+
+    const int tiles_m = (p.m + BM - 1) / BM;
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) {
+        bid = (bid & 7) * (nb >> 3) + (bid >> 3);     // consecutive logical tiles on one XCD
+    }
+    const int tm = bid % tiles_m, tn = bid / tiles_m; // the M tiles of a column band share B in L2
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wn0 = wave * TN;
+    const int kt = p.k / 64;
+
+    // A: rows 8 * (4 * wave + i) + lane / 8; B raw: rows 16 * (4 * wave + i) + lane / 4
+    const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
+    const int64_t b_bytes = (int64_t)(p.n - n0) * p.ldb;
+    const QBufRsrc rsb = q_buffer_rsrc(p.b + (int64_t)n0 * p.ldb,
+                                       (uint32_t)std::min<int64_t>(b_bytes, 0x7fffffff));
+    int a_off[4], b_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ra = 8 * (4 * wave + i) + (lane >> 3);
+        const int ca = (lane & 7) ^ ((ra >> 1) & 7);
+        a_off[i] = min(ra, p.m - 1 - m0) * (int)p.lda * 2 + ca * 16;
+        const int rb = 16 * (4 * wave + i) + (lane >> 2);
+        const int cb = (lane & 3) ^ ((rb >> 2) & 3);
+        b_off[i] = min(rb, p.n - 1 - n0) * (int)p.ldb + cb * 16;
+    }
+    auto issue = [&](int s) {
+        uint8_t* base = ring + (s % NS) * kStage;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q_buffer_load_lds16(rsa, base + (4 * wave + i) * 1024, a_off[i], s * 128);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q_buffer_load_lds16(rsb, base + kA + (4 * wave + i) * 1024, b_off[i], s * 40);
+        }
+    };
+
+    // this lane's fragment rows: A row (lane & 31) of fragment i; B row
+    // wn0 + 32 j + (lane & 31); k values 16 ks + 8 (lane >> 5) .. + 7
+    const int fr = lane & 31, kh = lane >> 5;
+    auto a_frag = [&](const uint8_t* st, int i, int ks) {
+        const int r = i * 32 + fr;
+        const int c = (2 * ks + kh) ^ ((r >> 1) & 7);
+        return *reinterpret_cast<const v8h*>(st + r * 128 + c * 16);
+    };
+    auto b_dword = [&](const uint8_t* row, int r, int byte) {
+        const int c = (byte >> 4) ^ ((r >> 2) & 3);
+        return *reinterpret_cast<const uint32_t*>(row + c * 16 + (byte & 15));
+    };
+    auto b_frag = [&](const uint8_t* st, int j, int ks) {
+        const int r = wn0 + 32 * j + fr;
+        const uint8_t* row = st + kA + r * 64;
+        const int blk = ks >> 1;                            // block of the stage
+        const int v0 = 16 * (ks & 1) + 8 * kh;              // first value within the block
+        const uint32_t dm = b_dword(row, r, 20 * blk);
+        const int nb0 = 20 * blk + 4 + (v0 & 15);           // first nibble byte
+        uint32_t w0 = b_dword(row, r, nb0), w1 = b_dword(row, r, nb0 + 4);
+        const int sh = v0 >= 16 ? 4 : 0;
+        w0 = (w0 >> sh) & 0x0f0f0f0fu;
+        w1 = (w1 >> sh) & 0x0f0f0f0fu;
+        const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x01000100u));
+        const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x03020302u));
+        return decode8_f16(w0, w1, d2, m2);
+    };
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            acc[i][j] = v16f{0.0f};
+        }
+    }
+
+    // prologue: stages 0..NS-2 in flight, stage 0 landed
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        if (s < kt) {
+            issue(s);
+        }
+    }
+    if (kt >= NS - 1) {
+        wait_vmcnt<(NS - 2) * 8>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+    // Within a step the fragments of slice ks+1 are read and decoded while the
+    // matrix cores run slice ks (two register sets, alternating).
+    v8h fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    auto load_frags = [&](const uint8_t* st, int ks, v8h (&fa)[FM], v8h (&fb)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            fa[i] = a_frag(st, i, ks);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            fb[j] = b_frag(st, j, ks);
+        }
+    };
+    auto mfma_slice = [&](const v8h (&fa)[FM], const v8h (&fb)[FN]) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+    for (int t = 0; t < kt; ++t) {
+        const uint8_t* st = ring + (t % NS) * kStage;
+        // stage t+NS-1 into the slot read in step t-1
+        const bool more = t + NS - 1 < kt;
+        if (more) {
+            issue(t + NS - 1);
+        }
+        load_frags(st, 0, fa0, fb0);
+        load_frags(st, 1, fa1, fb1);
+        mfma_slice(fa0, fb0);
+        load_frags(st, 2, fa0, fb0);
+        mfma_slice(fa1, fb1);
+        load_frags(st, 3, fa1, fb1);
+        mfma_slice(fa0, fb0);
+        mfma_slice(fa1, fb1);
+        // stage t+1 landed for this wave (issued NS-2 steps ago; every later
+        // stage may be in flight); the barrier makes every wave's pieces visible
+        // and frees slot t for step t+1's issue
+        if (more) {
+            wait_vmcnt<(NS - 2) * 8>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+
+    // C[m][n]: lane holds column n = (lane & 31) of fragment j, rows 8 (r / 4) + 4 (lane >> 5) + r % 4
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        if (n >= p.n) {
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.m) {
+                    if constexpr (OUT16) {
+                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)acc[i][j][r];
+                    } else {
+                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = acc[i][j][r];
+                    }
+                }
+            }
+        }
+    }
+}
+
+
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -1032,10 +1268,12 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     const bool pipe = g->k == 128 * 32 && g->ldb_bytes == 128 * 20 && ((uintptr_t)g->b & 15) == 0 &&
                                       (g->lda % 8) == 0 && ((uintptr_t)kk.a & 15) == 0;
                     if (pipe) {
+                        // 4 rows per wave: 10 KiB per wave in flight, one launch-wide wave of blocks
+                        const unsigned rb4 = (unsigned)((g->n + 15) / 16);
                         if (kk.m == 1) {
-                            hipLaunchKernelGGL((gemv_q4_1_pipe<1, R>), dim3(rb), dim3(256), 0, s, kk);
+                            hipLaunchKernelGGL((gemv_q4_1_pipe<1, 4>), dim3(rb4), dim3(256), 0, s, kk);
                         } else {
-                            hipLaunchKernelGGL((gemv_q4_1_pipe<2, R>), dim3(rb), dim3(256), 0, s, kk);
+                            hipLaunchKernelGGL((gemv_q4_1_pipe<2, 4>), dim3(rb4), dim3(256), 0, s, kk);
                         }
                     } else if (staged) {
                         if (kk.m == 1) {
@@ -1067,6 +1305,14 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 const int64_t total = (int64_t)kk.m * kk.n;
                 hipLaunchKernelGGL(reduce_q4_1, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
             }
+        }
+    } else if (g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0) {
+        // blocks along K: the ring kernel (A by DMA, B decoded in registers)
+        const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
+        if (k.out_f16) {
+            hipLaunchKernelGGL((gemm_q4_1_ring<true, 5>), dim3(tiles), dim3(256), 0, s, k);
+        } else {
+            hipLaunchKernelGGL((gemm_q4_1_ring<false, 5>), dim3(tiles), dim3(256), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

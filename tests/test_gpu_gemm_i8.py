@@ -76,6 +76,7 @@ SHAPES = [
     (96, 512, 512), (200, 1024, 256), (333, 2048, 512), (1024, 512, 4096),
     # column GEMV on a [K,N] B (16- and 4-column lane groups, K splits)
     (2, 4096, 1008), (5, 256, 100), (12, 1024, 2048), (16, 512, 4096),
+    (1, 1040, 8192), (2, 1024, 8256), (7, 512, 8192),
 ]
 
 

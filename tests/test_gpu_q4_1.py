@@ -33,6 +33,8 @@ CASES = [
     (1, 4096, 1024), (2, 4096, 512), (1, 96, 40), (1, 1000, 77), (2, 8200, 64),
     (3, 256, 130), (16, 4096, 256), (64, 512, 300), (130, 1000, 200),
     (1, 4096, 1003), (2, 4096, 77),
+    # ring GEMM (K % 64 == 0): ragged M and N tiles, a single k step
+    (300, 1024, 520), (7, 64, 256),
 ]
 
 
