@@ -610,7 +610,7 @@ enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2 };
 
 struct RingSplit {
     int splits;        // K ranges per output tile
-    int kt_per;        // 64-byte k steps per split (the last split takes the rest)
+    int kt_per;        // staged k steps per split (the last split takes the rest)
     int32_t* part;     // RING_PART: [splits][M][N] raw accumulators
 };
 
@@ -644,7 +644,7 @@ __device__ __forceinline__ void ring_coords(int tiles_m, int tiles_n, int& tm, i
     tn = in_group / gsize;
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int MODE, bool FLIP>
+template <int BM, int BN, int WM, int WN, int BK, int NS, int MODE, bool FLIP>
 __global__ __launch_bounds__(WM * WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
@@ -652,15 +652,19 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     constexpr int W = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
-    constexpr int QA = BM / 16 / W;              // 1 KiB load instructions per wave per stage (A)
-    constexpr int QB = BN / 16 / W;
+    constexpr int CPR = BK / 16;                  // 16-byte chunks per staged row
+    constexpr int RPI = 1024 / BK;                // rows per 1 KiB load instruction
+    constexpr int QA = BM / RPI / W;              // load instructions per wave per stage (A)
+    constexpr int QB = BN / RPI / W;
     constexpr int L = QA + QB;                    // vector-memory ops per wave per stage
-    constexpr int kStage = (BM + BN) * 64;
-    static_assert(QA * W * 16 == BM && QB * W * 16 == BN, "rows per stage");
+    constexpr int S = BK / 32;                    // 32-k MFMA slices per stage
+    constexpr int kStage = (BM + BN) * BK;
+    constexpr int kPitch8 = TN + 16;              // staged byte row pitch: 2-way bank conflicts at most
+    static_assert(BK == 64 || BK == 128, "stage depth");
+    static_assert(QA * W * RPI == BM && QB * W * RPI == BN, "rows per stage");
     static_assert(FM * 32 == TM && FN * 32 == TN, "wave tile");
-    constexpr int kPitch8 = TN + 16;             // staged byte row pitch: 2-way bank conflicts at most
     static_assert(W * TM * kPitch8 <= NS * kStage, "byte staging fits the ring");
-    static_assert((NS - 1) * L < 64, "vmcnt range");
+    static_assert(NS >= 2 && (NS - 1) * L < 64, "vmcnt range");
     static_assert(MODE == RING_PART || !FLIP, "u8 A needs the compensating output pass");
 
     __shared__ __attribute__((aligned(1024))) int8_t ring[NS * kStage];
@@ -672,34 +676,40 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm0 = (wave / WN) * TM, wn0 = (wave % WN) * TN;
     const int kt0 = sp * sk.kt_per;
-    const int kt = (sp == sk.splits - 1) ? p.k / 64 - kt0 : sk.kt_per;
+    const int kt = (sp == sk.splits - 1) ? p.k / BK - kt0 : sk.kt_per;
+
+    // Staged rows are BK bytes; chunk c of row r sits in slot c ^ swz(r), so
+    // the 16 rows a fragment read serves per LDS cycle hit 16 distinct 16-byte
+    // bank groups (BK = 64: 4 rows per 256 bytes, swz = (r >> 2) & 3;
+    // BK = 128: 2 rows per 256 bytes, swz = (r >> 1) & 7).
+    auto swz = [](int r) { return BK == 64 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
 
     // Descriptors over this tile's row panels from this split's first k; rows
     // past M/N are clamped to the last row (computed, never stored).
-    const BufRsrc rsa = buffer_rsrc(p.a + (int64_t)m0 * p.lda + kt0 * 64);
-    const BufRsrc rsb = buffer_rsrc(p.b + (int64_t)n0 * p.ldb + kt0 * 64);
+    const BufRsrc rsa = buffer_rsrc(p.a + (int64_t)m0 * p.lda + (int64_t)kt0 * BK);
+    const BufRsrc rsb = buffer_rsrc(p.b + (int64_t)n0 * p.ldb + (int64_t)kt0 * BK);
     int a_off[QA], b_off[QB];
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
-        const int r = (wave * QA + q) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        const int r = (wave * QA + q) * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ swz(r);
         a_off[q] = min(r, p.m - 1 - m0) * (int)p.lda + c * 16;
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
-        const int r = (wave * QB + q) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        const int r = (wave * QB + q) * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ swz(r);
         b_off[q] = min(r, p.n - 1 - n0) * (int)p.ldb + c * 16;
     }
-    auto issue = [&](int stage_k, int slot) {
-        int8_t* base = ring + slot * kStage;
+    auto issue = [&](int s) {
+        int8_t* base = ring + (s % NS) * kStage;
 #pragma unroll
         for (int q = 0; q < QA; ++q) {
-            buffer_load_lds16(rsa, base + (wave * QA + q) * 1024, a_off[q], stage_k);
+            buffer_load_lds16(rsa, base + (wave * QA + q) * 1024, a_off[q], s * BK);
         }
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            buffer_load_lds16(rsb, base + BM * 64 + (wave * QB + q) * 1024, b_off[q], stage_k);
+            buffer_load_lds16(rsb, base + BM * BK + (wave * QB + q) * 1024, b_off[q], s * BK);
         }
     };
 
@@ -731,22 +741,22 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     }
 
-    // Fragment read offsets: row (lane & 31) of each 32-row fragment, logical
-    // chunk ks/16 + lane/32 in slot (chunk ^ swz), swz = ((lane & 31) >> 2) & 3.
-    const int swz = ((lane & 31) >> 2) & 3;
-    const int c0 = ((lane >> 5) ^ swz) * 16;          // k half 0
-    const int c1 = ((2 + (lane >> 5)) ^ swz) * 16;    // k half 1
-    const int a_row = (wm0 + (lane & 31)) * 64;
-    const int b_row = BM * 64 + (wn0 + (lane & 31)) * 64;
-    auto read_frags = [&](const int8_t* st, int cc, v4i (&fa)[FM], v4i (&fb)[FN]) {
-        fb[0] = *reinterpret_cast<const v4i*>(st + b_row + cc);
+    // Fragment reads of slice ks: row (lane & 31) of each 32-row fragment,
+    // logical chunk 2 ks + (lane >> 5).
+    const int fr = lane & 31;
+    auto frag = [&](const int8_t* st, int row, int ks) {
+        const int c = (2 * ks + (lane >> 5)) ^ swz(row);
+        return *reinterpret_cast<const v4i*>(st + row * BK + c * 16);
+    };
+    auto read_frags = [&](const int8_t* st, int ks, v4i (&fa)[FM], v4i (&fb)[FN]) {
+        fb[0] = frag(st + BM * BK, wn0 + fr, ks);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            fa[i] = *reinterpret_cast<const v4i*>(st + a_row + i * 32 * 64 + cc);
+            fa[i] = frag(st, wm0 + i * 32 + fr, ks);
         }
 #pragma unroll
         for (int j = 1; j < FN; ++j) {
-            fb[j] = *reinterpret_cast<const v4i*>(st + b_row + j * 32 * 64 + cc);
+            fb[j] = frag(st + BM * BK, wn0 + j * 32 + fr, ks);
         }
     };
     auto mfma_all = [&](v4i (&fa)[FM], const v4i (&fb)[FN]) {
@@ -765,7 +775,8 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     };
     // One fragment read after each of the first FM + FN MFMAs, so every read
-    // has part of a phase of matrix work to land before it is needed.
+    // has part of a slice of matrix work to land before it is needed; with
+    // loads, they go on the last MFMAs of the slice.
     auto schedule = [&](bool loads) {
 #pragma unroll
         for (int q = 0; q < FM * FN; ++q) {
@@ -773,59 +784,67 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             if (q < FM + FN) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            if (loads && q >= FM * FN - L) {
+            if (loads && q >= FM * FN - L && q - (FM * FN - L) < L) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
         }
     };
 
     // Ring: stage s goes to slot s % NS; nothing is issued past this split's
-    // last k step, so the vmcnt waits count only the stages really in flight.
+    // last stage, so the vmcnt waits count only the stages really in flight.
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NS - 1; ++s) {
         if (s < kt) {
-            issue(s * 64, s);
+            issue(s);
         }
     }
-    if (kt >= NS) {
-        wait_vmcnt<(NS - 1) * L>();   // stage 0 landed, stages 1..NS-1 may be in flight
+    if (kt >= NS - 1) {
+        wait_vmcnt<(NS - 2) * L>();   // stage 0 landed, stages 1..NS-2 may be in flight
     } else {
         wait_vmcnt<0>();
     }
     block_barrier();
 
     v4i f0a[FM], f0b[FN], f1a[FM], f1b[FN];
-    read_frags(ring, c0, f0a, f0b);
-    // One k step: half 0 of stage t on the matrix cores while half 1's
-    // fragments load; wait for stage t+1 and for every wave's reads of stage t
-    // (the barrier), then half 1 of stage t while half 0 of stage t+1 loads and
-    // stage t+NS is issued into stage t's slot. STEADY: every stage up to
-    // t+NS-1 was issued, so exactly NS-2 stages may stay in flight.
-    auto step = [&](int t, bool steady) {
+    read_frags(ring, 0, f0a, f0b);
+    // One stage: stage t+NS-1 is issued into the slot read in step t-1 (freed
+    // by that step's barrier); slice ks runs on the matrix cores while slice
+    // ks+1's fragments load; after the last slice, wait for stage t+1 (its
+    // later stages may stay in flight) and for every wave's reads of stage t
+    // (lgkmcnt, then the barrier), then read slice 0 of stage t+1.
+    auto step = [&](int t) {
         const int8_t* st = ring + (t % NS) * kStage;
-        read_frags(st, c1, f1a, f1b);
-        mfma_all(f0a, f0b);
-        schedule(false);
-        if (steady) {
-            wait_vmcnt<(NS - 2) * L>();
-        } else {
-            wait_vmcnt<0>();
+        const bool more = t + NS - 1 < kt;
+        if (more) {
+            issue(t + NS - 1);
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's reads of stage t are done
-        block_barrier();
-        read_frags(ring + ((t + 1) % NS) * kStage, c0, f0a, f0b);
-        if (steady) {
-            issue((t + NS) * 64, t % NS);
+#pragma unroll
+        for (int ks = 0; ks < S; ++ks) {
+            v4i (&ca)[FM] = (ks & 1) ? f1a : f0a;
+            v4i (&cb)[FN] = (ks & 1) ? f1b : f0b;
+            v4i (&na)[FM] = (ks & 1) ? f0a : f1a;
+            v4i (&nb)[FN] = (ks & 1) ? f0b : f1b;
+            if (ks + 1 < S) {
+                read_frags(st, ks + 1, na, nb);
+                mfma_all(ca, cb);
+                schedule(false);
+            } else {
+                mfma_all(ca, cb);
+                if (more) {
+                    wait_vmcnt<(NS - 2) * L>();
+                } else {
+                    wait_vmcnt<0>();
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's reads of stage t are done
+                block_barrier();
+                if (t + 1 < kt) {
+                    read_frags(ring + ((t + 1) % NS) * kStage, 0, na, nb);
+                }
+            }
         }
-        mfma_all(f1a, f1b);
-        schedule(steady);
     };
-    int t = 0;
-    for (; t + NS < kt; ++t) {
-        step(t, true);
-    }
-    for (; t < kt; ++t) {
-        step(t, false);
+    for (int t = 0; t < kt; ++t) {
+        step(t);
     }
     __syncthreads();   // every wave is done with the ring before it is reused for staging
 
@@ -1355,6 +1374,7 @@ inline int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
 // Which ring-kernel configuration a call takes (all zero: another kernel).
 struct RingPlan {
     int bm = 0, bn = 0;     // block tile
+    int bk = 64;            // k bytes per staged row (128 when K allows)
     int splits = 0;         // K splits (1: no split)
     int mode = -1;          // RING_S8 / RING_S32 / RING_PART
 };
@@ -1437,8 +1457,10 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
         return r;
     }
     const int64_t tiles = ((g.m + r.bm - 1) / r.bm) * ((g.n + r.bn - 1) / r.bn);
-    const int kt = (int)(g.k / 64);
-    r.splits = (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / 8));
+    r.bk = (g.k % 128 == 0) ? 128 : 64;
+    const int kt = (int)(g.k / r.bk);
+    // at least 512 k per split
+    r.splits = (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / (512 / r.bk)));
     const bool compensate = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0 || g.zp_b != nullptr ||
                             g.zp_b_scalar != 0;
     const bool tables16 = ((uintptr_t)g.bias % 16 == 0) && ((uintptr_t)g.s_b % 16 == 0);
@@ -1517,19 +1539,32 @@ void launch_gemm(const GemmI8Kern& k, bool aligned, bool fullk, int epi, hipStre
     }
 }
 
-template <int BM, int BN, int WM, int WN>
-void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, hipStream_t s)
+template <int BM, int BN, int WM, int WN, int BK, int NS>
+void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, hipStream_t s)
 {
     const unsigned blocks = (unsigned)(((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN) * sk.splits);
     const dim3 block(WM * WN * 64);
     if (flip) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S8) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S32) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
     } else {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, 4, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
+    }
+}
+
+// 128-byte staged rows (whole cache lines: twice the bytes per L2 request of
+// 64-byte rows, which is what limits a CU's load rate) in 2 slots when K
+// allows, else 64-byte rows in 4 slots.
+template <int BM, int BN, int WM, int WN>
+void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode, bool flip, hipStream_t s)
+{
+    if (bk == 128) {
+        launch_ring_bk<BM, BN, WM, WN, 128, 2>(k, sk, mode, flip, s);
+    } else {
+        launch_ring_bk<BM, BN, WM, WN, 64, 4>(k, sk, mode, flip, s);
     }
 }
 
@@ -1581,17 +1616,17 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
 {
     RingSplit sk;
     sk.splits = r.splits;
-    sk.kt_per = (k.k / 64) / r.splits;
+    sk.kt_per = (k.k / r.bk) / r.splits;
     sk.part = part;
     const bool flip = k.a_xor != 0u;
     if (r.bm == 384) {
-        launch_ring_cfg<384, 128, 4, 2>(k, sk, r.mode, flip, s);
+        launch_ring_cfg<384, 128, 4, 2>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bm == 128) {
-        launch_ring_cfg<128, 256, 2, 4>(k, sk, r.mode, flip, s);
+        launch_ring_cfg<128, 256, 2, 4>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bn == 128) {
-        launch_ring_cfg<256, 128, 4, 2>(k, sk, r.mode, flip, s);
+        launch_ring_cfg<256, 128, 4, 2>(k, sk, r.bk, r.mode, flip, s);
     } else {
-        launch_ring_cfg<256, 256, 2, 4>(k, sk, r.mode, flip, s);
+        launch_ring_cfg<256, 256, 2, 4>(k, sk, r.bk, r.mode, flip, s);
     }
     if (r.mode == RING_PART) {
         launch_reduce(k, sk, s);
