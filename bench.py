@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy"])
+    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy", "ceilings"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -137,7 +137,8 @@ def run_cfg2(args, torch, dg, na, stream):
                    "weight_layout": "[N,K]"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": tops / PEAK_INT8_TOPS, "traffic": measured_traffic("gemm_i8_ring_cfg2"),
-                     "kernel": "gemm_i8_ring<256,256,2,4,4,EPI_S8>", "algorithmic_ops_per_launch": ops},
+                     "kernel": "gemm_i8_ring<256,256,2,4,BK=128,NS=2,RING_S8>", "algorithmic_ops_per_launch": ops,
+                     "algorithmic_bytes_per_launch": float(M * K + N * K + M * N + N * 8)},
         "dtype": "int8 (s32 accumulate)",
     }
 
@@ -231,6 +232,48 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
     tops = ops / (t["mean_ms"] * 1e-3) / 1e12
     return {"tops": tops, "frac_int8_mfma": tops / PEAK_INT8_TOPS, "us": t["mean_ms"] * 1e3,
             "M": M, "K": K, "N": N, "a_pitch": 14400, "c_pitch": 4160, "weight_layout": "[N,K]"}
+
+
+def ceilings(torch, na, stream):
+    """What this MI355X sustains outside our kernels: dense int8 MFMA fed
+    from registers (random and constant operands: the power budget lowers the
+    clock with the operands' switching), non-temporal streaming reads of 45 MiB
+    and 180 MiB rotated over 8 buffers (the cfg3/cfg4 GEMV sizes; the fixed
+    per-launch cost is the difference of the two), and an empty launch, each
+    timed as a HIP graph of back-to-back launches like the workloads."""
+    lib = na.lib()
+    s = stream.cuda_stream
+    out = torch.zeros(2048 * 256, dtype=torch.int32, device="cuda")
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (2048 * 256 * 24,), dtype=torch.int32, device="cuda")
+    res = {}
+    for constant in (0, 1):
+        blocks, iters = 2048, 2000
+        t = Timer(stream).time(lambda: lib.nnops_hip_diag_mfma_i8(src.data_ptr(), out.data_ptr(), blocks, iters,
+                                                                  constant, s), 10, 3)
+        ops = blocks * 4 * iters * 8 * 65536.0
+        res["mfma_i8_tops_" + ("constant" if constant else "random")] = ops / (t["mean_ms"] * 1e-3) / 1e12
+    for mib in (45, 180):
+        nbuf = 8
+        bufs = [torch.randint(0, 100, (mib * 2 ** 20,), dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+        it = [0]
+
+        def rd():
+            b = bufs[it[0] % nbuf]
+            it[0] += 1
+            lib.nnops_hip_diag_stream_read(b.data_ptr(), b.numel(), out.data_ptr(), 1024, s)
+
+        t = Timer(stream).time(rd, 40, 8)
+        res[f"stream_read_{mib}MiB_us"] = t["mean_ms"] * 1e3
+        res[f"stream_read_{mib}MiB_gbs"] = mib * 2 ** 20 / (t["mean_ms"] * 1e-3) / 1e9
+        del bufs
+    t = Timer(stream).time(lambda: lib.nnops_hip_diag_empty(out.data_ptr(), s), 100, 10)
+    res["empty_launch_us"] = t["mean_ms"] * 1e3
+    # two-point fit: t(bytes) = fixed + bytes / rate
+    t45, t180 = res["stream_read_45MiB_us"], res["stream_read_180MiB_us"]
+    rate = (180 - 45) * 2 ** 20 / ((t180 - t45) * 1e-6)
+    res["stream_asymptotic_gbs"] = rate / 1e9
+    res["stream_fixed_us"] = t45 - 45 * 2 ** 20 / rate * 1e6
+    return res
 
 
 def measured_traffic(kernel_key):
@@ -327,6 +370,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"workload": "copy", "bytes_per_copy": 2 ** 28, "copies": 3}))
         return
+    if args.workload == "ceilings":
+        print(json.dumps({"workload": "ceilings", **ceilings(torch, na, stream)}))
+        return
     if args.workload != "cfg2":
         res = {"cfg1": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=128, K=1024, N=1024,
                                             nbuf=1),
@@ -343,6 +389,8 @@ def main():
         secondary["cfg3_int8_gemv_m1_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, trans_b=False)
         secondary["cfg3_int8_gemv_m16_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
                                                           trans_b=True)
+        secondary["cfg3_int8_gemv_m16_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
+                                                          trans_b=False)
         secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup)
         secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
                                                          args.warmup)

@@ -86,6 +86,9 @@ SIGNATURES = {
     "nnops_hip_gemm_q4_1_workspace_size": (C.c_size_t, [C.POINTER(GemmQ41Args)]),
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
+    "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "nnops_hip_diag_stream_read": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
+    "nnops_hip_diag_empty": (C.c_int, [C.c_void_p, C.c_void_p]),
     "nnops_matmul_attrs_init": (None, [C.POINTER(MatMulAttrs)]),
     "nnops_linear_attrs_init": (None, [C.POINTER(LinearAttrs)]),
     "nnops_matmul_create": (C.c_void_p, [C.POINTER(MatMulAttrs), C.c_int32]),

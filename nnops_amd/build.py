@@ -24,6 +24,7 @@ LIB = os.path.join(PKG, "libnnops_amd.so")
 SOURCES = [
     "csrc/kernels/gemm_i8.hip",
     "csrc/kernels/q4_1.hip",
+    "csrc/kernels/diag.hip",
     "csrc/host/ops.cpp",
     "csrc/host/capi_ops.cpp",
 ]
