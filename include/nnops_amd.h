@@ -44,7 +44,7 @@ enum {
 
 /* Destination element types (nnops' s32/s8/u8 integer destinations,
  * MatMulAttributes::output_dtype, include/nnops/ops/matmul.hpp:53-60; f32/f16
- * for the Q4_1 route). */
+ * for the Q4_1 route and the int8 route's dequantizing destinations). */
 enum {
     NNOPS_OUT_S32 = 0,
     NNOPS_OUT_S8 = 1,
@@ -53,13 +53,22 @@ enum {
     NNOPS_OUT_F16 = 4,
 };
 
-/* Activations the output pass applies (a subset of EpilogueActivateType,
- * include/nnops/core/epilogue.hpp:22-33; the integer route of nnops honours
- * only Relu, matmul_tile_impl.h:411). */
+/* Activations the output pass applies: EpilogueActivateType's values
+ * (include/nnops/core/epilogue.hpp:25-36). The requantizing integer pass of
+ * nnops honours only Relu (matmul_tile_impl.h:411); the float epilogue of an
+ * s8/u8 destination takes None/Relu/Gelu; the dequantizing f32/f16
+ * destinations take all of them. */
 enum {
     NNOPS_ACT_NONE = 0,
     NNOPS_ACT_RELU = 1,
     NNOPS_ACT_GELU = 2,
+    NNOPS_ACT_SIGMOID = 3,
+    NNOPS_ACT_TANH = 4,
+    NNOPS_ACT_LEAKY_RELU = 5,
+    NNOPS_ACT_SILU = 6,
+    NNOPS_ACT_HARDSWISH = 7,
+    NNOPS_ACT_ELU = 8,
+    NNOPS_ACT_RELU6 = 9,
 };
 
 /* Integer GEMM  C[M,N] = epilogue(A[M,K] x B[K,N]).
@@ -84,7 +93,13 @@ enum {
  *   y = act(clamp(f [+ r if residual_pre])) [+ r otherwise];
  *   q = sat(round(clamp(y / s_out, lo - zp, hi - zp)) + zp)
  * which is how an s8 add_to residual and a GELU on an integer destination are
- * defined here (nnops rejects both: linear.cpp:226). */
+ * defined here (nnops rejects both: linear.cpp:226).
+ *
+ * f32/f16 destinations (nnops' dequantizing route, DqRoute, matmul_i8.cpp:
+ * 161-211; tests/reference/matmul_dq_ref.cpp:178-190):
+ *   f = float(v) * (s_a * s_b) [+ bias_fp[n]] [+ C_old if add_to];
+ *   y = act(clamp(f, min_clip, max_clip)), stored as f32 or f16 (nearest even);
+ * `bias` must be NULL there (the fp bias is `bias_fp`, in C's type). */
 typedef struct NnopsGemmI8Args {
     const void* a;
     const int8_t* b;
@@ -100,8 +115,10 @@ typedef struct NnopsGemmI8Args {
     int32_t act;                /* NNOPS_ACT_* (integer route: NONE or RELU) */
     int32_t round_even;
     int32_t float_ep;
-    float min_clip, max_clip;   /* float epilogue only */
-    int32_t add_to, residual_pre; /* float epilogue only */
+    float min_clip, max_clip;   /* float epilogue and f32/f16 destinations */
+    int32_t add_to, residual_pre; /* float epilogue and f32/f16 destinations */
+    const void* bias_fp;        /* [N] f32 or f16 (C's type), f32/f16 destinations only */
+    float act_alpha, act_beta;  /* LeakyRelu / Elu alpha, HardSwish beta */
 } NnopsGemmI8Args;
 
 size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* args);
@@ -132,6 +149,42 @@ typedef struct NnopsGemmQ41Args {
 size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* args);
 int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* args, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* QuantizeLinear / DequantizeLinear over a rows x cols view (row strides in
+ * elements), and the activation quantization of the fp-activation int8 MatMul.
+ * Replaces nnops' quantize_linear_impl / dequantize_linear_impl
+ * (src/backend/cpu/quant_linear.cpp:77-331) and quantize_activation in
+ * matmul_dq (src/backend/cpu/matmul/matmul_i8.cpp:400-446).
+ *
+ * Parameter of flat element i = r * cols + c: entry (i / inner) % dim of
+ * `scale` (f32) / `zero_point` (s8, u8 or s32 per zp_kind); dim <= 1 uses
+ * entry 0 (NULL tables: the scalars). PerTensor: dim = 1; PerToken:
+ * inner = cols, dim = rows; PerChannel(axis): inner = prod(shape[axis+1:]),
+ * dim = shape[axis] (include/nnops/ops/quant_linear.hpp resolve rules).
+ *   quantize    x f32/f16 -> y s8/u8:  clamp(rint(fma(x, 1/s, zp))), ties even;
+ *               NaN / |v| >= 2^31 -> qmin (the x86 integer indefinite);
+ *   dequantize  x s8/u8 -> y f32/f16:  fma(q, s, -zp*s) on each segment's whole
+ *               16-element blocks, (q - zp) * s on its last segment % 16
+ *               elements, as nnops' vector body and scalar tail
+ *               (src/backend/cpu/x86_64/quant.hpp:298-340); `segment` is the
+ *               reference's row: numel, cols or inner for the three modes. */
+typedef struct NnopsQdqArgs {
+    const void* x;
+    void* y;
+    int64_t rows, cols;
+    int64_t ld_x, ld_y;         /* elements */
+    int32_t x_kind, y_kind;     /* NNOPS_OUT_F32 / F16 / S8 / U8 */
+    int32_t zp_kind;            /* NNOPS_OUT_S8 / U8 / S32: zero_point's element type */
+    const float* scale;
+    const void* zero_point;
+    float scale_scalar;
+    int32_t zp_scalar;
+    int64_t inner, dim;
+    int64_t segment;            /* dequantize only */
+} NnopsQdqArgs;
+
+int nnops_hip_quantize_linear(const NnopsQdqArgs* args, void* stream);
+int nnops_hip_dequantize_linear(const NnopsQdqArgs* args, void* stream);
 
 /* Library version and build target, for the caller's diagnostics. */
 const char* nnops_hip_build_info(void);

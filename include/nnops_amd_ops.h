@@ -1,4 +1,5 @@
-/* nnops_amd_ops.h -- C ABI over the MatMul / Linear front end.
+/* nnops_amd_ops.h -- C ABI over the MatMul / Linear / QuantizeLinear /
+ * DequantizeLinear front end.
  *
  * For callers that cannot bind C++ (ctypes, cgo, JNI, N-API): each call maps
  * one-to-one onto the C++ operator contract of nnops
@@ -61,6 +62,9 @@ typedef struct NnopsMatMulAttrs {
     NnopsEpilogue epilogue;
     int32_t requant_round_even;  /* extension */
     int32_t float_epilogue;      /* extension */
+    /* storage of the fp-activation quantization (NNOPS_S8 / NNOPS_U8),
+       MatMulAttributes::act_quant_dtype (include/nnops/ops/matmul.hpp:62-64) */
+    int32_t act_quant_dtype;
 } NnopsMatMulAttrs;
 
 typedef struct NnopsLinearAttrs {
@@ -72,6 +76,12 @@ typedef struct NnopsLinearAttrs {
     int32_t float_epilogue;      /* extension */
 } NnopsLinearAttrs;
 
+/* nnops::QuantLinearAttributes (include/nnops/ops/quant_linear.hpp:26-35) */
+typedef struct NnopsQuantLinearAttrs {
+    int64_t axis;           /* -1 per token; >= 0 per channel (one scale: per tensor) */
+    int32_t output_dtype;   /* quantize: NNOPS_S8 / NNOPS_U8; dequantize: NNOPS_F32 / NNOPS_F16 */
+} NnopsQuantLinearAttrs;
+
 typedef struct NnopsOp NnopsOp;
 
 /* Attribute defaults matching the C++ structs (epilogue clip +-inf etc.). */
@@ -80,6 +90,11 @@ void nnops_linear_attrs_init(NnopsLinearAttrs* attrs);
 
 NnopsOp* nnops_matmul_create(const NnopsMatMulAttrs* attrs, int32_t backend);
 NnopsOp* nnops_linear_create(const NnopsLinearAttrs* attrs, int32_t backend);
+/* QuantizeLinear / DequantizeLinear (include/nnops/ops/quant_linear.hpp:47-140):
+ * inputs x, scale (f32, device), zero point (s8/u8, device, scale's size). */
+void nnops_quant_linear_attrs_init(NnopsQuantLinearAttrs* attrs);
+NnopsOp* nnops_quantize_linear_create(const NnopsQuantLinearAttrs* attrs, int32_t backend);
+NnopsOp* nnops_dequantize_linear_create(const NnopsQuantLinearAttrs* attrs, int32_t backend);
 void nnops_op_destroy(NnopsOp* op);
 
 /* Fills out_desc (dims, rank, dtype; data NULL). Returns 0 on success. */

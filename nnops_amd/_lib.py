@@ -8,13 +8,14 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnnops_am
 
 OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_INITIALIZED, OUT_OF_MEMORY, INTERNAL = range(6)
 OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16 = range(5)
-ACT_NONE, ACT_RELU, ACT_GELU = range(3)
+(ACT_NONE, ACT_RELU, ACT_GELU, ACT_SIGMOID, ACT_TANH, ACT_LEAKY_RELU, ACT_SILU, ACT_HARDSWISH, ACT_ELU,
+ ACT_RELU6) = range(10)
 DT_F32, DT_F16, DT_BF16, DT_S8, DT_U8, DT_S32 = 0, 1, 2, 3, 4, 5
 DT_Q4_1 = 11
 BACKEND_CPU, BACKEND_CUDA, BACKEND_HIP = 0, 1, 4
 # EpilogueActivateType / EpilogueQuantType values
 EP_NONE, EP_RELU, EP_GELU, EP_SIGMOID, EP_TANH = 0, 1, 2, 3, 4
-EP_RELU6 = 9
+EP_LEAKY_RELU, EP_SILU, EP_HARDSWISH, EP_ELU, EP_RELU6 = 5, 6, 7, 8, 9
 EQ_NONE, EQ_REQUANTIZE, EQ_DEQUANTIZE = 0, 1, 2
 
 
@@ -30,6 +31,17 @@ class GemmI8Args(C.Structure):
         ("out_kind", C.c_int32), ("act", C.c_int32), ("round_even", C.c_int32),
         ("float_ep", C.c_int32), ("min_clip", C.c_float), ("max_clip", C.c_float),
         ("add_to", C.c_int32), ("residual_pre", C.c_int32),
+        ("bias_fp", C.c_void_p), ("act_alpha", C.c_float), ("act_beta", C.c_float),
+    ]
+
+
+class QdqArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("y", C.c_void_p),
+        ("rows", C.c_int64), ("cols", C.c_int64), ("ld_x", C.c_int64), ("ld_y", C.c_int64),
+        ("x_kind", C.c_int32), ("y_kind", C.c_int32), ("zp_kind", C.c_int32),
+        ("scale", C.c_void_p), ("zero_point", C.c_void_p), ("scale_scalar", C.c_float),
+        ("zp_scalar", C.c_int32), ("inner", C.c_int64), ("dim", C.c_int64), ("segment", C.c_int64),
     ]
 
 
@@ -67,7 +79,12 @@ class MatMulAttrs(C.Structure):
         ("residual_pre_activation", C.c_int32), ("output_dtype", C.c_int32),
         ("epilogue", Epilogue),
         ("requant_round_even", C.c_int32), ("float_epilogue", C.c_int32),
+        ("act_quant_dtype", C.c_int32),
     ]
+
+
+class QuantLinearAttrs(C.Structure):
+    _fields_ = [("axis", C.c_int64), ("output_dtype", C.c_int32)]
 
 
 class LinearAttrs(C.Structure):
@@ -89,10 +106,15 @@ SIGNATURES = {
     "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "nnops_hip_diag_stream_read": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
     "nnops_hip_diag_empty": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "nnops_hip_quantize_linear": (C.c_int, [C.POINTER(QdqArgs), C.c_void_p]),
+    "nnops_hip_dequantize_linear": (C.c_int, [C.POINTER(QdqArgs), C.c_void_p]),
     "nnops_matmul_attrs_init": (None, [C.POINTER(MatMulAttrs)]),
     "nnops_linear_attrs_init": (None, [C.POINTER(LinearAttrs)]),
     "nnops_matmul_create": (C.c_void_p, [C.POINTER(MatMulAttrs), C.c_int32]),
     "nnops_linear_create": (C.c_void_p, [C.POINTER(LinearAttrs), C.c_int32]),
+    "nnops_quant_linear_attrs_init": (None, [C.POINTER(QuantLinearAttrs)]),
+    "nnops_quantize_linear_create": (C.c_void_p, [C.POINTER(QuantLinearAttrs), C.c_int32]),
+    "nnops_dequantize_linear_create": (C.c_void_p, [C.POINTER(QuantLinearAttrs), C.c_int32]),
     "nnops_op_destroy": (None, [C.c_void_p]),
     "nnops_op_output_desc": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.c_int32, C.POINTER(Tensor)]),
     "nnops_op_validate": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.c_int32, C.POINTER(Tensor), C.c_int32]),

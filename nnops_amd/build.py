@@ -1,6 +1,7 @@
 """Build libnnops_amd.so (HIP kernels for gfx950 + the C++ front end) in-tree.
 
     python -m nnops_amd.build        # or nnops_amd.build.build()
+    python -m nnops_amd.build --incremental   # only what changed
 
 Each translation unit is compiled by hipcc for --offload-arch=gfx950 only,
 objects go to nnops_amd/_build/, the shared library to nnops_amd/. Kernel TUs
@@ -25,7 +26,9 @@ SOURCES = [
     "csrc/kernels/gemm_i8.hip",
     "csrc/kernels/q4_1.hip",
     "csrc/kernels/diag.hip",
+    "csrc/kernels/quant.hip",
     "csrc/host/ops.cpp",
+    "csrc/host/quant_linear.cpp",
     "csrc/host/capi_ops.cpp",
 ]
 
@@ -65,11 +68,33 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link the shared library; returns its path."""
+def _headers_mtime() -> float:
+    t = 0.0
+    for d in (os.path.join(ROOT, "include"), os.path.join(PKG, "include"), os.path.join(PKG, "csrc")):
+        for root, _, files in os.walk(d):
+            for f in files:
+                if f.endswith((".h", ".hpp")):
+                    t = max(t, os.path.getmtime(os.path.join(root, f)))
+    return t
+
+
+def _stale(src: str, hdr: float) -> bool:
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if not os.path.exists(obj):
+        return True
+    return os.path.getmtime(obj) < max(hdr, os.path.getmtime(os.path.join(PKG, src)))
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile the sources and link the shared library; returns its path.
+    Every source is compiled unless ``incremental`` (then only those older
+    than their source or any header)."""
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    hdr = _headers_mtime()
+    todo = [s for s in SOURCES if not incremental or _stale(s, hdr)]
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(todo)))) as ex:
+        list(ex.map(_compile, todo))
+    objs = [os.path.join(BUILD, os.path.basename(s) + ".o") for s in SOURCES]
     tmp = LIB + ".tmp"
     cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -82,4 +107,4 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose="-q" not in sys.argv)
+    build(verbose="-q" not in sys.argv, incremental="--incremental" in sys.argv)

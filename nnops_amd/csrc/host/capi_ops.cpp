@@ -2,6 +2,7 @@
 // NnopsTensor records into TensorDesc / TensorView and forwards each call.
 #include "nnops/ops/linear.hpp"
 #include "nnops/ops/matmul.hpp"
+#include "nnops/ops/quant_linear.hpp"
 #include "nnops_amd_ops.h"
 
 #include <limits>
@@ -83,6 +84,7 @@ void nnops_matmul_attrs_init(NnopsMatMulAttrs* a)
     a->alpha = 1.0f;
     a->beta = 0.0f;
     a->output_dtype = static_cast<int32_t>(DataType::s32);
+    a->act_quant_dtype = static_cast<int32_t>(DataType::s8);
     init_epilogue(a->epilogue);
 }
 
@@ -109,6 +111,7 @@ NnopsOp* nnops_matmul_create(const NnopsMatMulAttrs* a, int32_t backend)
         attrs.epilogue = to_epilogue(a->epilogue);
         attrs.requant_round_even = a->requant_round_even != 0;
         attrs.float_epilogue = a->float_epilogue != 0;
+        attrs.act_quant_dtype = static_cast<DataType>(a->act_quant_dtype);
     }
     auto* h = new NnopsOp;
     h->op = MatMul::create(attrs, static_cast<Backend>(backend));
@@ -129,6 +132,45 @@ NnopsOp* nnops_linear_create(const NnopsLinearAttrs* a, int32_t backend)
     }
     auto* h = new NnopsOp;
     h->op = Linear::create(attrs, static_cast<Backend>(backend));
+    return h;
+}
+
+void nnops_quant_linear_attrs_init(NnopsQuantLinearAttrs* a)
+{
+    if (a == nullptr) {
+        return;
+    }
+    a->axis = -1;
+    a->output_dtype = static_cast<int32_t>(DataType::s8);
+}
+
+namespace {
+QuantLinearAttributes to_qlinear(const NnopsQuantLinearAttrs* a)
+{
+    QuantLinearAttributes attrs;
+    if (a != nullptr) {
+        attrs.axis = a->axis;
+        attrs.output_dtype = static_cast<DataType>(a->output_dtype);
+    }
+    return attrs;
+}
+}  // namespace
+
+NnopsOp* nnops_quantize_linear_create(const NnopsQuantLinearAttrs* a, int32_t backend)
+{
+    auto* h = new NnopsOp;
+    h->op = QuantizeLinear::create(to_qlinear(a), static_cast<Backend>(backend));
+    return h;
+}
+
+NnopsOp* nnops_dequantize_linear_create(const NnopsQuantLinearAttrs* a, int32_t backend)
+{
+    QuantLinearAttributes attrs = to_qlinear(a);
+    if (a == nullptr) {
+        attrs.output_dtype = DataType::f32;
+    }
+    auto* h = new NnopsOp;
+    h->op = DequantizeLinear::create(attrs, static_cast<Backend>(backend));
     return h;
 }
 

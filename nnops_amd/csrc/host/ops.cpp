@@ -137,11 +137,13 @@ struct Stager {
     }
 };
 
-/// Staging bytes a call may need: per-row (A scale/zp, output scale/zp) and
-/// per-column (B scale/zp) tables.
-size_t staging_bytes(int64_t m, int64_t n)
+/// Staging bytes a call may need: A's per-token scale / zero point (one entry
+/// per global row of A, `a_rows`), the epilogue's per-row output table (`m`)
+/// and B's per-column tables (`n`).
+size_t staging_bytes(int64_t a_rows, int64_t m, int64_t n)
 {
-    return 4 * align_up(static_cast<size_t>(m) * 4) + 2 * align_up(static_cast<size_t>(n) * 4);
+    return 2 * align_up(static_cast<size_t>(a_rows) * 4) + 2 * align_up(static_cast<size_t>(m) * 4) +
+           2 * align_up(static_cast<size_t>(n) * 4);
 }
 
 /// Read a scalar that may sit in host or device memory; device memory is not
@@ -185,6 +187,30 @@ int32_t out_kind_of(DataType dt)
     }
 }
 
+/// Matrices of A (the product of its own batch dims, before broadcasting).
+int64_t a_matrices(const Geometry& g)
+{
+    int64_t c = 1;
+    for (int64_t i = 0; i < g.nd; ++i) {
+        c *= g.a_batch[i];
+    }
+    return c;
+}
+
+/// Entries a per-token A table must hold: nnops indexes it by A's global row,
+/// row_base + m with row_base = (A's batch offset) / (A's row stride), on the
+/// dequantizing routes (src/backend/cpu/matmul/matmul_tile_impl.h:455-462).
+int64_t a_table_rows(const Geometry& g)
+{
+    const int64_t rows_per = g.trans_a ? g.k : g.m;
+    return (a_matrices(g) - 1) * rows_per + g.m;
+}
+
+bool is_fp_quant_pair(DataType a, DataType b)
+{
+    return (a == DataType::f32 || a == DataType::f16) && b == DataType::s8;
+}
+
 NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, const QuantCall& q, int32_t out_kind)
 {
     NnopsGemmI8Args x{};
@@ -215,6 +241,29 @@ NnopsGemmQ41Args q41_args_from_geometry(const Geometry& g, const QuantCall& q, i
     return x;
 }
 
+/// Workspace of the int8 GEMM call: staging for host-side tables, then the
+/// GEMM's own partial-sum / split-K region.
+size_t i8_workspace(const Geometry& g, const QuantCall& q, int32_t out_kind)
+{
+    // The kernel plan (and so its region) depends on what a descriptor does not
+    // carry: zero points, tables, pointer alignment. Size for the largest: the
+    // plan of plain operands (the [K,N] column GEMV's partials) and the plan
+    // with zero points (a staged B^T plus K-split partials).
+    NnopsGemmI8Args x = i8_args_from_geometry(g, q, out_kind);
+    size_t need = nnops_hip_gemm_i8_workspace_size(&x);
+    x.zp_a_scalar = 1;
+    need = std::max(need, nnops_hip_gemm_i8_workspace_size(&x));
+    return staging_bytes(a_table_rows(g), g.m, g.n) + align_up(need);
+}
+
+/// The fp-activation route's own prefix: A's staged scale / zero-point tables
+/// and the quantized copy A_q (compact, one byte per element).
+size_t fp_quant_prefix(const Geometry& g)
+{
+    const int64_t rows = a_matrices(g) * g.m;
+    return 2 * align_up(static_cast<size_t>(rows) * 4) + align_up(static_cast<size_t>(rows * g.k));
+}
+
 size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDesc* out,
                        const QuantCall& q, DataType out_dtype)
 {
@@ -223,8 +272,13 @@ size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDes
         return 0;
     }
     if (is_int8_matmul(a.dtype, b.dtype)) {
-        const NnopsGemmI8Args x = i8_args_from_geometry(g, q, out_kind_of(out_dtype));
-        return staging_bytes(g.m, g.n) + align_up(nnops_hip_gemm_i8_workspace_size(&x));
+        return i8_workspace(g, q, out_kind_of(out_dtype));
+    }
+    if (is_fp_quant_pair(a.dtype, b.dtype)) {
+        if (g.trans_a) {
+            return 0;
+        }
+        return fp_quant_prefix(g) + i8_workspace(g, q, out_kind_of(a.dtype));
     }
     if (is_q4_1_matmul(a.dtype, b.dtype)) {
         const DataType odt = out != nullptr ? out->dtype : a.dtype;
@@ -256,52 +310,52 @@ int64_t batch_offset(int64_t bi, const Geometry& g, const int64_t* dims, int64_t
     return off;
 }
 
-Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView> inputs,
-                 const ComputeContext& ctx, void* workspace, size_t ws_bytes)
+int32_t act_code(EpilogueActivateType t)
 {
-    const TensorView& a = inputs[0];
-    const TensorView& b = inputs[1];
-    const TensorView* bias = inputs.size() > 2 ? &inputs[2] : nullptr;
-    Geometry g;
-    if (Status s = matmul_geometry(a.desc(), b.desc(), q.trans_a, q.trans_b, g); !is_ok(s)) {
-        return s;
-    }
-    // The destination must be [..., M, N] with the broadcast batch.
-    if (out.rank() < 2 || out.shape(out.rank() - 2) != g.m || out.shape(out.rank() - 1) != g.n ||
-        out.numel() != g.batch * g.m * g.n) {
-        return Status::invalid_argument;
-    }
-    if (g.m == 0 || g.n == 0 || g.batch == 0) {
-        return Status::ok;
-    }
-    hipStream_t stream = static_cast<hipStream_t>(ctx.hip_stream);
-    const int64_t a_rows_per = g.trans_a ? g.k : g.m;
-    const int64_t b_rows_per = g.trans_b ? g.n : g.k;
+    return static_cast<int32_t>(t);  // NNOPS_ACT_* share nnops' numbering
+}
 
-    if (is_int8_matmul(a.data_type(), b.data_type())) {
-        const int32_t ok = out_kind_of(out.data_type());
-        if (ok != NNOPS_OUT_S32 && ok != NNOPS_OUT_S8 && ok != NNOPS_OUT_U8) {
-            return Status::unsupported;  // dequantizing destinations: not on this backend
-        }
-        if (bias != nullptr && (bias->data_type() != DataType::s32 || bias->numel() != g.n)) {
+/// The int8 GEMM over s8/u8 A (an fp activation arrives here already
+/// quantized), every destination: s32, s8/u8 requantized, f32/f16 dequantized
+/// (src/backend/cpu/matmul/matmul_i8.cpp:470-494). `ws` is i8_workspace()
+/// bytes: the staging tables first, then the GEMM's region.
+Status run_i8(const QuantCall& q, const Geometry& g, TensorView& out, const TensorView& a,
+              const TensorView& b, const TensorView* bias, hipStream_t stream, void* workspace,
+              size_t ws_bytes)
+{
+    const int32_t ok = out_kind_of(out.data_type());
+    if (ok < 0) {
+        return Status::unsupported;
+    }
+    const bool fp_out = ok == NNOPS_OUT_F32 || ok == NNOPS_OUT_F16;
+    if (bias != nullptr) {
+        const DataType want = fp_out ? out.data_type() : DataType::s32;
+        if (bias->data_type() != want || bias->numel() < g.n) {
             return Status::invalid_argument;
         }
-        const bool float_ep = q.float_ep || q.add_to;
-        if (q.add_to && ok == NNOPS_OUT_S32) {
-            return Status::unsupported;
-        }
-        NnopsGemmI8Args x = i8_args_from_geometry(g, q, ok);
-        x.a_u8 = a.data_type() == DataType::u8;
-        x.lda = a.row_stride_elems();
-        x.ldb = b.row_stride_elems();
-        x.ldc = out.row_stride_elems();
+    }
+    if (q.add_to && ok == NNOPS_OUT_S32) {
+        return Status::unsupported;
+    }
+    NnopsGemmI8Args x = i8_args_from_geometry(g, q, ok);
+    x.a_u8 = a.data_type() == DataType::u8;
+    x.lda = a.row_stride_elems();
+    x.ldb = b.row_stride_elems();
+    x.ldc = out.row_stride_elems();
+    x.add_to = q.add_to;
+    x.residual_pre = q.residual_pre;
+    x.min_clip = q.ep.min_clip;
+    x.max_clip = q.ep.max_clip;
+    x.act_alpha = q.ep.alpha;
+    x.act_beta = q.ep.beta;
+    if (fp_out) {
+        // dequantize -> bias -> [residual] -> clip -> activation, any activation
+        x.bias_fp = bias != nullptr ? bias->ptr<const void>() : nullptr;
+        x.act = act_code(q.ep.type);
+    } else {
         x.bias = bias != nullptr ? bias->ptr<const int32_t>() : nullptr;
         x.round_even = q.round_even;
-        x.float_ep = float_ep && ok != NNOPS_OUT_S32;
-        x.add_to = q.add_to;
-        x.residual_pre = q.residual_pre;
-        x.min_clip = q.ep.min_clip;
-        x.max_clip = q.ep.max_clip;
+        x.float_ep = (q.float_ep || q.add_to) && ok != NNOPS_OUT_S32;
         switch (q.ep.type) {
         case EpilogueActivateType::None: x.act = NNOPS_ACT_NONE; break;
         case EpilogueActivateType::Relu: x.act = NNOPS_ACT_RELU; break;
@@ -319,22 +373,27 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             x.min_clip = -std::numeric_limits<float>::infinity();
             x.max_clip = std::numeric_limits<float>::infinity();
         }
+    }
 
-        Stager st;
-        st.base = static_cast<char*>(workspace);
-        st.cap = workspace != nullptr ? std::min(ws_bytes, staging_bytes(g.m, g.n)) : 0;
-        st.stream = stream;
-        const QuantParams& qa = a.quant_params();
-        const QuantParams& qb = b.quant_params();
-        const QuantParams& qc = out.quant_params();
-        x.s_a = st.stage(qa.scale_data, g.m);
-        x.s_a_scalar = qa.scale;
-        x.zp_a = st.stage(qa.zero_point_data, g.m);
-        x.zp_a_scalar = qa.zero_point;
-        x.s_b = st.stage(qb.scale_data, g.n);
-        x.s_b_scalar = qb.scale;
-        x.zp_b = st.stage(qb.zero_point_data, g.n);
-        x.zp_b_scalar = qb.zero_point;
+    const int64_t a_rows = a_table_rows(g);
+    const size_t stage_cap = staging_bytes(a_rows, g.m, g.n);
+    Stager st;
+    st.base = static_cast<char*>(workspace);
+    st.cap = workspace != nullptr ? std::min(ws_bytes, stage_cap) : 0;
+    st.stream = stream;
+    const QuantParams& qa = a.quant_params();
+    const QuantParams& qb = b.quant_params();
+    const QuantParams& qc = out.quant_params();
+    // the dequantizing routes index A's per-token tables by global row
+    x.s_a = st.stage(qa.scale_data, fp_out ? a_rows : g.m);
+    x.s_a_scalar = qa.scale;
+    x.zp_a = st.stage(qa.zero_point_data, fp_out ? a_rows : g.m);
+    x.zp_a_scalar = qa.zero_point;
+    x.s_b = st.stage(qb.scale_data, g.n);
+    x.s_b_scalar = qb.scale;
+    x.zp_b = st.stage(qb.zero_point_data, g.n);
+    x.zp_b_scalar = qb.zero_point;
+    if (!fp_out) {
         x.s_out = qc.scale;
         x.zp_out = qc.zero_point;
         if (qc.scale_data != nullptr && !host_scalar(qc.scale_data, x.s_out)) {
@@ -360,30 +419,141 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
                 }
             }
         }
-        if (!st.ok) {
-            return Status::not_initialized;
-        }
-        const size_t stage_cap = staging_bytes(g.m, g.n);
-        const size_t need = nnops_hip_gemm_i8_workspace_size(&x);
-        if (need > 0 && (workspace == nullptr || ws_bytes < stage_cap + need)) {
-            return Status::not_initialized;
-        }
-        void* ws = need > 0 ? static_cast<char*>(workspace) + stage_cap : nullptr;
+    }
+    if (!st.ok) {
+        return Status::not_initialized;
+    }
+    const size_t need = nnops_hip_gemm_i8_workspace_size(&x);
+    if (need > 0 && (workspace == nullptr || ws_bytes < stage_cap + need)) {
+        return Status::not_initialized;
+    }
+    void* ws = need > 0 ? static_cast<char*>(workspace) + stage_cap : nullptr;
 
-        const int64_t a_mat = a_rows_per * a.pitch();
-        const int64_t b_mat = b_rows_per * b.pitch();
-        const int64_t c_mat = g.m * out.pitch();
-        for (int64_t bi = 0; bi < g.batch; ++bi) {
-            NnopsGemmI8Args xb = x;
-            xb.a = a.ptr<const char>() + batch_offset(bi, g, g.a_batch, a_mat);
-            xb.b = reinterpret_cast<const int8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
-            xb.c = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
-            const int rc = nnops_hip_gemm_i8(&xb, ws, need, stream);
-            if (rc != NNOPS_OK) {
-                return from_code(rc);
-            }
+    const int64_t a_rows_per = g.trans_a ? g.k : g.m;
+    const int64_t b_rows_per = g.trans_b ? g.n : g.k;
+    const int64_t a_mat = a_rows_per * a.pitch();
+    const int64_t b_mat = b_rows_per * b.pitch();
+    const int64_t c_mat = g.m * out.pitch();
+    for (int64_t bi = 0; bi < g.batch; ++bi) {
+        NnopsGemmI8Args xb = x;
+        const int64_t a_off = batch_offset(bi, g, g.a_batch, a_mat);
+        xb.a = a.ptr<const char>() + a_off;
+        xb.b = reinterpret_cast<const int8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
+        xb.c = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
+        if (fp_out && a.pitch() > 0) {
+            const int64_t row_base = a_off / a.pitch();
+            xb.s_a = x.s_a != nullptr ? x.s_a + row_base : nullptr;
+            xb.zp_a = x.zp_a != nullptr ? x.zp_a + row_base : nullptr;
         }
+        const int rc = nnops_hip_gemm_i8(&xb, ws, need, stream);
+        if (rc != NNOPS_OK) {
+            return from_code(rc);
+        }
+    }
+    return Status::ok;
+}
+
+/// fp activations with offline per-tensor / per-token QuantParams x s8
+/// weights: QuantizeLinear A into A_q (A's own parameters, ties to even), then
+/// the int8 GEMM dequantizing into A's dtype
+/// (src/backend/cpu/matmul/matmul_i8.cpp:334-463).
+Status run_fp_quant(const QuantCall& q, const Geometry& g, DataType act_dtype, TensorView& out,
+                    const TensorView& a, const TensorView& b, const TensorView* bias,
+                    hipStream_t stream, void* workspace, size_t ws_bytes)
+{
+    const QuantParams& qa = a.quant_params();
+    const bool quantized = qa.is_active() && (qa.granularity == QuantGranularity::PerTensor ||
+                                              qa.granularity == QuantGranularity::PerToken);
+    if (!quantized) {
+        return Status::invalid_argument;
+    }
+    if (g.trans_a) {
+        return Status::unsupported;
+    }
+    if (act_dtype != DataType::s8 && act_dtype != DataType::u8) {
+        return Status::invalid_argument;
+    }
+    if (out.data_type() != a.data_type()) {
+        return Status::invalid_argument;
+    }
+    const int64_t rows = a_matrices(g) * g.m;
+    const size_t prefix = fp_quant_prefix(g);
+    if (workspace == nullptr || ws_bytes < prefix) {
+        return Status::not_initialized;
+    }
+    Stager st;
+    st.base = static_cast<char*>(workspace);
+    st.cap = 2 * align_up(static_cast<size_t>(rows) * 4);
+    st.stream = stream;
+    const float* s_tab = st.stage(qa.scale_data, rows);
+    const int32_t* z_tab = st.stage(qa.zero_point_data, rows);
+    if (!st.ok) {
+        return Status::not_initialized;
+    }
+    void* aq = static_cast<char*>(workspace) + st.cap;
+
+    NnopsQdqArgs qd{};
+    qd.x = a.ptr<const void>();
+    qd.y = aq;
+    qd.rows = rows;
+    qd.cols = g.k;
+    qd.ld_x = a.row_stride_elems();
+    qd.ld_y = g.k;
+    qd.x_kind = out_kind_of(a.data_type());
+    qd.y_kind = act_dtype == DataType::u8 ? NNOPS_OUT_U8 : NNOPS_OUT_S8;
+    qd.zp_kind = NNOPS_OUT_S32;
+    qd.scale = s_tab;
+    qd.zero_point = z_tab;
+    qd.scale_scalar = qa.scale;
+    qd.zp_scalar = qa.zero_point;
+    qd.inner = g.k;
+    qd.dim = (s_tab != nullptr || z_tab != nullptr) ? rows : 1;
+    qd.segment = g.k;
+    if (const int rc = nnops_hip_quantize_linear(&qd, stream); rc != NNOPS_OK) {
+        return from_code(rc);
+    }
+
+    // A_q: A's shape, compact, A's (now device-resident) parameters
+    QuantParams qq = qa;
+    qq.scale_data = s_tab;
+    qq.zero_point_data = z_tab;
+    std::array<int64_t, TensorDesc::kMaxRank> shape{};
+    for (int64_t i = 0; i < a.rank(); ++i) {
+        shape[static_cast<size_t>(i)] = a.shape(i);
+    }
+    const TensorView av(std::span<const int64_t>(shape.data(), static_cast<size_t>(a.rank())), act_dtype,
+                        aq, g.k, TensorLayout::Dense, qq);
+    return run_i8(q, g, out, av, b, bias, stream, static_cast<char*>(workspace) + prefix, ws_bytes - prefix);
+}
+
+Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView> inputs,
+                 const ComputeContext& ctx, void* workspace, size_t ws_bytes,
+                 DataType act_dtype = DataType::s8)
+{
+    const TensorView& a = inputs[0];
+    const TensorView& b = inputs[1];
+    const TensorView* bias = inputs.size() > 2 ? &inputs[2] : nullptr;
+    Geometry g;
+    if (Status s = matmul_geometry(a.desc(), b.desc(), q.trans_a, q.trans_b, g); !is_ok(s)) {
+        return s;
+    }
+    // The destination must be [..., M, N] with the broadcast batch.
+    if (out.rank() < 2 || out.shape(out.rank() - 2) != g.m || out.shape(out.rank() - 1) != g.n ||
+        out.numel() != g.batch * g.m * g.n) {
+        return Status::invalid_argument;
+    }
+    if (g.m == 0 || g.n == 0 || g.batch == 0) {
         return Status::ok;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(ctx.hip_stream);
+    const int64_t a_rows_per = g.trans_a ? g.k : g.m;
+    const int64_t b_rows_per = g.trans_b ? g.n : g.k;
+
+    if (is_int8_matmul(a.data_type(), b.data_type())) {
+        return run_i8(q, g, out, a, b, bias, stream, workspace, ws_bytes);
+    }
+    if (is_fp_quant_pair(a.data_type(), b.data_type())) {
+        return run_fp_quant(q, g, act_dtype, out, a, b, bias, stream, workspace, ws_bytes);
     }
 
     if (is_q4_1_matmul(a.data_type(), b.data_type())) {
@@ -530,7 +700,8 @@ Status MatMul::compute(std::span<TensorView> outputs, std::span<const TensorView
     q.float_ep = attrs_.float_epilogue;
     const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),
                                        std::span<const TensorDesc>(&desc_out, 1));
-    return run_quant(q, outputs[0], inputs, ctx, workspace, workspace != nullptr ? ws : 0);
+    return run_quant(q, outputs[0], inputs, ctx, workspace, workspace != nullptr ? ws : 0,
+                     attrs_.act_quant_dtype);
 }
 
 // ===========================================================================
@@ -646,6 +817,9 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
     const TensorView& x = inputs[0];
     const TensorView& wv = inputs[1];
     TensorView& y = outputs[0];
+    if (!is_int8_matmul(x.data_type(), wv.data_type()) && !is_q4_1_matmul(x.data_type(), wv.data_type())) {
+        return Status::unsupported;  // nnops' Linear has no fp-activation x s8 route
+    }
     if (y.data_type() != linear_out_dtype(attrs_, x.data_type(), wv.data_type()) &&
         !(is_q4_1_matmul(x.data_type(), wv.data_type()) && y.data_type() == DataType::f32)) {
         return Status::invalid_argument;
@@ -669,7 +843,9 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
     q.trans_b = true;
     q.ep = attrs_.epilogue;
     q.add_to = attrs_.add_to;
-    q.residual_pre = attrs_.add_to && attrs_.residual_pre_activation;
+    // the pre-activation order folds into the GEMM, and an identity epilogue
+    // folds either way (src/backend/cpu/matmul/linear.cpp:276-282)
+    q.residual_pre = attrs_.add_to && (attrs_.residual_pre_activation || !epilogue_is_active(attrs_.epilogue));
     q.round_even = attrs_.requant_round_even;
     q.float_ep = attrs_.float_epilogue;
     const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),

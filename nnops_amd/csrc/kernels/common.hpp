@@ -54,7 +54,14 @@ struct EpiParams {
     float min_clip, max_clip;
     int32_t add_to, residual_pre;
     int32_t compensate;        // any of r_a / r_b is live
+    const void* bias_fp;       // [N] bias in the f32/f16 destination's type, or nullptr
+    float act_alpha, act_beta; // LeakyRelu / Elu alpha, HardSwish beta
 };
+
+__host__ __device__ __forceinline__ bool epi_is_fp(const EpiParams& p)
+{
+    return p.out_kind == NNOPS_OUT_F32 || p.out_kind == NNOPS_OUT_F16;
+}
 
 // Per-row constants of the output pass.
 struct EpiRow {
@@ -169,6 +176,76 @@ __device__ __forceinline__ float apply_act(const EpiParams& p, float x)
     return x;
 }
 
+// nnops' activation set on the dequantized value, after the clip
+// (apply_epilogue, simd_epilogue.hpp:56-90); exp and tanh are the device
+// library's.
+__device__ __forceinline__ float apply_act_fp(const EpiParams& p, float x)
+{
+    x = x < p.min_clip ? p.min_clip : x;
+    x = p.max_clip < x ? p.max_clip : x;
+    switch (p.act) {
+    case NNOPS_ACT_RELU:
+        return x > 0.0f ? x : 0.0f;
+    case NNOPS_ACT_RELU6: {
+        const float y = x > 0.0f ? x : 0.0f;
+        return y < 6.0f ? y : 6.0f;
+    }
+    case NNOPS_ACT_LEAKY_RELU:
+        return x > 0.0f ? x : __fmul_rn(p.act_alpha, x);
+    case NNOPS_ACT_SIGMOID:
+        return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
+    case NNOPS_ACT_TANH:
+        return tanhf(x);
+    case NNOPS_ACT_GELU: {
+        const float c = 0.7978845608028654f;
+        const float x3 = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
+        return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(__fmul_rn(c, __fadd_rn(x, x3)))));
+    }
+    case NNOPS_ACT_SILU:
+        return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));
+    case NNOPS_ACT_HARDSWISH: {
+        float r6 = __fadd_rn(x, 3.0f);
+        r6 = r6 > 0.0f ? r6 : 0.0f;
+        r6 = r6 < 6.0f ? r6 : 6.0f;
+        return __fmul_rn(__fmul_rn(x, r6), __fdiv_rn(p.act_beta, 6.0f));
+    }
+    case NNOPS_ACT_ELU:
+        return x > 0.0f ? x : __fmul_rn(p.act_alpha, __fsub_rn(expf(x), 1.0f));
+    default:
+        return x;
+    }
+}
+
+// The dequantizing output pass (nnops' DqRoute, dq_epilogue_row,
+// simd_epilogue.hpp:784-949, and tests/reference/matmul_dq_ref.cpp:178-190):
+// f = float(v) * (s_a * s_b) [+ bias[n]], then the residual, clip and activation.
+__device__ __forceinline__ float epi_value_fp(const EpiParams& p, const EpiRow& r, int n, int32_t raw,
+                                              float old)
+{
+    const EpiCol col = epi_col(p, n);
+    const int32_t v = epi_compensate(p, r, col, raw);
+    float f = __fmul_rn((float)v, __fmul_rn(r.s_a, col.s_b));
+    if (p.bias_fp != nullptr) {
+        const float b = p.out_kind == NNOPS_OUT_F16 ? (float)static_cast<const _Float16*>(p.bias_fp)[n]
+                                                    : static_cast<const float*>(p.bias_fp)[n];
+        f = __fadd_rn(f, b);
+    }
+    // a pre-activation residual joins before the clip; a post-activation one
+    // is added to the destination-typed result (nnops' Linear: a compact
+    // temporary, then residual_add, src/backend/cpu/matmul/linear.cpp:283-301)
+    if (p.add_to && p.residual_pre) {
+        f = __fadd_rn(f, old);
+    }
+    f = apply_act_fp(p, f);
+    if (p.add_to && !p.residual_pre) {
+        if (p.out_kind == NNOPS_OUT_F16) {
+            f = (float)(_Float16)f;
+        }
+        f = __fadd_rn(f, old);
+    }
+    return f;
+}
+
 // The output pass for one element: raw int32 accumulate in, the value to store
 // out (int32 for s32, the s8/u8 code otherwise). `old` is the destination's
 // current value, read only when add_to.
@@ -215,6 +292,16 @@ __device__ __forceinline__ int32_t epi_load_old(const EpiParams& p, const void* 
 __device__ __forceinline__ void epi_store(const EpiParams& p, const EpiRow& r, const EpiCol& col,
                                           int32_t raw, void* crow, int n)
 {
+    if (p.out_kind == NNOPS_OUT_F32) {
+        float* c = static_cast<float*>(crow) + n;
+        *c = epi_value_fp(p, r, n, raw, p.add_to ? *c : 0.0f);
+        return;
+    }
+    if (p.out_kind == NNOPS_OUT_F16) {
+        _Float16* c = static_cast<_Float16*>(crow) + n;
+        *c = (_Float16)epi_value_fp(p, r, n, raw, p.add_to ? (float)*c : 0.0f);
+        return;
+    }
     const int32_t q = epi_value(p, r, col, raw, epi_load_old(p, crow, n));
     if (p.out_kind == NNOPS_OUT_S32) {
         static_cast<int32_t*>(crow)[n] = q;

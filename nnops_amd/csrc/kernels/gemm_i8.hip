@@ -194,7 +194,7 @@ __device__ __forceinline__ void output_pass(const GemmI8Kern& p, v16i (&acc)[FM]
     const bool relu = ep.act == NNOPS_ACT_RELU;
     const bool u8 = ep.out_kind == NNOPS_OUT_U8;
     const bool s32 = ep.out_kind == NNOPS_OUT_S32;
-    const bool packed = (nb + 3 < p.n) && (((uintptr_t)p.c & 15) == 0) &&
+    const bool packed = !epi_is_fp(ep) && (nb + 3 < p.n) && (((uintptr_t)p.c & 15) == 0) &&
                         (s32 ? (p.ldc_bytes % 16 == 0) : (p.ldc_bytes % 4 == 0));
     // Fast modes (host-checked: N % 4 == 0, 16-byte-aligned C, pitch multiple
     // of the packed store, half-away rounding): branch-free per element.
@@ -993,6 +993,13 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     const EpiParams& ep = p.ep;
     const EpiRow row = epi_row(ep, m);
     char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+    if (epi_is_fp(ep)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            epi_store(ep, row, epi_col(ep, nb + e), raw[e], crow, nb + e);
+        }
+        return;
+    }
     const bool s32 = ep.out_kind == NNOPS_OUT_S32;
     const bool u8 = ep.out_kind == NNOPS_OUT_U8;
     if (s32) {
@@ -1464,8 +1471,9 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     const bool compensate = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0 || g.zp_b != nullptr ||
                             g.zp_b_scalar != 0;
     const bool tables16 = ((uintptr_t)g.bias % 16 == 0) && ((uintptr_t)g.s_b % 16 == 0);
+    const bool fp_out = g.out_kind == NNOPS_OUT_F32 || g.out_kind == NNOPS_OUT_F16;
     const bool plain = !compensate && g.s_out_rows == nullptr && g.zp_out_rows == nullptr && !g.float_ep &&
-                       !g.round_even && tables16 && ((uintptr_t)g.c % 16 == 0);
+                       !g.round_even && !fp_out && tables16 && ((uintptr_t)g.c % 16 == 0);
     r.mode = RING_PART;
     if (r.splits == 1 && plain) {
         if (g.out_kind == NNOPS_OUT_S32 && (g.ldc * 4) % 16 == 0) {
@@ -1639,7 +1647,7 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
 int choose_epi(const NnopsGemmI8Args& g, const EpiParams& e)
 {
     if (e.compensate || g.s_out_rows != nullptr || g.zp_out_rows != nullptr || g.float_ep ||
-        g.round_even || (g.n % 4) != 0 || ((uintptr_t)g.c & 15) != 0) {
+        g.round_even || (g.n % 4) != 0 || ((uintptr_t)g.c & 15) != 0 || epi_is_fp(e)) {
         return EPI_GENERIC;
     }
     if (g.out_kind == NNOPS_OUT_S32) {
@@ -1672,11 +1680,19 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     if (g->a == nullptr || g->b == nullptr || g->c == nullptr) {
         return NNOPS_INVALID_ARGUMENT;
     }
-    if (g->out_kind != NNOPS_OUT_S32 && g->out_kind != NNOPS_OUT_S8 && g->out_kind != NNOPS_OUT_U8) {
+    const bool fp_out = g->out_kind == NNOPS_OUT_F32 || g->out_kind == NNOPS_OUT_F16;
+    if (g->out_kind != NNOPS_OUT_S32 && g->out_kind != NNOPS_OUT_S8 && g->out_kind != NNOPS_OUT_U8 && !fp_out) {
         return NNOPS_UNSUPPORTED;
     }
     if (g->float_ep && g->out_kind == NNOPS_OUT_S32) {
         return NNOPS_UNSUPPORTED;
+    }
+    if (g->act < NNOPS_ACT_NONE || g->act > NNOPS_ACT_RELU6 ||
+        (!fp_out && g->act != NNOPS_ACT_NONE && g->act != NNOPS_ACT_RELU && g->act != NNOPS_ACT_GELU)) {
+        return NNOPS_UNSUPPORTED;
+    }
+    if ((fp_out && g->bias != nullptr) || (!fp_out && g->bias_fp != nullptr)) {
+        return NNOPS_INVALID_ARGUMENT;   // an f32/f16 destination takes its bias in its own type
     }
     // int32 accumulate: |sum| <= K * 128 * 255 must stay below 2^31.
     if (g->k > 65535 || g->m > INT32_MAX || g->n > INT32_MAX) {
@@ -1750,6 +1766,13 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     e.max_clip = g->max_clip;
     e.add_to = g->add_to;
     e.residual_pre = g->residual_pre;
+    e.bias_fp = fp_out ? g->bias_fp : nullptr;
+    e.act_alpha = g->act_alpha;
+    e.act_beta = g->act_beta;
+    if (fp_out) {
+        e.float_ep = 0;
+        e.round_even = 0;
+    }
     e.a_off = g->a_u8 ? -128 : 0;
     const bool need_rb = g->a_u8 || g->zp_a != nullptr || g->zp_a_scalar != 0;
     const bool need_ra = g->zp_b != nullptr || g->zp_b_scalar != 0;

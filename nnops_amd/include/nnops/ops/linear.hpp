@@ -5,9 +5,12 @@
 /// nnops' Linear (include/nnops/ops/linear.hpp:41-142, src/ops/linear.cpp):
 /// the weight is [N, K], the product is MatMul with transpose_b, the input is
 /// [..., K] and the output [..., N]. For an integer pair the output follows
-/// `output_dtype` (s32/s8/u8 here; the f32/f16 dequantizing destinations are
-/// not implemented on this backend and return unsupported); a q4_1 weight with
-/// an f16/f32 input follows the input dtype.
+/// `output_dtype`: s32/s8/u8, or f32/f16 dequantized (bias in the output
+/// dtype, any activation); a q4_1 weight with an f16/f32 input follows the
+/// input dtype. add_to on an fp output folds into the sum before the clip when
+/// residual_pre_activation is set or the epilogue is the identity, and is
+/// added to the (destination-typed) activation otherwise
+/// (src/backend/cpu/matmul/linear.cpp:276-301).
 ///
 /// add_to on an s8/u8 destination (nnops rejects it, linear.cpp:224-226) is
 /// defined here through the float epilogue: the old destination, dequantized

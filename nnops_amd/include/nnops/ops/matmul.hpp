@@ -7,10 +7,15 @@
 ///   - an integer pair (s8|u8 A x s8 B, is_int8_matmul) takes its output dtype
 ///     from `output_dtype`: s32 is the raw MatMulInteger accumulate, s8/u8
 ///     requantize with the output view's QuantParams (or the epilogue's
-///     Requantize table), half away from zero;
+///     Requantize table), half away from zero; f32/f16 dequantize
+///     (v * s_a * s_b + bias, [residual], clip, activation);
+///   - an fp A (f32/f16) with active per-tensor / per-token QuantParams
+///     against an s8 B (is_fp_quant_matmul) is quantized to act_quant_dtype
+///     with those parameters and dequantized back into A's dtype;
 ///   - an fp A (f16/f32) against a q4_1 B is the Q4_1 weight route; the output
 ///     dtype follows A, and an f32 destination for an f16 A is accepted too.
-/// The optional third input is an int32 [N] bias on integer destinations.
+/// The optional third input is the [N] bias: int32 on integer destinations,
+/// the output dtype on f32/f16 ones.
 ///
 /// Extensions (off by default, so nnops semantics are untouched):
 ///   requant_round_even  round half to even in the requant instead;

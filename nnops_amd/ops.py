@@ -91,9 +91,9 @@ def _workspace(nbytes, device):
 
 
 def _epilogue(ep, act=None, min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NONE,
-              quant_scales=None, quant_zero_points=None, quant_param_count=0):
+              quant_scales=None, quant_zero_points=None, quant_param_count=0, alpha=0.0, beta=1.0):
     ep.type = act or L.EP_NONE
-    ep.alpha, ep.beta = 0.0, 1.0
+    ep.alpha, ep.beta = alpha, beta
     ep.min_clip, ep.max_clip = min_clip, max_clip
     ep.quant = quant
     ep.quant_scales = _ptr(quant_scales)
@@ -166,7 +166,8 @@ class MatMul(_Op):
     def __init__(self, *, transpose_a=False, transpose_b=False, output_dtype=L.DT_S32, act=None,
                  min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NONE, quant_scales=None,
                  quant_zero_points=None, quant_param_count=0, residual_pre_activation=False,
-                 requant_round_even=False, float_epilogue=False, backend=L.BACKEND_HIP):
+                 requant_round_even=False, float_epilogue=False, act_quant_dtype=L.DT_S8,
+                 act_alpha=0.0, act_beta=1.0, backend=L.BACKEND_HIP):
         a = L.MatMulAttrs()
         L.lib().nnops_matmul_attrs_init(C.byref(a))
         a.transpose_a, a.transpose_b = int(transpose_a), int(transpose_b)
@@ -174,8 +175,10 @@ class MatMul(_Op):
         a.residual_pre_activation = int(residual_pre_activation)
         a.requant_round_even = int(requant_round_even)
         a.float_epilogue = int(float_epilogue)
+        a.act_quant_dtype = act_quant_dtype
         self._keep = _host_tables(quant_scales, quant_zero_points)
-        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count,
+                  alpha=act_alpha, beta=act_beta)
         super().__init__(L.lib().nnops_matmul_create(C.byref(a), backend))
 
 
@@ -183,7 +186,7 @@ class Linear(_Op):
     def __init__(self, *, output_dtype=L.DT_F32, act=None, min_clip=-math.inf, max_clip=math.inf,
                  add_to=False, residual_pre_activation=False, quant=L.EQ_NONE, quant_scales=None,
                  quant_zero_points=None, quant_param_count=0, requant_round_even=False,
-                 float_epilogue=False, gated=False, backend=L.BACKEND_HIP):
+                 float_epilogue=False, gated=False, act_alpha=0.0, act_beta=1.0, backend=L.BACKEND_HIP):
         a = L.LinearAttrs()
         L.lib().nnops_linear_attrs_init(C.byref(a))
         a.output_dtype = output_dtype
@@ -193,17 +196,41 @@ class Linear(_Op):
         a.float_epilogue = int(float_epilogue)
         a.gated = int(gated)
         self._keep = _host_tables(quant_scales, quant_zero_points)
-        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count)
+        _epilogue(a.epilogue, act, min_clip, max_clip, quant, *self._keep, quant_param_count,
+                  alpha=act_alpha, beta=act_beta)
         super().__init__(L.lib().nnops_linear_create(C.byref(a), backend))
+
+
+class QuantizeLinear(_Op):
+    """inputs: x (f32/f16), scale (f32 device tensor), zero point (s8/u8
+    device tensor of scale's size); output s8/u8 of x's shape."""
+
+    def __init__(self, *, axis=-1, output_dtype=L.DT_S8, backend=L.BACKEND_HIP):
+        a = L.QuantLinearAttrs()
+        L.lib().nnops_quant_linear_attrs_init(C.byref(a))
+        a.axis, a.output_dtype = axis, output_dtype
+        super().__init__(L.lib().nnops_quantize_linear_create(C.byref(a), backend))
+
+
+class DequantizeLinear(_Op):
+    """inputs: x (s8/u8), scale (f32), zero point (s8/u8); output f32/f16."""
+
+    def __init__(self, *, axis=-1, output_dtype=L.DT_F32, backend=L.BACKEND_HIP):
+        a = L.QuantLinearAttrs()
+        L.lib().nnops_quant_linear_attrs_init(C.byref(a))
+        a.axis, a.output_dtype = axis, output_dtype
+        super().__init__(L.lib().nnops_dequantize_linear_create(C.byref(a), backend))
 
 
 def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_S32,
             s_a=1.0, zp_a=0, s_b=1.0, zp_b=0, s_out=1.0, zp_out=0, s_out_rows=None,
             zp_out_rows=None, act=L.ACT_NONE, round_even=False, float_ep=False,
             min_clip=-math.inf, max_clip=math.inf, add_to=False, residual_pre=False,
+            bias_fp=None, act_alpha=0.0, act_beta=1.0,
             m=None, n=None, k=None, workspace=None, stream=None, check=True):
     """Direct call of nnops_hip_gemm_i8 on torch device tensors. Scales/zero
-    points are python scalars or device tensors (per row / per column)."""
+    points are python scalars or device tensors (per row / per column). An
+    f32/f16 destination (OUT_F32 / OUT_F16) takes its bias as `bias_fp`."""
     import torch
     g = L.GemmI8Args()
     M = m if m is not None else (a.shape[1] if trans_a else a.shape[0])
@@ -227,6 +254,7 @@ def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_
     g.out_kind, g.act, g.round_even = out_kind, act, int(round_even)
     g.float_ep, g.min_clip, g.max_clip = int(float_ep), min_clip, max_clip
     g.add_to, g.residual_pre = int(add_to), int(residual_pre)
+    g.bias_fp, g.act_alpha, g.act_beta = _ptr(bias_fp), act_alpha, act_beta
     lib = L.lib()
     need = lib.nnops_hip_gemm_i8_workspace_size(C.byref(g))
     if workspace is None:

@@ -16,8 +16,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
-OUT_S32, OUT_S8, OUT_U8, OUT_F32 = 0, 1, 2, 3
-ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
+OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16 = 0, 1, 2, 3, 4
+(ACT_NONE, ACT_RELU, ACT_GELU, ACT_SIGMOID, ACT_TANH, ACT_LEAKY_RELU, ACT_SILU, ACT_HARDSWISH, ACT_ELU,
+ ACT_RELU6) = range(10)
 
 
 class GemmI8(C.Structure):
@@ -33,6 +34,7 @@ class GemmI8(C.Structure):
         ("float_ep", C.c_int32), ("min_clip", C.c_float), ("max_clip", C.c_float),
         ("add_to", C.c_int32), ("residual_pre", C.c_int32),
         ("m_begin", C.c_int64), ("m_end", C.c_int64),
+        ("act_alpha", C.c_float), ("act_beta", C.c_float),
     ]
 
 
@@ -74,6 +76,10 @@ def lib():
         _lib.orc_f16_to_f32.restype = C.c_float
         _lib.orc_q4_1_decode.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
         _lib.orc_q4_1_quantize.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
+        _lib.orc_quantize_linear.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64,
+                                             C.c_void_p, C.c_void_p, C.c_int64, C.c_int64]
+        _lib.orc_dequantize_linear.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64,
+                                               C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64]
     return _lib
 
 
@@ -99,6 +105,13 @@ def ref_lib():
         _ref.ref_requant_scale.restype = C.c_float
         _ref.ref_q4_1_quantize.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
         _ref.ref_q4_1_decode.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
+        _ref.ref_matmul_dq.argtypes = [
+            C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+            C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+            C.c_int, C.c_int,
+            C.c_void_p, C.c_float, C.c_void_p, C.c_int32,
+            C.c_void_p, C.c_float, C.c_void_p, C.c_int32,
+            C.c_int, C.c_float, C.c_float, C.c_float, C.c_float]
         _ref.ref_gelu.argtypes = [C.c_float]
         _ref.ref_gelu.restype = C.c_float
         _ref.ref_f32_to_f16.argtypes = [C.c_float]
@@ -116,7 +129,7 @@ def gemm_i8(a, b, *, trans_b=False, trans_a=False, bias=None, out_kind=OUT_S32,
             s_a=1.0, zp_a=0, s_b=1.0, zp_b=0, s_out=1.0, zp_out=0,
             s_out_rows=None, zp_out_rows=None, act=ACT_NONE, round_even=False,
             float_ep=False, min_clip=-np.inf, max_clip=np.inf, add_to=False,
-            residual_pre=False, c=None, rows=None, m=None, n=None, k=None):
+            residual_pre=False, c=None, rows=None, m=None, n=None, k=None, act_alpha=0.0, act_beta=1.0):
     """Run the oracle on numpy operands.
 
     ``a``: int8/uint8 2-D array ([M,K], or [K,M] with trans_a); its row stride is
@@ -132,7 +145,8 @@ def gemm_i8(a, b, *, trans_b=False, trans_a=False, bias=None, out_kind=OUT_S32,
     M = a.shape[1] if trans_a else a.shape[0]
     K = a.shape[0] if trans_a else a.shape[1]
     N = b.shape[0] if trans_b else b.shape[1]
-    odt = {OUT_S32: np.int32, OUT_S8: np.int8, OUT_U8: np.uint8, OUT_F32: np.float32}[out_kind]
+    odt = {OUT_S32: np.int32, OUT_S8: np.int8, OUT_U8: np.uint8, OUT_F32: np.float32,
+           OUT_F16: np.float16}[out_kind]
     if c is None:
         c = np.zeros((M, N), dtype=odt)
     assert c.dtype == odt and c.strides[1] == c.itemsize
@@ -150,7 +164,7 @@ def gemm_i8(a, b, *, trans_b=False, trans_a=False, bias=None, out_kind=OUT_S32,
     so_arr, zo_arr = arr(s_out_rows, np.float32), arr(zp_out_rows, np.int32)
     bias_arr = None
     if bias is not None:
-        bias_arr = arr(bias, np.float32 if out_kind == OUT_F32 else np.int32)
+        bias_arr = arr(bias, {OUT_F32: np.float32, OUT_F16: np.float16}.get(out_kind, np.int32))
     p = GemmI8()
     p.a, p.b, p.c = a.ctypes.data, b.ctypes.data, c.ctypes.data
     p.bias = _p(bias_arr)
@@ -167,6 +181,7 @@ def gemm_i8(a, b, *, trans_b=False, trans_a=False, bias=None, out_kind=OUT_S32,
     p.float_ep, p.min_clip, p.max_clip = int(float_ep), float(min_clip), float(max_clip)
     p.add_to, p.residual_pre = int(add_to), int(residual_pre)
     p.m_begin, p.m_end = (rows if rows is not None else (0, 0))
+    p.act_alpha, p.act_beta = float(act_alpha), float(act_beta)
     lib().orc_gemm_i8(C.byref(p))
     return c
 
@@ -204,3 +219,51 @@ def q4_1_quantize(x):
     out = np.zeros(nb * 20, dtype=np.uint8)
     lib().orc_q4_1_quantize(x.ctypes.data, x.size, out.ctypes.data)
     return out
+
+
+def qdq_layout(shape, n_params, axis=-1):
+    """(inner, dim, segment) of QuantizeLinear / DequantizeLinear for a tensor
+    of ``shape`` with ``n_params`` scales: per tensor when n_params <= 1, per
+    token for axis < 0, per channel along ``axis`` otherwise
+    (src/backend/cpu/quant_linear.cpp:92-118)."""
+    numel = int(np.prod(shape)) if len(shape) else 1
+    if n_params <= 1:
+        return 1, 1, max(numel, 1)
+    if axis < 0:
+        cols = shape[-1]
+        return cols, numel // cols, cols
+    inner = int(np.prod(shape[axis + 1:])) if axis + 1 < len(shape) else 1
+    return inner, shape[axis], inner
+
+
+def _params(scale, zero_point):
+    s = np.ascontiguousarray(np.atleast_1d(np.asarray(scale, dtype=np.float32)))
+    z = None if zero_point is None else np.ascontiguousarray(np.atleast_1d(np.asarray(zero_point)).astype(np.int32))
+    return s, z
+
+
+def quantize_linear(x, scale, zero_point=None, *, out_dtype=np.int8, axis=-1):
+    """x: float32/float16 array; scale: f32 scalar or 1-D; zero_point: int
+    scalar / 1-D or None. Returns an int8/uint8 array of x's shape."""
+    x = np.ascontiguousarray(x)
+    assert x.dtype in (np.float32, np.float16)
+    s, z = _params(scale, zero_point)
+    inner, dim, _ = qdq_layout(x.shape, s.size, axis)
+    y = np.zeros(x.shape, dtype=out_dtype)
+    lib().orc_quantize_linear(x.ctypes.data, int(x.dtype == np.float16), y.ctypes.data,
+                              int(np.dtype(out_dtype) == np.uint8), x.size, s.ctypes.data,
+                              _p(z), inner, dim)
+    return y
+
+
+def dequantize_linear(x, scale, zero_point=None, *, out_dtype=np.float32, axis=-1):
+    """x: int8/uint8 array. Returns float32/float16 of x's shape."""
+    x = np.ascontiguousarray(x)
+    assert x.dtype in (np.int8, np.uint8)
+    s, z = _params(scale, zero_point)
+    inner, dim, seg = qdq_layout(x.shape, s.size, axis)
+    y = np.zeros(x.shape, dtype=out_dtype)
+    lib().orc_dequantize_linear(x.ctypes.data, int(x.dtype == np.uint8), y.ctypes.data,
+                                int(np.dtype(out_dtype) == np.float16), x.size, s.ctypes.data,
+                                _p(z), inner, dim, seg)
+    return y

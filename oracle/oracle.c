@@ -165,14 +165,45 @@ float orc_gelu_tanh(float x)
     return (0.5f * x) * (1.0f + orc_tanhf(inner));
 }
 
-static float apply_act(int32_t act, float x, float lo, float hi)
+static float apply_act_ab(int32_t act, float x, float lo, float hi, float alpha, float beta)
 {
     /* apply_epilogue: activate(clamp(x, min_clip, max_clip)), simd_epilogue.hpp:56-90 */
     if (x < lo) x = lo;
     if (hi < x) x = hi;
-    if (act == ORC_ACT_RELU) return x > 0.0f ? x : 0.0f;
-    if (act == ORC_ACT_GELU) return orc_gelu_tanh(x);
-    return x;
+    switch (act) {
+    case ORC_ACT_RELU: return x > 0.0f ? x : 0.0f;
+    case ORC_ACT_RELU6: { float y = x > 0.0f ? x : 0.0f; return y < 6.0f ? y : 6.0f; }
+    case ORC_ACT_LEAKY_RELU: return x > 0.0f ? x : alpha * x;
+    case ORC_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
+    case ORC_ACT_TANH: return tanhf(x);
+    case ORC_ACT_GELU: return orc_gelu_tanh(x);
+    case ORC_ACT_SILU: return x / (1.0f + expf(-x));
+    case ORC_ACT_HARDSWISH: {
+        float r6 = x + 3.0f;
+        r6 = r6 > 0.0f ? r6 : 0.0f;
+        r6 = r6 < 6.0f ? r6 : 6.0f;
+        return x * r6 * (beta / 6.0f);
+    }
+    case ORC_ACT_ELU: return x > 0.0f ? x : alpha * (expf(x) - 1.0f);
+    default: return x;
+    }
+}
+
+/* the reference's GELU for dequantized (f32/f16) destinations: std::tanh */
+static float apply_act_fp(int32_t act, float x, float lo, float hi, float alpha, float beta)
+{
+    if (act == ORC_ACT_GELU) {
+        if (x < lo) x = lo;
+        if (hi < x) x = hi;
+        const float c = 0.7978845608028654f;
+        return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+    }
+    return apply_act_ab(act, x, lo, hi, alpha, beta);
+}
+
+static float apply_act(int32_t act, float x, float lo, float hi)
+{
+    return apply_act_ab(act, x, lo, hi, 0.0f, 1.0f);
 }
 
 static inline int32_t load_a(const orc_gemm_i8_t* p, int64_t m, int64_t k)
@@ -232,15 +263,27 @@ void orc_gemm_i8(const orc_gemm_i8_t* p)
             /* matmul_int8_compensate with u8_offset 0: the dot was over true values */
             int32_t v = raw[n] - zp_a * r_b[n] - zp_b * r_a + kk * zp_a * zp_b;
 
-            if (p->out_kind == ORC_OUT_F32) {
-                /* dq route (simd_epilogue.hpp:934-949) */
-                float* c = (float*)p->c + m * p->ldc + n;
+            if (p->out_kind == ORC_OUT_F32 || p->out_kind == ORC_OUT_F16) {
+                /* dq route (simd_epilogue.hpp:784-949, matmul_dq_ref.cpp:178-190):
+                 * f = float(v) * (s_a * s_b) [+ bias[n]]; a pre-activation
+                 * residual joins before the clip; a post-activation one is
+                 * added to the destination-typed result (linear.cpp:283-301:
+                 * a compact temporary, then residual_add). */
+                const int f16 = p->out_kind == ORC_OUT_F16;
+                float* c32 = (float*)p->c + m * p->ldc + n;
+                uint16_t* c16 = (uint16_t*)p->c + m * p->ldc + n;
+                const float old = p->add_to ? (f16 ? orc_f16_to_f32(*c16) : *c32) : 0.0f;
                 float f = (float)v * (s_a * s_b);
-                if (p->bias) f += ((const float*)p->bias)[n]; /* column bias, always added */
-                if (p->add_to && p->residual_pre) f += *c;
-                f = apply_act(p->act, f, p->min_clip, p->max_clip);
-                if (p->add_to && !p->residual_pre) f += *c;
-                *c = f;
+                if (p->bias) {
+                    f += f16 ? orc_f16_to_f32(((const uint16_t*)p->bias)[n]) : ((const float*)p->bias)[n];
+                }
+                if (p->add_to && p->residual_pre) f += old;
+                f = apply_act_fp(p->act, f, p->min_clip, p->max_clip, p->act_alpha, p->act_beta);
+                if (p->add_to && !p->residual_pre) {
+                    if (f16) f = orc_f16_to_f32(orc_f32_to_f16(f));
+                    f = f + old;
+                }
+                if (f16) *c16 = orc_f32_to_f16(f); else *c32 = f;
                 continue;
             }
 
@@ -429,5 +472,68 @@ void orc_xs128_u64(uint64_t seed, int64_t count, uint64_t* out)
         a ^= a << 23;
         s1 = a ^ b ^ (a >> 18) ^ (b >> 5);
         out[i] = s1 + b;
+    }
+}
+
+/* ---------------------------------------------------------------------------
+ * QuantizeLinear / DequantizeLinear over a flat row-major array of `count`
+ * elements. Element i takes parameter j = (i / inner) % dim (per tensor: dim
+ * 1; per token: inner = cols, dim = rows; per channel: inner = product of the
+ * dims after the axis, dim = the axis extent), as
+ * src/backend/cpu/quant_linear.cpp:97-118 maps the granularities onto the
+ * kernel's per-row M x N shape.
+ * ------------------------------------------------------------------------- */
+static int64_t qdq_index(int64_t i, int64_t inner, int64_t dim)
+{
+    return dim <= 1 ? 0 : (i / inner) % dim;
+}
+
+/* src/backend/cpu/x86_64/quant.hpp:52-85 (vector body) and :162-167 (tail,
+ * contracted to one FMA under -mfma): v = fma(x, 1/s, zp), rounded to nearest
+ * even; the conversion of NaN or |v| >= 2^31 yields INT32_MIN, which the
+ * saturating pack / clamp turn into qmin. */
+void orc_quantize_linear(const void* x, int32_t x_f16, void* y, int32_t y_u8, int64_t count,
+                         const float* scale, const int32_t* zero_point, int64_t inner, int64_t dim)
+{
+    const int32_t qmin = y_u8 ? 0 : -128, qmax = y_u8 ? 255 : 127;
+    for (int64_t i = 0; i < count; ++i) {
+        const float xv = x_f16 ? orc_f16_to_f32(((const uint16_t*)x)[i]) : ((const float*)x)[i];
+        const int64_t j = qdq_index(i, inner, dim);
+        const float inv = 1.0f / scale[j];
+        const float zf = zero_point ? (float)zero_point[j] : 0.0f;
+        const float v = fmaf(xv, inv, zf);
+        int32_t q = INT32_MIN;
+        if (fabsf(v) < 2147483648.0f) q = (int32_t)nearbyintf(v);
+        if (q < qmin) q = qmin;
+        if (q > qmax) q = qmax;
+        if (y_u8) ((uint8_t*)y)[i] = (uint8_t)q;
+        else ((int8_t*)y)[i] = (int8_t)q;
+    }
+}
+
+/* src/backend/cpu/x86_64/quant.hpp:282-330: per row (here: per segment of
+ * `segment` elements) the whole 16-element blocks compute fma(q, s, -zp*s) and
+ * the last segment % 16 elements (q - zp) * s; f16 narrows the f32 result with
+ * round to nearest even (the F16C conversion). */
+void orc_dequantize_linear(const void* x, int32_t x_u8, void* y, int32_t y_f16, int64_t count,
+                           const float* scale, const int32_t* zero_point, int64_t inner, int64_t dim,
+                           int64_t segment)
+{
+    const int64_t body = segment - segment % 16;
+    for (int64_t i = 0; i < count; ++i) {
+        const int32_t q = x_u8 ? (int32_t)((const uint8_t*)x)[i] : (int32_t)((const int8_t*)x)[i];
+        const int64_t j = qdq_index(i, inner, dim);
+        const float s = scale[j];
+        const float zf = zero_point ? (float)zero_point[j] : 0.0f;
+        float v;
+        if (i % segment < body) {
+            const float nzs = -zf * s;
+            v = fmaf((float)q, s, nzs);
+        } else {
+            const float d = (float)q - zf;
+            v = d * s;
+        }
+        if (y_f16) ((uint16_t*)y)[i] = orc_f32_to_f16(v);
+        else ((float*)y)[i] = v;
     }
 }

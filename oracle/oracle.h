@@ -13,8 +13,10 @@
  *   orc_gemm_i8 int32/s8/u8 outputs  known answers of tests/test_matmul_int8.cpp,
  *                                    brute-force int64 matmul, golden vectors
  *                                    from the compiled reference oracle.
- *   orc_gemm_i8 f32 (dq) output      golden vectors from the compiled reference
- *                                    matmul_dq_ref (when built).
+ *   orc_gemm_i8 f32/f16 (dq) output  the compiled reference matmul_dq_ref (when
+ *                                    built) on the same int8 operands, bit for
+ *                                    bit, and the known answers of
+ *                                    tests/test_matmul_dq.cpp:185-247.
  *   orc_gemm_i8 float epilogue       s8 add_to / gelu on an integer destination:
  *                                    no reference route exists, so the composite
  *                                    is PARITY UNPINNED; its pieces are pinned
@@ -26,6 +28,11 @@
  *                                    tests/test_q4_1.cpp, golden bytes from the
  *                                    compiled reference quantize_q4.
  *   orc_gemm_q4_1                    float64 brute force from decoded weights.
+ *   orc_quantize/dequantize_linear   known answers of tests/test_quant_linear.cpp
+ *                                    (ties to even, clamps, per-channel and
+ *                                    per-token indexing, u8 zero points), exact
+ *                                    rational checks (power-of-two scales), and
+ *                                    the round trip q -> x -> q.
  */
 #ifndef NNOPS_ORACLE_H
 #define NNOPS_ORACLE_H
@@ -36,14 +43,18 @@
 extern "C" {
 #endif
 
-enum { ORC_OUT_S32 = 0, ORC_OUT_S8 = 1, ORC_OUT_U8 = 2, ORC_OUT_F32 = 3 };
-enum { ORC_ACT_NONE = 0, ORC_ACT_RELU = 1, ORC_ACT_GELU = 2 };
+enum { ORC_OUT_S32 = 0, ORC_OUT_S8 = 1, ORC_OUT_U8 = 2, ORC_OUT_F32 = 3, ORC_OUT_F16 = 4 };
+/* EpilogueActivateType values (include/nnops/core/epilogue.hpp:25-36) */
+enum {
+    ORC_ACT_NONE = 0, ORC_ACT_RELU = 1, ORC_ACT_GELU = 2, ORC_ACT_SIGMOID = 3, ORC_ACT_TANH = 4,
+    ORC_ACT_LEAKY_RELU = 5, ORC_ACT_SILU = 6, ORC_ACT_HARDSWISH = 7, ORC_ACT_ELU = 8, ORC_ACT_RELU6 = 9
+};
 
 typedef struct {
     const void* a;        /* s8 or u8, [M,K] (or [K,M] with trans_a) */
     const int8_t* b;      /* s8, [K,N] (or [N,K] with trans_b) */
-    const void* bias;     /* [N]: int32 for integer outputs, f32 for ORC_OUT_F32; may be NULL */
-    void* c;              /* destination; read first when add_to */
+    const void* bias;     /* [N]: int32 for integer outputs, f32 / f16 bits for ORC_OUT_F32 / F16; may be NULL */
+    void* c;              /* destination (f16 as its bits); read first when add_to */
     int64_t m, n, k;
     int64_t lda, ldb, ldc; /* row strides in elements */
     int32_t trans_a, trans_b, a_u8;
@@ -60,6 +71,7 @@ typedef struct {
     int32_t add_to, residual_pre;
     /* rows [m_begin, m_end) are computed; m_end <= 0 means all rows */
     int64_t m_begin, m_end;
+    float act_alpha, act_beta;  /* LeakyRelu / Elu alpha, HardSwish beta */
 } orc_gemm_i8_t;
 
 void orc_gemm_i8(const orc_gemm_i8_t* p);
@@ -91,6 +103,15 @@ typedef struct {
 } orc_gemm_q4_1_t;
 
 void orc_gemm_q4_1(const orc_gemm_q4_1_t* p);
+
+/* QuantizeLinear / DequantizeLinear over `count` flat elements; element i
+ * uses parameter (i / inner) % dim; `segment` is the reference kernel's row
+ * length (numel per tensor, cols per token, inner per channel). */
+void orc_quantize_linear(const void* x, int32_t x_f16, void* y, int32_t y_u8, int64_t count,
+                         const float* scale, const int32_t* zero_point, int64_t inner, int64_t dim);
+void orc_dequantize_linear(const void* x, int32_t x_u8, void* y, int32_t y_f16, int64_t count,
+                           const float* scale, const int32_t* zero_point, int64_t inner, int64_t dim,
+                           int64_t segment);
 
 /* xorshift128+ stream of the reference test harness (random_tensor.hpp:18-57) */
 void orc_xs128_u64(uint64_t seed, int64_t count, uint64_t* out);

@@ -47,8 +47,16 @@ def test_gemm_i8_rejects_before_any_launch():
     assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT  # null data
     g.a = g.b = g.c = 16  # never dereferenced: every rejection below happens first
     g.lda, g.ldb, g.ldc = 4, 4, 4
-    g.out_kind = na.OUT_F32
+    g.out_kind = 7                       # no such destination
     assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    g.out_kind = na.OUT_S8
+    g.act = na.ACT_SIGMOID               # the requantizing pass honours Relu (and Gelu via float_ep) only
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
+    g.act = na.ACT_NONE
+    g.out_kind = na.OUT_F32
+    g.bias = 16                          # an f32 destination takes its bias as bias_fp
+    assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.bias = None
     g.out_kind = na.OUT_S32
     g.float_ep = 1
     assert lib.nnops_hip_gemm_i8(C.byref(g), None, 0, None) == na.UNSUPPORTED
@@ -161,3 +169,45 @@ def test_compute_rejections_without_gpu():
     # gated Linear has no quantized route
     assert na.Linear(gated=True).validate([desc([4, 8], na.DT_S8), desc([6, 8], na.DT_S8)],
                                           [desc([4, 6], na.DT_F32)]) == na.UNSUPPORTED
+
+
+def test_fp_activation_matmul_descriptors():
+    # fp A x s8 B follows A's dtype; workspace holds A_q plus the int8 call's
+    op = na.MatMul(act_quant_dtype=na.DT_U8)
+    ins = [desc([2, 4, 64], na.DT_F16), desc([64, 32], na.DT_S8)]
+    shape, dt = op.output_desc(ins)
+    assert shape == [2, 4, 32] and dt == na.DT_F16
+    assert op.workspace_size(ins, [desc([2, 4, 32], na.DT_F16)]) >= 2 * 4 * 64
+    # dequantizing destinations of the int8 pair
+    shape, dt = na.MatMul(output_dtype=na.DT_F16).output_desc([desc([3, 8], na.DT_S8), desc([8, 5], na.DT_S8)])
+    assert shape == [3, 5] and dt == na.DT_F16
+
+
+def test_quant_linear_descriptors_and_validate():
+    # quant_linear.hpp: same shape, output_dtype; dequantize resolves non-float to f32
+    q = na.QuantizeLinear(output_dtype=na.DT_U8)
+    ins = [desc([3, 5, 7], na.DT_F32), desc([15], na.DT_F32), desc([15], na.DT_U8)]
+    shape, dt = q.output_desc(ins)
+    assert shape == [3, 5, 7] and dt == na.DT_U8
+    assert q.validate(ins, [desc([3, 5, 7], na.DT_U8)]) == na.OK
+    assert q.validate(ins, [desc([3, 5, 7], na.DT_S32)]) == na.INVALID_ARGUMENT
+    assert q.validate([desc([3, 5, 7], na.DT_S32)] + ins[1:], [desc([3, 5, 7], na.DT_U8)]) == na.UNSUPPORTED
+    assert q.validate([ins[0], desc([15], na.DT_F16), ins[2]], [desc([3, 5, 7], na.DT_U8)]) == na.INVALID_ARGUMENT
+    assert q.validate(ins[:2], [desc([3, 5, 7], na.DT_U8)]) == na.INVALID_ARGUMENT
+    d = na.DequantizeLinear(output_dtype=na.DT_S8)
+    _, dt = d.output_desc([desc([4, 4], na.DT_S8), desc([1], na.DT_F32), desc([1], na.DT_S8)])
+    assert dt == na.DT_F32
+    d16 = na.DequantizeLinear(output_dtype=na.DT_F16)
+    assert d16.validate([desc([4, 4], na.DT_S8), desc([1], na.DT_F32), desc([1], na.DT_S8)],
+                        [desc([4, 4], na.DT_F16)]) == na.OK
+    # backend with no kernels
+    x = desc([4], na.DT_F32)
+    x.data = 256
+    s = desc([1], na.DT_F32)
+    s.data = 256
+    z = desc([1], na.DT_S8)
+    z.data = 256
+    o = desc([4], na.DT_S8)
+    o.data = 512
+    assert na.QuantizeLinear(backend=na.BACKEND_CPU).compute([o], [x, s, z], stream=0, workspace=0) \
+        == na.UNSUPPORTED
