@@ -143,14 +143,29 @@ def run_cfg2(args, torch, dg, na, stream):
     }
 
 
-def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbuf=8, trans_b=False):
-    """Config 3: int8 GEMV with `nbuf` rotated weight buffers (> MALL)."""
+def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbuf=8, trans_b=False,
+                 prepacked=False):
+    """Config 3: int8 GEMV with `nbuf` rotated weight buffers (> MALL).
+    `prepacked`: each weight goes through prepackWeights first (outside the
+    timed region, once at load time), and the call reads the packed form."""
     import numpy as np
     a = torch.from_numpy(dg.ints(301, (M, K), -127, 127)).cuda()
     ws_list = []
     base = torch.from_numpy(dg.ints(302, (N, K) if trans_b else (K, N), -127, 127)).cuda()
     for i in range(nbuf):
         ws_list.append(base if i == 0 else torch.roll(base, shifts=i, dims=1).contiguous())
+    if prepacked:
+        kp = (K + 127) // 128 * 128
+        packed = []
+        for w in ws_list:
+            blob = torch.empty(na.lib().nnops_hip_prepack_i8_bytes(K, N), dtype=torch.uint8, device="cuda")
+            rc = na.lib().nnops_hip_prepack_i8(w.data_ptr(), K, N, w.stride(0), int(trans_b), blob.data_ptr(),
+                                               stream.cuda_stream)
+            assert rc == 0, rc
+            packed.append(blob[:N * kp].view(torch.int8).view(N, kp))
+        stream.synchronize()
+        ws_list = packed
+        trans_b = True
     c = torch.zeros((M, N), dtype=torch.int32, device="cuda")
     s = stream.cuda_stream
     probe = na.GemmI8Args()
@@ -168,7 +183,8 @@ def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbu
     nbytes = K * N + K * M + N * M * 4
     gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
     return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3,
-            "bytes": nbytes, "M": M, "K": K, "N": N, "weight_layout": "[N,K]" if trans_b else "[K,N]",
+            "bytes": nbytes, "M": M, "K": K, "N": N,
+            "weight_layout": "prepacked [K,N] -> [N][kp]" if prepacked else ("[N,K]" if trans_b else "[K,N]"),
             "rotated_weight_bytes": nbuf * K * N}
 
 
@@ -391,6 +407,10 @@ def main():
                                                           trans_b=True)
         secondary["cfg3_int8_gemv_m16_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
                                                           trans_b=False)
+        secondary["cfg3_int8_gemv_m1_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                                   prepacked=True)
+        secondary["cfg3_int8_gemv_m16_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, args.steps,
+                                                                    args.warmup, M=16, prepacked=True)
         secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup)
         secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
                                                          args.warmup)

@@ -119,11 +119,29 @@ typedef struct NnopsGemmI8Args {
     int32_t add_to, residual_pre; /* float epilogue and f32/f16 destinations */
     const void* bias_fp;        /* [N] f32 or f16 (C's type), f32/f16 destinations only */
     float act_alpha, act_beta;  /* LeakyRelu / Elu alpha, HardSwish beta */
+    const int32_t* b_col_sums;  /* [N] sum over k of B[k,n] (a prepacked B carries them), or
+                                   NULL: computed into the workspace when the A zero point
+                                   or a u8 A needs them */
 } NnopsGemmI8Args;
 
 size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* args);
 int nnops_hip_gemm_i8(const NnopsGemmI8Args* args, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* Prepacked s8 B for the HIP kernels (nnops' MatMul::prepackWeights,
+ * src/ops/matmul.cpp:96-141, with a gfx950 layout in place of the CPU
+ * panels). From B [K,N] (trans_b = 0) or [N,K] (trans_b = 1), row stride ldb,
+ * it writes:
+ *   rows   [N][kp] k-contiguous, kp = K rounded up to 128, zero padded;
+ *   sums   int32 [N] = sum over k of B[k,n], at byte offset
+ *          align_up(N * kp, 256).
+ * A call then passes b = out, ldb = kp, trans_b = 1, b_col_sums = out + that
+ * offset: every route reads the weight k-contiguous and 16-byte aligned (no
+ * per-call transpose, no column-sum pass). `out` must be 256-byte aligned and
+ * hold nnops_hip_prepack_i8_bytes(k, n) bytes. Stream-ordered, no allocation. */
+size_t nnops_hip_prepack_i8_bytes(int64_t k, int64_t n);
+int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int32_t trans_b, void* out,
+                         void* stream);
 
 /* Q4_1-weight GEMM  C[M,N] = A[M,K] x dequant(B).
  * Replaces nnops' fp x q4_1 route: matmul_qblock_fused (small M,

@@ -42,6 +42,8 @@ typedef struct NnopsTensor {
     const float* scale_data;        /* host or device */
     const int32_t* zero_point_data; /* host or device */
     int64_t num_scales;
+    int32_t layout;         /* nnops::TensorLayout value; 0 = Dense (12). 18 = PackedBHip,
+                               the prepacked weight nnops_op_prepack_weights describes */
 } NnopsTensor;
 
 /* nnops::Epilogue (include/nnops/core/epilogue.hpp:73-92) */
@@ -96,6 +98,15 @@ void nnops_quant_linear_attrs_init(NnopsQuantLinearAttrs* attrs);
 NnopsOp* nnops_quantize_linear_create(const NnopsQuantLinearAttrs* attrs, int32_t backend);
 NnopsOp* nnops_dequantize_linear_create(const NnopsQuantLinearAttrs* attrs, int32_t backend);
 void nnops_op_destroy(NnopsOp* op);
+
+/* OpBase::prepackWeights (include/nnops/core/op_base.hpp:72-78) for MatMul /
+ * Linear: with outputs[0].data == NULL it is the query and writes the packed
+ * descriptor (dims, dtype, pitch, layout = 18; rank 0 = no packed form) into
+ * outputs[0]; with outputs[0] describing a device buffer of that size (256-byte
+ * aligned) it fills it on `hip_stream`. inputs[0] is the raw weight. Returns a
+ * Status. The packed weight then goes to compute() as the B / weight input. */
+int nnops_op_prepack_weights(NnopsOp* op, const NnopsTensor* inputs, int32_t n_inputs, NnopsTensor* outputs,
+                             int32_t n_outputs, void* hip_stream);
 
 /* Fills out_desc (dims, rank, dtype; data NULL). Returns 0 on success. */
 int nnops_op_output_desc(const NnopsOp* op, const NnopsTensor* inputs, int32_t n_inputs,

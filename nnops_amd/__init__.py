@@ -13,7 +13,7 @@ from ._lib import (  # noqa: F401
     OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_INITIALIZED, OUT_OF_MEMORY, INTERNAL,
     OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16, ACT_NONE, ACT_RELU, ACT_GELU,
     ACT_SIGMOID, ACT_TANH, ACT_LEAKY_RELU, ACT_SILU, ACT_HARDSWISH, ACT_ELU, ACT_RELU6,
-    DT_F32, DT_F16, DT_S8, DT_U8, DT_S32, DT_Q4_1, BACKEND_HIP, BACKEND_CPU,
+    DT_F32, DT_F16, DT_S8, DT_U8, DT_S32, DT_Q4_1, BACKEND_HIP, BACKEND_CPU, LAYOUT_DENSE, LAYOUT_PACKED_B_HIP,
     EP_NONE, EP_RELU, EP_GELU, EP_SIGMOID, EP_TANH, EP_LEAKY_RELU, EP_SILU, EP_HARDSWISH, EP_ELU,
     EP_RELU6, EQ_NONE, EQ_REQUANTIZE,
 )

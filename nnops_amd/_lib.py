@@ -12,6 +12,7 @@ OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16 = range(5)
  ACT_RELU6) = range(10)
 DT_F32, DT_F16, DT_BF16, DT_S8, DT_U8, DT_S32 = 0, 1, 2, 3, 4, 5
 DT_Q4_1 = 11
+LAYOUT_DENSE, LAYOUT_PACKED_B_HIP = 12, 18
 BACKEND_CPU, BACKEND_CUDA, BACKEND_HIP = 0, 1, 4
 # EpilogueActivateType / EpilogueQuantType values
 EP_NONE, EP_RELU, EP_GELU, EP_SIGMOID, EP_TANH = 0, 1, 2, 3, 4
@@ -32,6 +33,7 @@ class GemmI8Args(C.Structure):
         ("float_ep", C.c_int32), ("min_clip", C.c_float), ("max_clip", C.c_float),
         ("add_to", C.c_int32), ("residual_pre", C.c_int32),
         ("bias_fp", C.c_void_p), ("act_alpha", C.c_float), ("act_beta", C.c_float),
+        ("b_col_sums", C.c_void_p),
     ]
 
 
@@ -60,6 +62,7 @@ class Tensor(C.Structure):
         ("data", C.c_void_p), ("pitch", C.c_int64),
         ("granularity", C.c_int32), ("scale", C.c_float), ("zero_point", C.c_int32),
         ("scale_data", C.c_void_p), ("zero_point_data", C.c_void_p), ("num_scales", C.c_int64),
+        ("layout", C.c_int32),
     ]
 
 
@@ -103,6 +106,9 @@ SIGNATURES = {
     "nnops_hip_gemm_q4_1_workspace_size": (C.c_size_t, [C.POINTER(GemmQ41Args)]),
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
+    "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
+    "nnops_hip_prepack_i8": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p,
+                                       C.c_void_p]),
     "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "nnops_hip_diag_stream_read": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
     "nnops_hip_diag_empty": (C.c_int, [C.c_void_p, C.c_void_p]),
@@ -116,6 +122,8 @@ SIGNATURES = {
     "nnops_quantize_linear_create": (C.c_void_p, [C.POINTER(QuantLinearAttrs), C.c_int32]),
     "nnops_dequantize_linear_create": (C.c_void_p, [C.POINTER(QuantLinearAttrs), C.c_int32]),
     "nnops_op_destroy": (None, [C.c_void_p]),
+    "nnops_op_prepack_weights": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.c_int32, C.POINTER(Tensor), C.c_int32,
+                                           C.c_void_p]),
     "nnops_op_output_desc": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.c_int32, C.POINTER(Tensor)]),
     "nnops_op_validate": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.c_int32, C.POINTER(Tensor), C.c_int32]),
     "nnops_op_workspace_size": (C.c_size_t, [C.c_void_p, C.POINTER(Tensor), C.c_int32,

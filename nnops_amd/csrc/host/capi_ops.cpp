@@ -28,10 +28,11 @@ TensorView to_view(const NnopsTensor& t)
     const int64_t rank = t.rank < 0 ? 0 : (t.rank > 8 ? 8 : t.rank);
     std::span<const int64_t> shape(t.dims, static_cast<size_t>(rank));
     const DataType dt = static_cast<DataType>(t.dtype);
+    const TensorLayout lay = t.layout == 0 ? TensorLayout::Dense : static_cast<TensorLayout>(t.layout);
     if (t.pitch > 0) {
-        return TensorView(shape, dt, t.data, t.pitch, TensorLayout::Dense, qp);
+        return TensorView(shape, dt, t.data, t.pitch, lay, qp);
     }
-    return TensorView(shape, dt, t.data, TensorLayout::Dense, qp);
+    return TensorView(shape, dt, t.data, lay, qp);
 }
 
 Epilogue to_epilogue(const NnopsEpilogue& e)
@@ -198,6 +199,46 @@ int nnops_op_output_desc(const NnopsOp* op, const NnopsTensor* inputs, int32_t n
     out->dtype = static_cast<int32_t>(o[0].dtype);
     out->scale = 1.0f;
     return 0;
+}
+
+int nnops_op_prepack_weights(NnopsOp* op, const NnopsTensor* inputs, int32_t n_inputs, NnopsTensor* outputs,
+                             int32_t n_outputs, void* hip_stream)
+{
+    if (op == nullptr || inputs == nullptr || outputs == nullptr || n_inputs < 1 || n_outputs < 1) {
+        return static_cast<int>(Status::invalid_argument);
+    }
+    const TensorView in = to_view(inputs[0]);
+    TensorView out[1] = {outputs[0].data != nullptr ? to_view(outputs[0]) : TensorView{}};
+    ComputeContext ctx;
+    ctx.hip_stream = hip_stream;
+    Status st = Status::unsupported;
+    if (auto* mm = dynamic_cast<MatMul*>(op->op.get())) {
+        st = mm->prepack(std::span<const TensorView>(&in, 1), std::span<TensorView>(out, 1), ctx);
+    } else if (auto* ln = dynamic_cast<Linear*>(op->op.get())) {
+        st = ln->prepack(std::span<const TensorView>(&in, 1), std::span<TensorView>(out, 1), ctx);
+    } else {
+        // no packed form: the query answers empty
+        st = outputs[0].data == nullptr ? Status::ok : Status::unsupported;
+    }
+    if (is_ok(st) && outputs[0].data == nullptr) {
+        NnopsTensor d{};
+        d.rank = out[0].rank();
+        for (int64_t i = 0; i < d.rank; ++i) {
+            d.dims[i] = out[0].shape(i);
+        }
+        d.dtype = static_cast<int32_t>(out[0].data_type());
+        d.pitch = out[0].pitch();
+        d.layout = d.rank > 0 ? static_cast<int32_t>(out[0].layout()) : 0;
+        const QuantParams& qp = out[0].quant_params();
+        d.granularity = static_cast<int32_t>(qp.granularity);
+        d.scale = d.rank > 0 ? qp.scale : 1.0f;
+        d.zero_point = qp.zero_point;
+        d.scale_data = qp.scale_data;
+        d.zero_point_data = qp.zero_point_data;
+        d.num_scales = qp.num_scales;
+        outputs[0] = d;
+    }
+    return static_cast<int>(st);
 }
 
 int nnops_op_validate(const NnopsOp* op, const NnopsTensor* inputs, int32_t n_inputs,

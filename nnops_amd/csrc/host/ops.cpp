@@ -44,6 +44,7 @@ struct Geometry {
     int64_t m = 0, n = 0, k = 0;
     int64_t batch = 1;
     bool trans_a = false, trans_b = false;
+    bool b_packed = false;  // B is a PackedBHip blob (always [N][kp])
     // leading (batch) dims, broadcast
     int64_t nd = 0;
     int64_t out_batch[TensorDesc::kMaxRank]{};
@@ -66,10 +67,22 @@ Status matmul_geometry(const TensorDesc& a, const TensorDesc& b, bool ta, bool t
     g.trans_b = tb;
     g.m = ta ? ak : am;
     g.k = ta ? am : ak;
-    const int64_t kb = tb ? b1 : b0;
-    g.n = tb ? b0 : b1;
-    if (kb != g.k) {
-        return Status::invalid_argument;
+    if (b.layout == TensorLayout::PackedBHip) {
+        // A packed B carries N but no K: K is A's, and the blob must be large
+        // enough for it (nnops: the backend's numel check, matmul.cpp:84-90)
+        if (b.rank != 2 || b.dtype != DataType::s8 ||
+            b0 * b1 < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(g.k, b0))) {
+            return Status::invalid_argument;
+        }
+        g.n = b0;
+        g.trans_b = true;
+        g.b_packed = true;
+    } else {
+        const int64_t kb = tb ? b1 : b0;
+        g.n = tb ? b0 : b1;
+        if (kb != g.k) {
+            return Status::invalid_argument;
+        }
     }
     g.nd = std::max(a.rank, b.rank) - 2;
     g.batch = 1;
@@ -206,6 +219,12 @@ int64_t a_table_rows(const Geometry& g)
     return (a_matrices(g) - 1) * rows_per + g.m;
 }
 
+/// Row pitch of a PackedBHip blob for a K (nnops_hip_prepack_i8's layout).
+int64_t packed_pitch(int64_t k)
+{
+    return (k + 127) / 128 * 128;
+}
+
 bool is_fp_quant_pair(DataType a, DataType b)
 {
     return (a == DataType::f32 || a == DataType::f16) && b == DataType::s8;
@@ -217,10 +236,10 @@ NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, const QuantCall& q, int
     x.m = g.m;
     x.n = g.n;
     x.k = g.k;
-    x.trans_a = q.trans_a;
-    x.trans_b = q.trans_b;
+    x.trans_a = g.trans_a;
+    x.trans_b = g.trans_b;
     x.lda = g.trans_a ? g.m : g.k;
-    x.ldb = g.trans_b ? g.k : g.n;
+    x.ldb = g.b_packed ? packed_pitch(g.k) : (g.trans_b ? g.k : g.n);
     x.ldc = g.n;
     x.out_kind = out_kind;
     return x;
@@ -340,8 +359,12 @@ Status run_i8(const QuantCall& q, const Geometry& g, TensorView& out, const Tens
     NnopsGemmI8Args x = i8_args_from_geometry(g, q, ok);
     x.a_u8 = a.data_type() == DataType::u8;
     x.lda = a.row_stride_elems();
-    x.ldb = b.row_stride_elems();
+    x.ldb = g.b_packed ? packed_pitch(g.k) : b.row_stride_elems();
     x.ldc = out.row_stride_elems();
+    if (g.b_packed) {
+        x.b_col_sums = reinterpret_cast<const int32_t*>(
+            b.ptr<const char>() + align_up(static_cast<size_t>(g.n * packed_pitch(g.k))));
+    }
     x.add_to = q.add_to;
     x.residual_pre = q.residual_pre;
     x.min_clip = q.ep.min_clip;
@@ -769,7 +792,12 @@ Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const Tens
     if (!linear_descs(inputs, x2, w)) {
         return Status::invalid_argument;
     }
-    if (x2.dims[1] != w.dims[1]) {
+    if (w.layout == TensorLayout::PackedBHip) {
+        if (w.dtype != DataType::s8 ||
+            w.dims[0] * w.dims[1] < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(x2.dims[1], w.dims[0]))) {
+            return Status::invalid_argument;
+        }
+    } else if (x2.dims[1] != w.dims[1]) {
         return Status::invalid_argument;
     }
     if (inputs.size() > 2 && inputs[2].numel() != w.dims[0]) {
@@ -852,6 +880,86 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
                                        std::span<const TensorDesc>(&desc_out, 1));
     return run_quant(q, y2, std::span<const TensorView>(ins, inputs.size()), ctx, workspace,
                      workspace != nullptr ? ws : 0);
+}
+
+// ===========================================================================
+// prepackWeights: s8 B -> TensorLayout::PackedBHip
+// ===========================================================================
+namespace {
+
+/// The query / fill contract of nnops' prepackWeights (src/ops/matmul.cpp:
+/// 96-141): an empty outputs[0] is the query and receives the descriptor
+/// [N, ceil(bytes / N)] (s8, PackedBHip, pitched at its row length, carrying
+/// the weight's QuantParams); a populated one is filled on ctx's stream. A
+/// weight with no packed form (anything but a 2-D s8 B) answers empty.
+Status prepack_s8(const TensorView& raw, bool trans_b, std::span<TensorView> outputs, const ComputeContext& ctx,
+                  Backend backend)
+{
+    if (outputs.empty()) {
+        return Status::invalid_argument;
+    }
+    if (backend != Backend::HIP || raw.rank() != 2 || raw.data_type() != DataType::s8 ||
+        raw.layout() != TensorLayout::Dense) {
+        if (outputs[0].is_empty()) {
+            outputs[0] = TensorView{};
+            return Status::ok;
+        }
+        return Status::unsupported;
+    }
+    const int64_t n = trans_b ? raw.shape(0) : raw.shape(1);
+    const int64_t k = trans_b ? raw.shape(1) : raw.shape(0);
+    if (n <= 0 || k <= 0) {
+        if (outputs[0].is_empty()) {
+            outputs[0] = TensorView{};
+            return Status::ok;
+        }
+        return Status::invalid_argument;
+    }
+    const int64_t bytes = static_cast<int64_t>(nnops_hip_prepack_i8_bytes(k, n));
+    const int64_t cols = (bytes + n - 1) / n;
+    const int64_t shape[2] = {n, cols};
+    if (outputs[0].is_empty()) {
+        outputs[0] = TensorView(shape, DataType::s8, nullptr, cols, TensorLayout::PackedBHip, raw.quant_params());
+        return Status::ok;
+    }
+    const TensorView& o = outputs[0];
+    if (o.layout() != TensorLayout::PackedBHip || o.data_type() != DataType::s8 || o.rank() != 2 ||
+        o.shape(0) != n || o.shape(1) != cols) {
+        return Status::invalid_argument;  // the packed buffer does not match the geometry
+    }
+    const int rc = nnops_hip_prepack_i8(raw.ptr<const int8_t>(), k, n, raw.row_stride_elems(), trans_b ? 1 : 0,
+                                        o.ptr<void>(), ctx.hip_stream);
+    return from_code(rc);
+}
+
+}  // namespace
+
+Status MatMul::prepack(std::span<const TensorView> inputs, std::span<TensorView> outputs, const ComputeContext& ctx)
+{
+    if (inputs.empty()) {
+        return Status::invalid_argument;
+    }
+    return prepack_s8(inputs[0], attrs_.transpose_b, outputs, ctx, backend_);
+}
+
+void MatMul::prepackWeights(std::span<const TensorView> inputs, std::span<TensorView> outputs,
+                            const ComputeContext& ctx)
+{
+    (void)prepack(inputs, outputs, ctx);
+}
+
+Status Linear::prepack(std::span<const TensorView> inputs, std::span<TensorView> outputs, const ComputeContext& ctx)
+{
+    if (inputs.empty()) {
+        return Status::invalid_argument;
+    }
+    return prepack_s8(inputs[0], true, outputs, ctx, backend_);  // the weight is [N, K]
+}
+
+void Linear::prepackWeights(std::span<const TensorView> inputs, std::span<TensorView> outputs,
+                            const ComputeContext& ctx)
+{
+    (void)prepack(inputs, outputs, ctx);
 }
 
 }  // namespace nnops

@@ -1371,6 +1371,29 @@ __global__ __launch_bounds__(256) void rowsum_i8(const int8_t* src, int64_t ld, 
     }
 }
 
+// Row copy into a wider, zero-padded pitch (the prepack of an [N,K] B):
+// 16 bytes per thread where source and destination allow it.
+__global__ __launch_bounds__(256) void pad_rows_i8(const int8_t* src, int64_t lds_, int R, int C,
+                                                  int8_t* dst, int64_t ldd)
+{
+    const int64_t chunks = ldd / 16;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)R * chunks) {
+        return;
+    }
+    const int r = (int)(t / chunks);
+    const int c0 = (int)(t - (int64_t)r * chunks) * 16;
+    const int8_t* s = src + (int64_t)r * lds_;
+    int8_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        v[i] = c0 + i < C ? s[c0 + i] : (int8_t)0;
+    }
+    int4 o;
+    __builtin_memcpy(&o, v, 16);
+    *reinterpret_cast<int4*>(dst + (int64_t)r * ldd + c0) = o;
+}
+
 // ---------------------------------------------------------------------------
 // Host side: workspace plan and dispatch.
 // ---------------------------------------------------------------------------
@@ -1661,6 +1684,47 @@ int choose_epi(const NnopsGemmI8Args& g, const EpiParams& e)
 
 using namespace nnops_amd;
 
+namespace {
+int64_t prepack_pitch(int64_t k) { return (k + 127) / 128 * 128; }
+}  // namespace
+
+extern "C" size_t nnops_hip_prepack_i8_bytes(int64_t k, int64_t n)
+{
+    if (k < 0 || n < 0) {
+        return 0;
+    }
+    return align_up((size_t)n * (size_t)prepack_pitch(k)) + (size_t)n * 4;
+}
+
+extern "C" int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int32_t trans_b,
+                                    void* out, void* stream)
+{
+    if (k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    if (k == 0 || n == 0) {
+        return NNOPS_OK;
+    }
+    if (b == nullptr || out == nullptr || (uintptr_t)out % 256 != 0 || ldb < (trans_b ? k : n)) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t kp = prepack_pitch(k);
+    int8_t* rows = static_cast<int8_t*>(out);
+    int32_t* sums = reinterpret_cast<int32_t*>(static_cast<char*>(out) + align_up((size_t)n * (size_t)kp));
+    if (trans_b) {
+        const int64_t threads = n * (kp / 16);
+        hipLaunchKernelGGL(pad_rows_i8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, b, ldb, (int)n,
+                           (int)k, rows, kp);
+    } else {
+        dim3 grid((unsigned)((n + 63) / 64), (unsigned)((kp + 63) / 64));
+        hipLaunchKernelGGL(transpose_i8, grid, dim3(256), 0, s, b, ldb, (int)k, (int)n, rows, kp, (int)kp);
+    }
+    hipLaunchKernelGGL(rowsum_i8, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rows, kp, (int)n, (int)k, 0,
+                       sums);
+    return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+}
+
 extern "C" size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* g)
 {
     if (g == nullptr) {
@@ -1777,7 +1841,9 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     const bool need_rb = g->a_u8 || g->zp_a != nullptr || g->zp_a_scalar != 0;
     const bool need_ra = g->zp_b != nullptr || g->zp_b_scalar != 0;
     e.compensate = need_ra || need_rb;
-    if (need_rb) {
+    if (need_rb && g->b_col_sums != nullptr) {
+        e.r_b = g->b_col_sums;
+    } else if (need_rb) {
         int32_t* rb = reinterpret_cast<int32_t*>(ws + w.r_b);
         hipLaunchKernelGGL(rowsum_i8, dim3((unsigned)((g->n + 3) / 4)), dim3(256), 0, s, k.b, k.ldb,
                            (int)g->n, (int)g->k, 0, rb);

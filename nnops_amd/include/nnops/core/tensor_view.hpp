@@ -23,6 +23,11 @@ namespace nnops {
 enum class TensorLayout : uint8_t {
     PackedB = 10,
     Dense = 12,
+    /// The HIP backend's prepacked matmul B (MatMul / Linear ::prepackWeights):
+    /// an s8 weight as [N][kp] k-contiguous rows (kp = K rounded up to 128,
+    /// zero padded) followed by its int32 column sums. Shape [N, ceil(bytes/N)]
+    /// like nnops' PackedB; appended after nnops' last tag (17).
+    PackedBHip = 18,
 };
 
 struct TensorDesc {

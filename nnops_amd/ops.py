@@ -152,6 +152,32 @@ class _Op:
         ao, no = self._arr(outputs)
         return L.lib().nnops_op_workspace_size(self._h, ai, ni, ao, no)
 
+    def prepack(self, weight, *, stream=None, device="cuda"):
+        """prepackWeights: query the packed form of ``weight`` (an NnopsTensor
+        from :func:`tensor`), allocate it (torch, device memory) and fill it.
+        Returns ``(buffer, packed)`` -- ``packed`` is the NnopsTensor to pass as
+        the B / weight input -- or ``(None, None)`` when the weight has no
+        packed form."""
+        import torch
+        ins = (L.Tensor * 1)(weight)
+        out = (L.Tensor * 1)()
+        rc = L.lib().nnops_op_prepack_weights(self._h, ins, 1, out, 1, None)
+        if rc != 0:
+            raise ValueError(f"prepack query failed: status {rc}")
+        d = out[0]
+        if d.rank == 0:
+            return None, None
+        nbytes = d.dims[0] * d.pitch
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        d.data = buf.data_ptr()
+        out[0] = d
+        rc = L.lib().nnops_op_prepack_weights(self._h, ins, 1, out, 1, _stream_ptr(stream))
+        if rc != 0:
+            raise ValueError(f"prepack failed: status {rc}")
+        packed = out[0]
+        packed._keep = [buf] + list(getattr(weight, "_keep", []))
+        return buf, packed
+
     def compute(self, outputs, inputs, *, stream=None, workspace=None, device="cuda"):
         """Run compute(); allocates a workspace of workspace_size() bytes when
         none is given. Returns the nnops Status code."""

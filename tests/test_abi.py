@@ -211,3 +211,37 @@ def test_quant_linear_descriptors_and_validate():
     o.data = 512
     assert na.QuantizeLinear(backend=na.BACKEND_CPU).compute([o], [x, s, z], stream=0, workspace=0) \
         == na.UNSUPPORTED
+
+
+def test_prepack_query_descriptor():
+    # query: [N, ceil(bytes / N)] s8 PackedBHip (no launch); non-s8 answers empty
+    lib = na.lib()
+    op = na.MatMul(output_dtype=na.DT_S8)             # B [K, N]
+    w = desc([300, 100], na.DT_S8)
+    ins = (L.Tensor * 1)(w)
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(op._h, ins, 1, out, 1, None) == na.OK
+    kp = 384
+    nbytes = ((100 * kp + 255) // 256) * 256 + 4 * 100
+    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == -(-nbytes // 100)
+    assert out[0].dtype == na.DT_S8 and out[0].layout == L.LAYOUT_PACKED_B_HIP
+    assert out[0].pitch == out[0].dims[1]
+    assert lib.nnops_hip_prepack_i8_bytes(300, 100) == nbytes
+    # Linear: the weight is [N, K]
+    lop = na.Linear(output_dtype=na.DT_S8)
+    ins = (L.Tensor * 1)(desc([100, 300], na.DT_S8))
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(lop._h, ins, 1, out, 1, None) == na.OK
+    assert out[0].dims[0] == 100 and out[0].dims[1] == -(-nbytes // 100)
+    # q4_1 / f32 weights: no packed form
+    ins = (L.Tensor * 1)(desc([64, 16], na.DT_F32))
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(op._h, ins, 1, out, 1, None) == na.OK
+    assert out[0].rank == 0
+    # a packed B: output descriptor from its N and A's K; a blob too small for K is rejected
+    packed = desc([100, -(-nbytes // 100)], na.DT_S8)
+    packed.layout = L.LAYOUT_PACKED_B_HIP
+    shape, dt = op.output_desc([desc([7, 300], na.DT_S8), packed])
+    assert shape == [7, 100] and dt == na.DT_S8
+    assert op.validate([desc([7, 300], na.DT_S8), packed], [desc([7, 100], na.DT_S8)]) == na.OK
+    assert op.validate([desc([7, 600], na.DT_S8), packed], [desc([7, 100], na.DT_S8)]) == na.INVALID_ARGUMENT

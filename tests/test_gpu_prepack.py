@@ -1,0 +1,99 @@
+"""prepackWeights on the GPU: the packed s8 weight (TensorLayout PackedBHip)
+gives bit-for-bit the result of the raw weight on every route (GEMV, small-M
+MFMA, ring GEMM, split K), for [K,N] and [N,K] raw forms, with the precomputed
+column sums standing in for the per-call pass (u8 A, A zero points), and
+through the fp-activation and dequantizing routes."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import datagen as dg
+import nnops_amd as na
+from gpu_util import dev, host, announce
+
+pytestmark = pytest.mark.gpu
+
+
+def run(op, a_t, w_t, out_dtype, shape):
+    import torch
+    c = torch.zeros(shape, dtype=out_dtype, device="cuda")
+    assert op.compute([na.tensor(c)], [a_t, w_t]) == na.OK
+    torch.cuda.synchronize()
+    return host(c)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1008), (3, 640, 200), (16, 1024, 512), (100, 512, 333),
+                                   (512, 4096, 1024), (333, 2048, 512), (5, 100, 37)])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("u8", [False, True])
+def test_matmul_prepacked_matches_raw(M, K, N, trans_b, u8):
+    import torch
+    announce(f"prepack matmul {M}x{K}x{N} tb={trans_b} u8={u8}")
+    seed = M + K + N + 2 * trans_b + 4 * u8
+    a = dg.ints(seed, (M, K), 0, 255, np.uint8) if u8 else dg.act_s8(seed, (M, K))
+    b = dg.ints(seed + 1, (N, K) if trans_b else (K, N), -127, 127)
+    sb = dg.uniform(seed + 2, (N,), 0.001, 0.01)
+    zp_a = 128 if u8 else 3
+    op = na.MatMul(output_dtype=na.DT_S8, transpose_b=trans_b, act=na.EP_RELU)
+    wt = na.tensor(dev(b), scale_data=sb, granularity=2)
+    buf, packed = op.prepack(wt)
+    assert packed is not None and packed.layout == na.LAYOUT_PACKED_B_HIP
+    at = na.tensor(dev(a), scale=0.02, zero_point=zp_a)
+    got_p = run(op, at, packed, torch.int8, (M, N))
+    got_r = run(op, at, wt, torch.int8, (M, N))
+    np.testing.assert_array_equal(got_p, got_r)
+    # and against the oracle with an output scale
+    c = torch.zeros((M, N), dtype=torch.int8, device="cuda")
+    assert op.compute([na.tensor(c, scale=0.05)], [at, packed]) == na.OK
+    torch.cuda.synchronize()
+    want = oracle.gemm_i8(a, b, trans_b=trans_b, out_kind=oracle.OUT_S8, s_a=0.02, zp_a=zp_a, s_b=sb,
+                          s_out=0.05, act=oracle.ACT_RELU)
+    np.testing.assert_array_equal(host(c), want)
+
+
+@pytest.mark.parametrize("M", [1, 16, 300])
+def test_linear_prepacked_s32_and_f16(M):
+    import torch
+    announce(f"prepack linear M={M}")
+    K, N = 1536, 384
+    x = dg.act_s8(70 + M, (M, K))
+    w = dg.ints(71, (N, K), -127, 127)
+    for odt, tdt, ok in ((na.DT_S32, torch.int32, oracle.OUT_S32), (na.DT_F16, torch.float16, oracle.OUT_F16)):
+        op = na.Linear(output_dtype=odt)
+        wt = na.tensor(dev(w), scale=0.004)
+        _, packed = op.prepack(wt)
+        got = run(op, na.tensor(dev(x), scale=0.02), packed, tdt, (M, N))
+        want = oracle.gemm_i8(x, w, trans_b=True, out_kind=ok, s_a=0.02, s_b=0.004)
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_matmul_fp_activation_prepacked():
+    import torch
+    announce("prepack fp-A matmul")
+    M, K, N = 24, 1024, 256
+    a = dg.normal(81, (M, K), 2.0).astype(np.float16)
+    b = dg.ints(82, (K, N), -127, 127)
+    s_a = dg.uniform(83, (M,), 0.01, 0.03)
+    zp_a = dg.ints(84, (M,), -5, 5, np.int32)
+    op = na.MatMul()
+    _, packed = op.prepack(na.tensor(dev(b), scale=0.003))
+    at = na.tensor(dev(a), scale_data=s_a, zero_point_data=zp_a, granularity=1)
+    got = run(op, at, packed, torch.float16, (M, N))
+    aq = oracle.quantize_linear(a, s_a, zp_a, axis=-1)
+    want = oracle.gemm_i8(aq, b, out_kind=oracle.OUT_F16, s_a=s_a, zp_a=zp_a, s_b=0.003)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_prepack_rejects_mismatched_buffer_and_k():
+    import torch
+    announce("prepack rejects")
+    K, N = 256, 64
+    b = dg.ints(91, (K, N), -127, 127)
+    op = na.MatMul(output_dtype=na.DT_S32)
+    _, packed = op.prepack(na.tensor(dev(b)))
+    # an A whose K needs a larger blob than this one
+    a = dg.act_s8(92, (4, 512))
+    c = torch.zeros((4, N), dtype=torch.int32, device="cuda")
+    assert op.compute([na.tensor(c)], [na.tensor(dev(a)), packed]) == na.INVALID_ARGUMENT
