@@ -126,3 +126,58 @@ def test_linear_q4_1_f16():
     want = oracle.gemm_q4_1(x, blk, N, trans_b=True)
     from gpu_util import norm_err
     assert norm_err(host(y), want) <= 2e-3
+
+
+def test_linear_from_gguf_q4_1_and_i8(tmp_path):
+    """A GGUF file's Q4_1 and I8 tensors, read through the memory map and
+    uploaded, drive Linear directly (the [N][K/32] block rows are the Linear
+    weight form)."""
+    import torch
+    from nnops_amd import gguf
+    announce("linear from gguf")
+    M, K, N = 3, 1024, 200
+    blk = dg.q4_1_blocks(121, N, K)
+    w8 = dg.ints(122, (N, K), -127, 127)
+    p = str(tmp_path / "m.gguf")
+    gguf.write_gguf(p, {"q": (gguf.GGML_Q4_1, (K, N), blk.tobytes()), "i": (gguf.GGML_I8, (K, N), w8.tobytes())})
+    g = gguf.open_gguf(p)
+    wq, dtq, (n, k) = gguf.load_weight(g, "q")
+    wi, dti, _ = gguf.load_weight(g, "i")
+    g.close()
+    assert (n, k) == (N, K) and dtq == na.DT_Q4_1 and dti == na.DT_S8
+    x = dg.normal(123, (M, K)).astype(np.float16)
+    y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    assert na.Linear().compute([na.tensor(y)], [na.tensor(dev(x)), na.tensor(wq, dtype=dtq, shape=[N, K])]) == na.OK
+    xs = dg.act_s8(124, (M, K))
+    yi = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    assert na.Linear(output_dtype=na.DT_S32).compute([na.tensor(yi)], [na.tensor(dev(xs)), na.tensor(wi)]) == na.OK
+    torch.cuda.synchronize()
+    want = oracle.gemm_q4_1(x, blk, N, trans_b=True, w_round_f16=True, c_f16=True).astype(np.float32)
+    from gpu_util import norm_err
+    assert norm_err(host(y).astype(np.float32), want) <= 2e-3
+    np.testing.assert_array_equal(host(yi), oracle.gemm_i8(xs, w8, trans_b=True))
+
+
+def test_matmul_rank6_broadcast():
+    """Rank-6 operands with broadcast on several leading axes (nnops' batch
+    walk, matmul_internal.h:90-151; its CUDA ceiling is rank 6)."""
+    import torch
+    announce("matmul rank6")
+    a_shape = (2, 1, 3, 1, 5, 64)
+    b_shape = (1, 2, 1, 2, 64, 24)
+    a = dg.ints(131, a_shape, -127, 127)
+    b = dg.ints(132, b_shape, -127, 127)
+    out_shape = (2, 2, 3, 2, 5, 24)
+    c = torch.zeros(out_shape, dtype=torch.int32, device="cuda")
+    op = na.MatMul()
+    ins = [na.tensor(dev(a)), na.tensor(dev(b))]
+    shape, dt = op.output_desc(ins)
+    assert tuple(shape) == out_shape
+    assert op.compute([na.tensor(c)], ins) == na.OK
+    torch.cuda.synchronize()
+    got = host(c)
+    for idx in np.ndindex(*out_shape[:-2]):
+        ia = tuple(i if d > 1 else 0 for i, d in zip(idx, a_shape[:-2]))
+        ib = tuple(i if d > 1 else 0 for i, d in zip(idx, b_shape[:-2]))
+        np.testing.assert_array_equal(got[idx], oracle.gemm_i8(np.ascontiguousarray(a[ia]),
+                                                               np.ascontiguousarray(b[ib])))
