@@ -403,6 +403,8 @@ def main():
     if not args.no_secondary:
         secondary["cfg3_int8_gemv_m1_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, trans_b=True)
         secondary["cfg3_int8_gemv_m1_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, trans_b=False)
+        secondary["cfg3_int8_gemv_m4_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=4,
+                                                         trans_b=True)
         secondary["cfg3_int8_gemv_m16_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
                                                           trans_b=True)
         secondary["cfg3_int8_gemv_m16_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,

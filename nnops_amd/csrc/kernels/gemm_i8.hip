@@ -8,7 +8,9 @@
 //                  fragment reads of 8 consecutive rows hit disjoint banks),
 //                  double-buffered global->register->LDS, v_mfma_i32_32x32x32_i8.
 //                  Bound: MFMA (4096^3: arithmetic intensity ~2730 op/B).
-//   gemv_i8_mfma   M <= 16: one 16-column slice of B per block, K split over
+//   gemv_i8_lds    4 < M <= 16, B [N][K]: 16 rows of B per block staged through
+//                  LDS in 1 KiB row pieces, v_mfma_i32_16x16x64_i8.
+//   gemv_i8_mfma   M <= 16 otherwise: one 16-column slice of B per block, K split over
 //                  the block's 4 waves, fragments loaded straight from HBM into
 //                  v_mfma_i32_16x16x64_i8 operands (no LDS on the weight path),
 //                  partial tiles summed through LDS. Bound: HBM (weight bytes).
@@ -1011,6 +1013,19 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
         return;
     }
     int8_t* c8 = reinterpret_cast<int8_t*>(crow) + nb;
+    if (((uintptr_t)c8 & 3) == 0) {
+        // one 4-byte read of the residual and one 4-byte store
+        const uint32_t oldw = ep.add_to ? *reinterpret_cast<const uint32_t*>(c8) : 0u;
+        uint32_t outw = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
+            const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
+            outw |= ((uint32_t)epi_value(ep, row, epi_col(ep, nb + e), raw[e], old) & 0xffu) << (8 * e);
+        }
+        *reinterpret_cast<uint32_t*>(c8) = outw;
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int32_t old = ep.add_to ? (u8 ? (int32_t)((const uint8_t*)c8)[e] : (int32_t)c8[e]) : 0;
@@ -1053,6 +1068,94 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma(GemmI8Kern p)
         for (int u = 0; u < U; ++u) {
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u], fb[u], acc, 0, 0, 0);
         }
+    }
+
+    if (wave > 0) {
+        red[wave - 1][lane] = acc;
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+        acc += red[w][lane];
+    }
+    // 16x16 layout: lane holds column (lane & 15), rows 4*(lane/16) + r.
+    const int n = n0 + (lane & 15);
+    if (n >= p.n) {
+        return;
+    }
+    const EpiCol c = epi_col(p.ep, n);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * (lane >> 4) + r;
+        if (m < p.m) {
+            const EpiRow row = epi_row(p.ep, m);
+            char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+            epi_store(p.ep, row, c, acc[r], crow, n);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM, 4 < M <= 16, B k-contiguous ([N][K], 16-byte aligned rows):
+// one block per 16 rows of B (16 output columns), its W waves splitting K in
+// 1 KiB pieces (wave w: k = 1024 w + 1024 W j). Each wave moves its 16 rows x
+// 1 KiB of B into LDS with one direct-to-LDS load per row (1 KiB of whole
+// cache lines per instruction, where the register-fed GEMV's fragment loads
+// fetch 64-byte half lines) while its A fragments (16 rows x 1 KiB, from L2)
+// go to registers; then 16 v_mfma_i32_16x16x64_i8 read B back from LDS (row
+// pitch 1040 bytes: a fragment read's 16 rows fall in distinct bank groups).
+// K tails: A reads zero past K; B reads past the block's last row come back
+// zero from the buffer's range check. Bound: HBM (the B stream).
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(W * 64) void gemv_i8_lds(GemmI8Kern p)
+{
+    constexpr int KW = 1024;                         // k bytes per wave piece
+    constexpr int PITCH = KW + 16;                   // LDS row pitch
+    constexpr int T = KW / 64;                       // MFMAs per piece
+    __shared__ __attribute__((aligned(16))) int8_t stage[W][16 * PITCH];
+    __shared__ v4i red[W - 1][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int rows = min(16, p.n - n0);
+    const int64_t span = (int64_t)(rows - 1) * p.ldb + p.k;
+#if __HIP_DEVICE_COMPILE__
+    const BufRsrc rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.b + (int64_t)n0 * p.ldb), 0,
+                                                         (int)span, 0x00020000);
+#else
+    const BufRsrc rs{};
+#endif
+    const int arow = lane & 15;
+    const bool a_live = arow < p.m;
+    const int8_t* a_row = p.a + (int64_t)(a_live ? arow : 0) * p.lda;
+    const int kq = (lane >> 4) * 16;
+    int8_t* st = stage[wave];
+
+    v4i acc = {0, 0, 0, 0};
+    for (int kb = wave * KW; kb < p.k; kb += W * KW) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            buffer_load_lds16(rs, st + r * PITCH, (int)((int64_t)r * p.ldb) + kb + lane * 16, 0);
+        }
+        v4i fa[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            fa[t] = a_live ? load16_a<true>(a_row, kb + 64 * t + kq, p.k, p.a_xor) : v4i{0, 0, 0, 0};
+        }
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const v4i fb = *reinterpret_cast<const v4i*>(st + arow * PITCH + 64 * t + kq);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[t], fb, acc, 0, 0, 0);
+        }
+        // the next piece's loads overwrite this stage: its reads must be done
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
     }
 
     if (wave > 0) {
@@ -1461,8 +1564,8 @@ inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 
 
 // The ring kernel needs 64-byte k steps, 16-byte-aligned k-contiguous rows,
 // N % 4 == 0 (int32 groups), and 32-bit buffer offsets within a row panel.
-// Tile shape by M: 384x128 covers a 257..384-row problem in one M tile,
-// 128x256 and 256x128 the small ones, 256x256 the rest. K is split when the
+// Tile shape by M: a 257..384-row problem takes two 192x128 tiles (384x128 when
+// K % 128 != 0), 128x256 and 256x128 the small ones, 256x256 the rest. K is split when the
 // tiles alone do not fill the 256 CUs (at least 8 k steps per split). The
 // fused output modes need row-uniform parameters, no zero-point terms,
 // half-away rounding, 16-byte-aligned tables and destination, and no split;
@@ -1473,7 +1576,11 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     if (g.m <= 16 || g.k % 64 != 0 || g.n % 4 != 0 || g.m < 64 || !aligned16(a, lda) || !aligned16(b, ldb)) {
         return r;
     }
-    if (g.m > 256 && g.m <= 384) {
+    if (g.m > 256 && g.m <= 384 && g.k % 128 == 0) {
+        // two 192-row tiles: twice the tiles of one 384-row tile, so half the
+        // K splits (and half the partial-sum traffic) fill the CUs
+        r.bm = 192; r.bn = 128;
+    } else if (g.m > 256 && g.m <= 384) {
         r.bm = 384; r.bn = 128;
     } else if (g.m <= 128) {
         r.bm = 128; r.bn = 256;
@@ -1594,7 +1701,7 @@ void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode,
 {
     if (bk == 128) {
         launch_ring_bk<BM, BN, WM, WN, 128, 2>(k, sk, mode, flip, s);
-    } else {
+    } else if constexpr (BM % (16 * WM * WN) == 0 && BN % (16 * WM * WN) == 0) {
         launch_ring_bk<BM, BN, WM, WN, 64, 4>(k, sk, mode, flip, s);
     }
 }
@@ -1652,6 +1759,8 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
     const bool flip = k.a_xor != 0u;
     if (r.bm == 384) {
         launch_ring_cfg<384, 128, 4, 2>(k, sk, r.bk, r.mode, flip, s);
+    } else if (r.bm == 192) {
+        launch_ring_cfg<192, 128, 2, 4>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bm == 128) {
         launch_ring_cfg<128, 256, 2, 4>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bn == 128) {
@@ -1686,6 +1795,13 @@ using namespace nnops_amd;
 
 namespace {
 int64_t prepack_pitch(int64_t k) { return (k + 127) / 128 * 128; }
+
+// The LDS skinny GEMM: M 5..16 (M <= 4 streams faster through the row GEMV),
+// a block's 16 rows within a 32-bit buffer range.
+bool gemv_lds_ok(const NnopsGemmI8Args& g)
+{
+    return g.m > 4 && (int64_t)16 * g.ldb + g.k < (int64_t)INT32_MAX;
+}
 }  // namespace
 
 extern "C" size_t nnops_hip_prepack_i8_bytes(int64_t k, int64_t n)
@@ -1861,16 +1977,23 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     const int epi = choose_epi(*g, e);
     if (w.kn.cpl != 0) {
         launch_kn(k, w.kn, reinterpret_cast<int32_t*>(ws + w.part), s);
+    } else if (g->m <= 16 && aligned && g->k % 64 == 0 && gemv_lds_ok(*g)) {
+        hipLaunchKernelGGL((gemv_i8_lds<4>), dim3((unsigned)((g->n + 15) / 16)), dim3(256), 0, s, k);
     } else if (g->m <= 4 && aligned) {
-        constexpr int R = 1;
-        const unsigned blocks = (unsigned)((g->n + 4 * R - 1) / (4 * R));
         const bool flip = k.a_xor != 0u;
-#define NNOPS_ROWS(MT)                                                                              \
-        if (flip) {                                                                                 \
-            hipLaunchKernelGGL((gemv_i8_rows<MT, R, true>), dim3(blocks), dim3(256), 0, s, k);      \
-        } else {                                                                                    \
-            hipLaunchKernelGGL((gemv_i8_rows<MT, R, false>), dim3(blocks), dim3(256), 0, s, k);     \
+        // two rows per wave from M = 3: halves the A re-reads per weight byte
+        const int rsel = g->m >= 3 ? 2 : 1;
+#define NNOPS_ROWS_R(MT, R)                                                                         \
+        {                                                                                           \
+            const unsigned blocks = (unsigned)((g->n + 4 * R - 1) / (4 * R));                      \
+            if (flip) {                                                                             \
+                hipLaunchKernelGGL((gemv_i8_rows<MT, R, true>), dim3(blocks), dim3(256), 0, s, k);  \
+            } else {                                                                                \
+                hipLaunchKernelGGL((gemv_i8_rows<MT, R, false>), dim3(blocks), dim3(256), 0, s, k); \
+            }                                                                                       \
         }
+#define NNOPS_ROWS(MT)                                                                              \
+        if (rsel == 2) NNOPS_ROWS_R(MT, 2) else NNOPS_ROWS_R(MT, 1)
         if (g->m == 1) {
             NNOPS_ROWS(1)
         } else if (g->m == 2) {
@@ -1878,6 +2001,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         } else {
             NNOPS_ROWS(4)
         }
+#undef NNOPS_ROWS_R
 #undef NNOPS_ROWS
     } else if (g->m <= 16) {
         const unsigned blocks = (unsigned)((g->n + 15) / 16);
