@@ -22,6 +22,7 @@
 //                  f32, rounded once) into LDS, A tiles staged k-contiguous.
 #include "common.hpp"
 
+
 #include <utility>
 
 namespace nnops_amd {
@@ -1003,12 +1004,15 @@ __device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v
     return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
 }
 
-template <bool OUT16, int NS>
-__global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
+template <bool OUT16, int NS, int WM>
+__global__ __launch_bounds__(256 * WM, 1) void gemm_q4_1_ring(Q41Kern p)
 {
-    static_assert(NS >= 3 && (NS - 2) * 8 < 64, "stages");
+    constexpr int W = 4 * WM;                       // waves: WM along M x 4 along N
+    constexpr int QA = 16 / W, QB = 16 / W;         // 1 KiB pieces per wave per stage
+    constexpr int L = QA + QB;
+    static_assert(NS >= 3 && (NS - 2) * L < 64, "stages");
     constexpr int BM = 128, BN = 256;
-    constexpr int TN = 64, FM = 4, FN = 2;
+    constexpr int TM = BM / WM, TN = 64, FM = TM / 32, FN = 2;
     constexpr int kA = BM * 128, kB = BN * 64, kStage = kA + kB;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
 
@@ -1022,7 +1026,8 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn0 = wave * TN;
+    const int wn0 = (wave % 4) * TN;
+    const int wm0 = (wave / 4) * TM;
     const int kt = p.k / 64;
 
     // A: rows 8 * (4 * wave + i) + lane / 8; B raw: rows 16 * (4 * wave + i) + lane / 4
@@ -1030,25 +1035,28 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
     const int64_t b_bytes = (int64_t)(p.n - n0) * p.ldb;
     const QBufRsrc rsb = q_buffer_rsrc(p.b + (int64_t)n0 * p.ldb,
                                        (uint32_t)std::min<int64_t>(b_bytes, 0x7fffffff));
-    int a_off[4], b_off[4];
+    int a_off[QA], b_off[QB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int ra = 8 * (4 * wave + i) + (lane >> 3);
+    for (int i = 0; i < QA; ++i) {
+        const int ra = 8 * (QA * wave + i) + (lane >> 3);
         const int ca = (lane & 7) ^ ((ra >> 1) & 7);
         a_off[i] = min(ra, p.m - 1 - m0) * (int)p.lda * 2 + ca * 16;
-        const int rb = 16 * (4 * wave + i) + (lane >> 2);
+    }
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+        const int rb = 16 * (QB * wave + i) + (lane >> 2);
         const int cb = (lane & 3) ^ ((rb >> 2) & 3);
         b_off[i] = min(rb, p.n - 1 - n0) * (int)p.ldb + cb * 16;
     }
     auto issue = [&](int s) {
         uint8_t* base = ring + (s % NS) * kStage;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q_buffer_load_lds16(rsa, base + (4 * wave + i) * 1024, a_off[i], s * 128);
+        for (int i = 0; i < QA; ++i) {
+            q_buffer_load_lds16(rsa, base + (QA * wave + i) * 1024, a_off[i], s * 128);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q_buffer_load_lds16(rsb, base + kA + (4 * wave + i) * 1024, b_off[i], s * 40);
+        for (int i = 0; i < QB; ++i) {
+            q_buffer_load_lds16(rsb, base + kA + (QB * wave + i) * 1024, b_off[i], s * 40);
         }
     };
 
@@ -1056,7 +1064,7 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
     // wn0 + 32 j + (lane & 31); k values 16 ks + 8 (lane >> 5) .. + 7
     const int fr = lane & 31, kh = lane >> 5;
     auto a_frag = [&](const uint8_t* st, int i, int ks) {
-        const int r = i * 32 + fr;
+        const int r = wm0 + i * 32 + fr;
         const int c = (2 * ks + kh) ^ ((r >> 1) & 7);
         return *reinterpret_cast<const v8h*>(st + r * 128 + c * 16);
     };
@@ -1064,20 +1072,20 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
         const int c = (byte >> 4) ^ ((r >> 2) & 3);
         return *reinterpret_cast<const uint32_t*>(row + c * 16 + (byte & 15));
     };
-    auto b_frag = [&](const uint8_t* st, int j, int ks) {
+    // B fragments of both slices of one block (ks = 2 blk, 2 blk + 1): the
+    // lane's 8 nibble bytes hold its values of the first slice in their low
+    // nibbles and of the second in their high ones, so one read of d/m and
+    // the 8 bytes decodes both
+    auto b_frag2 = [&](const uint8_t* st, int j, int blk, v8h& lo, v8h& hi) {
         const int r = wn0 + 32 * j + fr;
         const uint8_t* row = st + kA + r * 64;
-        const int blk = ks >> 1;                            // block of the stage
-        const int v0 = 16 * (ks & 1) + 8 * kh;              // first value within the block
         const uint32_t dm = b_dword(row, r, 20 * blk);
-        const int nb0 = 20 * blk + 4 + (v0 & 15);           // first nibble byte
-        uint32_t w0 = b_dword(row, r, nb0), w1 = b_dword(row, r, nb0 + 4);
-        const int sh = v0 >= 16 ? 4 : 0;
-        w0 = (w0 >> sh) & 0x0f0f0f0fu;
-        w1 = (w1 >> sh) & 0x0f0f0f0fu;
+        const int nb0 = 20 * blk + 4 + 8 * kh;               // first nibble byte
+        const uint32_t w0 = b_dword(row, r, nb0), w1 = b_dword(row, r, nb0 + 4);
         const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x01000100u));
         const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x03020302u));
-        return decode8_f16(w0, w1, d2, m2);
+        lo = decode8_f16(w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, d2, m2);
+        hi = decode8_f16((w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu, d2, m2);
     };
 
     v16f acc[FM][FN];
@@ -1097,23 +1105,26 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
         }
     }
     if (kt >= NS - 1) {
-        wait_vmcnt<(NS - 2) * 8>();
+        wait_vmcnt<(NS - 2) * L>();
     } else {
         wait_vmcnt<0>();
     }
     __syncthreads();
 
-    // Within a step the fragments of slice ks+1 are read and decoded while the
-    // matrix cores run slice ks (two register sets, alternating).
-    v8h fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-    auto load_frags = [&](const uint8_t* st, int ks, v8h (&fa)[FM], v8h (&fb)[FN]) {
+    // Within a step the fragments of the next slice are read and decoded
+    // while the matrix cores run this one (B for both slices of a block at
+    // once; two register sets, alternating).
+    v8h fa0[FM], fb0[FN], fa1[FM], fb1[FN], fb2[FN], fb3[FN];
+    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[FM]) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             fa[i] = a_frag(st, i, ks);
         }
+    };
+    auto load_b = [&](const uint8_t* st, int blk, v8h (&lo)[FN], v8h (&hi)[FN]) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            fb[j] = b_frag(st, j, ks);
+            b_frag2(st, j, blk, lo[j], hi[j]);
         }
     };
     auto mfma_slice = [&](const v8h (&fa)[FM], const v8h (&fb)[FN]) {
@@ -1132,19 +1143,21 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
         if (more) {
             issue(t + NS - 1);
         }
-        load_frags(st, 0, fa0, fb0);
-        load_frags(st, 1, fa1, fb1);
+        load_b(st, 0, fb0, fb1);
+        load_a(st, 0, fa0);
+        load_a(st, 1, fa1);
         mfma_slice(fa0, fb0);
-        load_frags(st, 2, fa0, fb0);
+        load_b(st, 1, fb2, fb3);
+        load_a(st, 2, fa0);
         mfma_slice(fa1, fb1);
-        load_frags(st, 3, fa1, fb1);
-        mfma_slice(fa0, fb0);
-        mfma_slice(fa1, fb1);
+        load_a(st, 3, fa1);
+        mfma_slice(fa0, fb2);
+        mfma_slice(fa1, fb3);
         // stage t+1 landed for this wave (issued NS-2 steps ago; every later
         // stage may be in flight); the barrier makes every wave's pieces visible
         // and frees slot t for step t+1's issue
         if (more) {
-            wait_vmcnt<(NS - 2) * 8>();
+            wait_vmcnt<(NS - 2) * L>();
         } else {
             wait_vmcnt<0>();
         }
@@ -1164,7 +1177,7 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_ring(Q41Kern p)
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < p.m) {
                     if constexpr (OUT16) {
                         static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)acc[i][j][r];
@@ -1310,9 +1323,9 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         // blocks along K: the ring kernel (A by DMA, B decoded in registers)
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
         if (k.out_f16) {
-            hipLaunchKernelGGL((gemm_q4_1_ring<true, 5>), dim3(tiles), dim3(256), 0, s, k);
+            hipLaunchKernelGGL((gemm_q4_1_ring<true, 5, 1>), dim3(tiles), dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_ring<false, 5>), dim3(tiles), dim3(256), 0, s, k);
+            hipLaunchKernelGGL((gemm_q4_1_ring<false, 5, 1>), dim3(tiles), dim3(256), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
