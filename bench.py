@@ -316,10 +316,12 @@ def measured_traffic(kernel_key):
 
 
 def cpu_baseline(seconds):
-    """The CPU oracle on a bounded sample of config 2: rows of the same
-    4096^3 problem, split over this host's cores with one oracle call per row
-    block (ctypes releases the GIL). Prefers the reference's compiled oracle
-    (nnops tests/reference/matmul_int8_ref) when oracle/_ref was built."""
+    """nnops' own CPU path on a bounded sample of config 2: its MatMul int8
+    route (AVX-512-VNNI panels, compiled from the reference sources into
+    oracle/_ref/libnnops_cpu.so) on row blocks of the same 4096^3 problem, one
+    call per block over a std::thread pool of this host's cores. Falls back to
+    the reference's naive oracle (tests/reference/matmul_int8_ref) and then to
+    the oracle port when those are what this host has."""
     import concurrent.futures as cf
     import numpy as np
     import oracle
@@ -329,10 +331,26 @@ def cpu_baseline(seconds):
     w = dg.ints(202, (N, K), -127, 127)
     sb = dg.uniform(203, (N,), 0.001, 0.01)
     bias = dg.ints(204, (N,), -5000, 5000, np.int32)
-    ref = oracle.ref_lib()
     cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    rows_per = 8
     out = np.zeros((M, N), np.int8)
+    cpu = oracle.cpu_lib()
+    if cpu is not None:
+        # the whole problem per call; repeated until `seconds` have passed
+        reps = 0
+        t0 = time.perf_counter()
+        while reps == 0 or time.perf_counter() - t0 < seconds:
+            rc = cpu.ref_cpu_matmul_s8(a.ctypes.data, w.ctypes.data, bias.ctypes.data, out.ctypes.data, M, N, K,
+                                       0.02, sb.ctypes.data, 0.05, 0, 1, cores)
+            if rc != 0:
+                raise RuntimeError(f"nnops CPU MatMul failed: status {rc}")
+            reps += 1
+        dt = time.perf_counter() - t0
+        return {"value": 2.0 * reps * M * N * K / dt / 1e12, "unit": "TOPS", "cores": cores, "kind": "reference",
+                "sample": f"config 2 in full (4096^3, s8 out, per-channel scales, bias, relu), {reps} calls in "
+                          f"{dt:.1f}s; nnops' CPU MatMul (src/backend/cpu/matmul, AVX-512-VNNI) compiled from "
+                          f"source, {cores} threads"}
+    ref = oracle.ref_lib()
+    rows_per = 8
 
     def block(r0):
         if ref is not None:
@@ -357,7 +375,7 @@ def cpu_baseline(seconds):
     return {"value": tops, "unit": "TOPS", "cores": cores,
             "kind": "reference" if ref is not None else "port",
             "sample": f"config 2 rows [0,{done}) of 4096 (s8 out, per-channel scales, bias, relu) in "
-                      f"{dt:.1f}s; " + ("nnops tests/reference/matmul_int8_ref compiled from source"
+                      f"{dt:.1f}s; " + ("nnops tests/reference/matmul_int8_ref (naive loops) compiled from source"
                                         if ref is not None else "oracle/oracle.c restatement")
                       + f", {cores} threads"}
 

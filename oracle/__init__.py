@@ -121,6 +121,39 @@ def ref_lib():
     return _ref
 
 
+_cpu = None
+
+
+def cpu_lib():
+    """nnops' own CPU MatMul (oracle/_ref/libnnops_cpu.so: its AVX-512-VNNI
+    int8 route compiled from the reference sources), or None where it was not
+    built or this host lacks AVX-512 VNNI/VL/BW (loading it would then fault
+    on the first vector instruction)."""
+    global _cpu
+    if _cpu is None:
+        path = os.path.join(_HERE, "_ref", "libnnops_cpu.so")
+        if not os.path.exists(path) or not host_has_avx512_vnni():
+            return None
+        _cpu = C.CDLL(path)
+        _cpu.ref_cpu_matmul_s8.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
+                                           C.c_int64, C.c_float, C.c_void_p, C.c_float, C.c_int32, C.c_int,
+                                           C.c_int]
+        _cpu.ref_cpu_matmul_s8.restype = C.c_int
+    return _cpu
+
+
+def host_has_avx512_vnni():
+    try:
+        flags = set()
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                flags = set(line.split(":", 1)[1].split())
+                break
+    except OSError:
+        return False
+    return {"avx512f", "avx512_vnni", "avx512vl", "avx512bw", "avx2", "fma", "f16c"} <= flags
+
+
 def _p(x):
     return None if x is None else x.ctypes.data
 

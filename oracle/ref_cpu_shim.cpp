@@ -1,0 +1,163 @@
+// C entry point over nnops' own CPU MatMul (the AVX-512-VNNI int8 route that
+// the reference ships as its CPU backend), for the CPU baseline of bench.py
+// and a parity cross-check of the oracle. Test infrastructure only: compiled
+// by oracle/Makefile (target `ref`) against the nnops sources where they lie,
+// into oracle/_ref/. Nothing from the reference is copied here; this file
+// builds the reference's TensorViews and calls
+//   nnops::MatMul::create / compute   include/nnops/ops/matmul.hpp:88-135
+// with a ComputeContext whose CpuBackend hooks (include/nnops/core/
+// parallel_for.hpp:60-110) run on a small std::thread pool defined below.
+#include "nnops/ops/matmul.hpp"
+
+#include <atomic>
+#include <condition_variable>
+#include <cstdint>
+#include <functional>
+#include <mutex>
+#include <span>
+#include <thread>
+#include <vector>
+
+using namespace nnops;
+
+namespace {
+
+// Fixed worker pool: parallel_for hands out indices through one atomic
+// counter; the caller's thread takes part as worker 0.
+class Pool {
+public:
+    explicit Pool(int n) : n_(n < 1 ? 1 : n)
+    {
+        for (int i = 1; i < n_; ++i) {
+            th_.emplace_back([this, i] { loop(i); });
+        }
+    }
+    ~Pool()
+    {
+        {
+            std::lock_guard<std::mutex> g(m_);
+            stop_ = true;
+            ++gen_;
+        }
+        cv_.notify_all();
+        for (auto& t : th_) {
+            t.join();
+        }
+    }
+    int size() const { return n_; }
+    static int& tid()
+    {
+        thread_local int id = 0;
+        return id;
+    }
+    void run(int64_t begin, int64_t end, const ParallelForBody& body)
+    {
+        {
+            std::lock_guard<std::mutex> g(m_);
+            body_ = &body;
+            next_.store(begin);
+            end_ = end;
+            busy_ = n_ - 1;
+            ++gen_;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> l(m_);
+        done_.wait(l, [this] { return busy_ == 0; });
+    }
+
+private:
+    void work()
+    {
+        for (;;) {
+            const int64_t i = next_.fetch_add(1);
+            if (i >= end_) {
+                return;
+            }
+            (*body_)(i);
+        }
+    }
+    void loop(int id)
+    {
+        tid() = id;
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> l(m_);
+                cv_.wait(l, [&] { return gen_ != seen; });
+                seen = gen_;
+                if (stop_) {
+                    return;
+                }
+            }
+            work();
+            std::lock_guard<std::mutex> g(m_);
+            if (--busy_ == 0) {
+                done_.notify_one();
+            }
+        }
+    }
+    int n_;
+    std::vector<std::thread> th_;
+    std::mutex m_;
+    std::condition_variable cv_, done_;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+    const ParallelForBody* body_ = nullptr;
+    std::atomic<int64_t> next_{0};
+    int64_t end_ = 0;
+    int busy_ = 0;
+};
+
+}  // namespace
+
+extern "C" {
+
+// s8 A [M,K] x s8 W [N,K] (the Linear weight) -> s8 C [M,N]: per-tensor A
+// scale, per-channel W scales, int32 bias, Relu, per-tensor output scale and
+// zero point (nnops' requant, half away from zero). `threads` workers.
+int ref_cpu_matmul_s8(const int8_t* a, const int8_t* w, const int32_t* bias, int8_t* c, int64_t M, int64_t N,
+                      int64_t K, float s_a, const float* s_b, float s_out, int32_t zp_out, int relu, int threads)
+{
+    static std::mutex pm;
+    static std::unique_ptr<Pool> pool;
+    std::lock_guard<std::mutex> g(pm);
+    if (!pool || pool->size() != threads) {
+        pool.reset();
+        pool = std::make_unique<Pool>(threads);
+    }
+    Pool* p = pool.get();
+
+    QuantParams qa;
+    qa.scale = s_a;
+    QuantParams qb;
+    qb.granularity = QuantGranularity::PerChannel;
+    qb.scale_data = s_b;
+    qb.num_scales = N;
+    QuantParams qc;
+    qc.scale = s_out;
+    qc.zero_point = zp_out;
+    const int64_t ashape[] = {M, K}, wshape[] = {N, K}, cshape[] = {M, N}, bshape[] = {N};
+    TensorView av(ashape, DataType::s8, const_cast<int8_t*>(a), TensorLayout::Dense, qa);
+    TensorView wv(wshape, DataType::s8, const_cast<int8_t*>(w), TensorLayout::Dense, qb);
+    TensorView bv(bshape, DataType::s32, const_cast<int32_t*>(bias));
+    TensorView cv(cshape, DataType::s8, c, TensorLayout::Dense, qc);
+
+    MatMulAttributes attrs{};
+    attrs.transpose_b = true;
+    attrs.output_dtype = DataType::s8;
+    if (relu) {
+        attrs.epilogue.type = EpilogueActivateType::Relu;
+    }
+    auto op = MatMul::create(attrs, Backend::CPU);
+    ComputeContext ctx{};
+    ctx.cpu.parallel_for = [p](int64_t b, int64_t e, const ParallelForBody& body) { p->run(b, e, body); };
+    ctx.cpu.num_threads = [p] { return p->size(); };
+    ctx.cpu.thread_id = [] { return Pool::tid(); };
+    const TensorView ins[] = {av, wv, bv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, bias ? 3 : 2), ctx);
+    return static_cast<int>(st);
+}
+
+}  // extern "C"

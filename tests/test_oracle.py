@@ -234,3 +234,28 @@ def test_oracle_q4_1_quantize_matches_reference_partial_blocks():
         want = np.zeros(nb * 20, np.uint8)
         oracle.ref_lib().ref_q4_1_quantize(x.ctypes.data, count, want.ctypes.data)
         np.testing.assert_array_equal(oracle.q4_1_quantize(x), want)
+
+
+# --- nnops' own CPU MatMul (its production int8 route), where built ----------
+
+cpu_only = pytest.mark.skipif(oracle.cpu_lib() is None,
+                              reason="oracle/_ref/libnnops_cpu.so not built or no AVX-512 VNNI on this host")
+
+
+@cpu_only
+@pytest.mark.parametrize("M,N,K,relu,zp", [(1, 64, 64, True, 0), (37, 130, 300, True, 5), (64, 256, 1024, False, -3),
+                                           (333, 96, 1440, True, 0)])
+def test_oracle_matches_nnops_cpu_matmul(M, N, K, relu, zp):
+    """The oracle against the reference's shipped CPU kernels (tiled VNNI
+    MatMul, requant epilogue), bit for bit."""
+    a = dg.act_s8(M + 1, (M, K))
+    w = dg.ints(N + 2, (N, K), -127, 127)
+    sb = dg.uniform(K + 3, (N,), 0.001, 0.01)
+    bias = dg.ints(4, (N,), -5000, 5000, np.int32)
+    c = np.zeros((M, N), np.int8)
+    rc = oracle.cpu_lib().ref_cpu_matmul_s8(a.ctypes.data, w.ctypes.data, bias.ctypes.data, c.ctypes.data, M, N, K,
+                                            0.02, sb.ctypes.data, 0.05, zp, int(relu), 4)
+    assert rc == 0
+    want = oracle.gemm_i8(a, w, trans_b=True, bias=bias, out_kind=oracle.OUT_S8, s_a=0.02, s_b=sb, s_out=0.05,
+                          zp_out=zp, act=oracle.ACT_RELU if relu else oracle.ACT_NONE)
+    np.testing.assert_array_equal(c, want)
