@@ -948,9 +948,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
 
 // ---------------------------------------------------------------------------
 // MFMA GEMM, f16 A, B blocks along K ([N][K/32], 2 blocks = 40 bytes per row
-// per 64-k stage), K % 64 == 0. 128 x 256 tiles, 4 waves, each 128 x 64 of
-// 32x32 fragments (v_mfma_f32_32x32x16_f16), a 3-stage LDS ring filled only
-// by buffer_load ... lds (so every wait below is an explicit vmcnt):
+// per 64-k stage), K % 64 == 0. 128 x 256 tiles, WM x WN waves (the launch
+// uses 1 x 8: each wave 128 x 32, two per SIMD) of 32x32 fragments
+// (v_mfma_f32_32x32x16_f16), an NS-stage LDS ring filled only by
+// buffer_load ... lds (so every wait below is an explicit vmcnt):
 //   A     128 rows x 128 bytes; 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7)
 //   Braw  256 rows x 64 bytes (the row's 40 stage bytes + 24 not used); chunk
 //         c of row r in slot c ^ ((r >> 2) & 3)
@@ -1004,15 +1005,15 @@ __device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v
     return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
 }
 
-template <bool OUT16, int NS, int WM>
-__global__ __launch_bounds__(256 * WM, 1) void gemm_q4_1_ring(Q41Kern p)
+template <bool OUT16, int NS, int WM, int WN = 4>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 {
-    constexpr int W = 4 * WM;                       // waves: WM along M x 4 along N
+    constexpr int W = WM * WN;                      // waves: WM along M x WN along N
     constexpr int QA = 16 / W, QB = 16 / W;         // 1 KiB pieces per wave per stage
     constexpr int L = QA + QB;
     static_assert(NS >= 3 && (NS - 2) * L < 64, "stages");
     constexpr int BM = 128, BN = 256;
-    constexpr int TM = BM / WM, TN = 64, FM = TM / 32, FN = 2;
+    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     constexpr int kA = BM * 128, kB = BN * 64, kStage = kA + kB;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
 
@@ -1026,8 +1027,8 @@ __global__ __launch_bounds__(256 * WM, 1) void gemm_q4_1_ring(Q41Kern p)
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn0 = (wave % 4) * TN;
-    const int wm0 = (wave / 4) * TM;
+    const int wn0 = (wave % WN) * TN;
+    const int wm0 = (wave / WN) * TM;
     const int kt = p.k / 64;
 
     // A: rows 8 * (4 * wave + i) + lane / 8; B raw: rows 16 * (4 * wave + i) + lane / 4
@@ -1322,10 +1323,12 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
     } else if (g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0) {
         // blocks along K: the ring kernel (A by DMA, B decoded in registers)
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
+        // 8 waves (2 per SIMD), each 128 x 32: one wave's decode and stalls
+        // overlap the other's matrix-core work, and no B row is decoded twice
         if (k.out_f16) {
-            hipLaunchKernelGGL((gemm_q4_1_ring<true, 5, 1>), dim3(tiles), dim3(256), 0, s, k);
+            hipLaunchKernelGGL((gemm_q4_1_ring<true, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_ring<false, 5, 1>), dim3(tiles), dim3(256), 0, s, k);
+            hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
