@@ -77,6 +77,9 @@ SHAPES = [
     # column GEMV on a [K,N] B (16- and 4-column lane groups, K splits)
     (2, 4096, 1008), (5, 256, 100), (12, 1024, 2048), (16, 512, 4096),
     (1, 1040, 8192), (2, 1024, 8256), (7, 512, 8192),
+    # row GEMV with two rows per wave (M = 3..4), LDS-staged skinny GEMM
+    # (4 < M <= 16) with a ragged last group of rows and a K tail past 4 KiB
+    (3, 512, 130), (4, 4096, 1000), (8, 5120, 77), (16, 1088, 4099),
 ]
 
 
