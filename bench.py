@@ -250,6 +250,63 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
             "M": M, "K": K, "N": N, "a_pitch": 14400, "c_pitch": 4160, "weight_layout": "[N,K]"}
 
 
+def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False):
+    """QuantizeLinear f16 [R,C] -> s8 (per-token scales and zero points), or
+    DequantizeLinear s8 -> f16, through the operator API. HBM-bound."""
+    import numpy as np
+    scale = torch.from_numpy(dg.uniform(601, (R,), 0.01, 0.05)).cuda()
+    zp = torch.from_numpy(dg.ints(602, (R,), -8, 8, np.int8)).cuda()
+    if dequant:
+        x = torch.from_numpy(dg.ints(603, (R, C), -128, 127)).cuda()
+        y = torch.empty((R, C), dtype=torch.float16, device="cuda")
+        op = na.DequantizeLinear(axis=-1, output_dtype=na.DT_F16)
+    else:
+        x = torch.from_numpy(dg.normal(603, (R, C), 1.0).astype("float16")).cuda()
+        y = torch.empty((R, C), dtype=torch.int8, device="cuda")
+        op = na.QuantizeLinear(axis=-1, output_dtype=na.DT_S8)
+    ins = [na.tensor(x), na.tensor(scale), na.tensor(zp)]
+    outs = [na.tensor(y)]
+    s = stream.cuda_stream
+    t = Timer(stream).time(lambda: op.compute(outs, ins, stream=s), steps, warmup)
+    nbytes = R * C * 3 + R * 5
+    gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
+    return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
+            "shape": [R, C], "op": "DequantizeLinear s8->f16" if dequant else "QuantizeLinear f16->s8",
+            "granularity": "per token"}
+
+
+def fp_act_case(torch, dg, na, stream, steps, warmup, M=4096, N=4096, K=4096, dq_only=False):
+    """The fp-activation int8 MatMul at config 2's shape: f16 A with per-token
+    scales, s8 [N,K] weights with per-channel scales, f16 out (quantize A into
+    the workspace, int8 GEMM, dequantize). dq_only: the int8 pair with an f16
+    destination (the dequantizing output pass alone)."""
+    import numpy as np
+    w = torch.from_numpy(dg.ints(702, (N, K), -127, 127)).cuda()
+    sb = torch.from_numpy(dg.uniform(703, (N,), 0.001, 0.01)).cuda()
+    bias = torch.from_numpy(dg.normal(704, (N,)).astype("float16")).cuda()
+    c = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    sa = torch.from_numpy(dg.uniform(705, (M,), 0.01, 0.03)).cuda()
+    if dq_only:
+        a = torch.from_numpy(dg.act_s8(701, (M, K))).cuda()
+        op = na.Linear(output_dtype=na.DT_F16, act=na.EP_RELU)
+        ins = [na.tensor(a, scale_data=sa, granularity=1), na.tensor(w, scale_data=sb, granularity=2),
+               na.tensor(bias)]
+    else:
+        a = torch.from_numpy(dg.normal(701, (M, K), 1.0).astype("float16")).cuda()
+        op = na.MatMul(transpose_b=True, act=na.EP_RELU)
+        ins = [na.tensor(a, scale_data=sa, granularity=1), na.tensor(w, scale_data=sb, granularity=2),
+               na.tensor(bias)]
+    outs = [na.tensor(c)]
+    ws = torch.empty(max(op.workspace_size(ins, outs), 1), dtype=torch.uint8, device="cuda")
+    s = stream.cuda_stream
+    t = Timer(stream).time(lambda: op.compute(outs, ins, stream=s, workspace=ws), steps, warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / (t["mean_ms"] * 1e-3) / 1e12
+    return {"tops": tops, "frac_int8_mfma": tops / PEAK_INT8_TOPS, "us": t["mean_ms"] * 1e3, "M": M, "N": N,
+            "K": K, "route": "int8 pair -> f16 (dequantizing destination)" if dq_only
+            else "f16 A (per-token QuantParams) x s8 -> f16"}
+
+
 def ceilings(torch, na, stream):
     """What this MI355X sustains outside our kernels: dense int8 MFMA fed
     from registers (random and constant operands: the power budget lowers the
@@ -434,6 +491,13 @@ def main():
         secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup)
         secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
                                                          args.warmup)
+        secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, max(5, args.steps // 5),
+                                                        args.warmup, dq_only=True)
+        secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, max(5, args.steps // 5),
+                                                          args.warmup)
+        secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup)
+        secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                                dequant=True)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, max(5, args.steps // 5), args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {

@@ -266,11 +266,16 @@ size_t i8_workspace(const Geometry& g, const QuantCall& q, int32_t out_kind)
 {
     // The kernel plan (and so its region) depends on what a descriptor does not
     // carry: zero points, tables, pointer alignment. Size for the largest: the
-    // plan of plain operands (the [K,N] column GEMV's partials) and the plan
-    // with zero points (a staged B^T plus K-split partials).
+    // plan of plain operands (the [K,N] column GEMV's partials), the plan with
+    // zero points (a staged B^T plus K-split partials) and the plan of an
+    // unaligned destination (raw partials for the reduce).
     NnopsGemmI8Args x = i8_args_from_geometry(g, q, out_kind);
     size_t need = nnops_hip_gemm_i8_workspace_size(&x);
     x.zp_a_scalar = 1;
+    need = std::max(need, nnops_hip_gemm_i8_workspace_size(&x));
+    // a destination too unaligned for the fused output passes (never
+    // dereferenced by the size query): the split-partials plan
+    x.c = reinterpret_cast<void*>(uintptr_t{1});
     need = std::max(need, nnops_hip_gemm_i8_workspace_size(&x));
     return staging_bytes(a_table_rows(g), g.m, g.n) + align_up(need);
 }

@@ -22,6 +22,7 @@
 // is associative), so both kernels are bit-exact whatever the k split.
 #include "common.hpp"
 
+#include <type_traits>
 #include <utility>
 
 #include <algorithm>
@@ -608,7 +609,7 @@ __device__ __forceinline__ void buffer_load_lds16(BufRsrc r, int8_t* lds, int vo
 #endif
 }
 
-enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2 };
+enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2, RING_FP = 3 };
 
 struct RingSplit {
     int splits;        // K ranges per output tile
@@ -911,6 +912,174 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             if (m < p.m && n < p.n) {
                 char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + n;
                 __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(cptr));
+            }
+        }
+    } else if constexpr (MODE == RING_FP) {
+        // f32 / f16 destination, plain operands (no zero points) and an
+        // identity or Relu activation (host-checked): f = v * (s_a * s_b[n])
+        // [+ bias[n]] [+ C_old before / after the clip], clip, Relu -- the
+        // operation order of the generic pass (epi_value_fp). Host-checked:
+        // N % 4 == 0, 16-byte-aligned C and pitch.
+        const bool f16 = ep.out_kind == NNOPS_OUT_F16;
+        const bool relu = ep.act == NNOPS_ACT_RELU;
+        const bool pre = ep.add_to && ep.residual_pre, post = ep.add_to && !ep.residual_pre;
+        // the 4 values of (i, j, g) for this lane: row wm0 + 32 i + (lane & 31),
+        // columns wn0 + 32 j + 8 g + 4 (lane >> 5) .. + 3
+        auto values = [&](int i, int j, int g, float sa) {
+            const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+            const int m = m0 + wm0 + i * 32 + (lane & 31);
+            v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (n >= p.n || m >= p.m) {
+                return o;
+            }
+            v4f sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+            if (ep.s_b != nullptr) {
+                sb = *reinterpret_cast<const v4f*>(ep.s_b + n);
+            }
+            v4f bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (ep.bias_fp != nullptr) {
+                if (f16) {
+                    const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + n;
+                    bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
+                } else {
+                    bias = *reinterpret_cast<const v4f*>(static_cast<const float*>(ep.bias_fp) + n);
+                }
+            }
+            v4f old = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (ep.add_to) {
+                const char* cptr = static_cast<const char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
+                if (f16) {
+                    const _Float16* o16 = reinterpret_cast<const _Float16*>(cptr);
+                    old = v4f{(float)o16[0], (float)o16[1], (float)o16[2], (float)o16[3]};
+                } else {
+                    old = *reinterpret_cast<const v4f*>(cptr);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float f = __fmul_rn((float)acc[i][j][4 * g + e], __fmul_rn(sa, sb[e]));
+                if (ep.bias_fp != nullptr) {
+                    f = __fadd_rn(f, bias[e]);
+                }
+                if (pre) {
+                    f = __fadd_rn(f, old[e]);
+                }
+                f = f < ep.min_clip ? ep.min_clip : f;
+                f = ep.max_clip < f ? ep.max_clip : f;
+                if (relu) {
+                    f = f > 0.0f ? f : 0.0f;
+                }
+                if (post) {
+                    if (f16) {
+                        f = (float)(_Float16)f;
+                    }
+                    f = __fadd_rn(f, old[e]);
+                }
+                o[e] = f;
+            }
+            return o;
+        };
+        float sa_i[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int m = min(m0 + wm0 + i * 32 + (lane & 31), p.m - 1);
+            sa_i[i] = ep.s_a != nullptr ? ep.s_a[m] : ep.s_a_scalar;
+        }
+        if constexpr (W * TM * 128 <= NS * kStage) {
+            // Staged through LDS so the global stores are 16-byte chunks
+            // along rows (whole 128-byte lines per 8 lanes): per wave a
+            // [TM][128-byte] tile of one slab of columns (32 f32 or 64 f16),
+            // entries of 4 columns at slot q ^ (row % groups) in the row.
+            int8_t* tile = ring + wave * (TM * 128);
+            auto slab = [&](auto esz_c) {
+                constexpr int ESZ = decltype(esz_c)::value;          // output element bytes
+                constexpr int SC = (TN < 128 / ESZ) ? TN : 128 / ESZ; // columns per slab
+                constexpr int GPS = SC / 4;                          // 4-column entries per slab row
+                constexpr int E = 4 * ESZ;                           // entry bytes
+                constexpr int RB = GPS * E;                          // slab row bytes
+                constexpr int CPRW = RB / 16;                        // 16-byte chunks per row
+#pragma unroll
+                for (int s0 = 0; s0 < TN / SC; ++s0) {
+#pragma unroll
+                    for (int jj = 0; jj < SC / 32; ++jj) {
+                        const int j = s0 * (SC / 32) + jj;
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const int q = jj * 8 + 2 * g + (lane >> 5);
+#pragma unroll
+                            for (int i = 0; i < FM; ++i) {
+                                const int r = i * 32 + (lane & 31);
+                                const v4f o = values(i, j, g, sa_i[i]);
+                                int8_t* dst = tile + r * RB + ((q ^ (r % GPS)) * E);
+                                if constexpr (ESZ == 4) {
+                                    *reinterpret_cast<v4f*>(dst) = o;
+                                } else {
+                                    _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+                                    uint2 w;
+                                    __builtin_memcpy(&w, h, 8);
+                                    *reinterpret_cast<uint2*>(dst) = w;
+                                }
+                            }
+                        }
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                    for (int t = 0; t < TM * CPRW / 64; ++t) {
+                        const int idx = t * 64 + lane, r = idx / CPRW, cc = idx % CPRW;
+                        const int m = m0 + wm0 + r;
+                        const int n = n0 + wn0 + s0 * SC + cc * (16 / ESZ);
+                        v4i v;
+                        if constexpr (ESZ == 4) {
+                            v = *reinterpret_cast<const v4i*>(tile + r * RB + ((cc ^ (r % GPS)) * E));
+                        } else {
+                            const uint2 lo = *reinterpret_cast<const uint2*>(tile + r * RB + (((2 * cc) ^ (r % GPS)) * E));
+                            const uint2 hi = *reinterpret_cast<const uint2*>(tile + r * RB + (((2 * cc + 1) ^ (r % GPS)) * E));
+                            v = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                        }
+                        if (m < p.m && n < p.n) {
+                            char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * ESZ;
+                            if (n + 16 / ESZ <= p.n) {
+                                *reinterpret_cast<v4i*>(cptr) = v;
+                            } else {
+                                // a row's last group of 4 columns (N % 8 == 4, f16)
+                                *reinterpret_cast<uint2*>(cptr) = uint2{(uint32_t)v.x, (uint32_t)v.y};
+                            }
+                        }
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+            };
+            if (f16) {
+                slab(std::integral_constant<int, 2>{});
+            } else {
+                slab(std::integral_constant<int, 4>{});
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        const int m = m0 + wm0 + i * 32 + (lane & 31);
+                        if (m >= p.m || n >= p.n) {
+                            continue;
+                        }
+                        const v4f o = values(i, j, g, sa_i[i]);
+                        char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
+                        if (f16) {
+                            _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+                            uint2 w;
+                            __builtin_memcpy(&w, h, 8);
+                            *reinterpret_cast<uint2*>(cptr) = w;
+                        } else {
+                            *reinterpret_cast<v4f*>(cptr) = o;
+                        }
+                    }
+                }
             }
         }
     } else {
@@ -1605,7 +1774,12 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     const bool plain = !compensate && g.s_out_rows == nullptr && g.zp_out_rows == nullptr && !g.float_ep &&
                        !g.round_even && !fp_out && tables16 && ((uintptr_t)g.c % 16 == 0);
     r.mode = RING_PART;
-    if (r.splits == 1 && plain) {
+    const size_t ebytes = g.out_kind == NNOPS_OUT_F16 ? 2 : 4;
+    if (r.splits == 1 && fp_out && !compensate && (g.act == NNOPS_ACT_NONE || g.act == NNOPS_ACT_RELU) &&
+        (uintptr_t)g.c % 16 == 0 && (g.ldc * ebytes) % 16 == 0 &&
+        ((uintptr_t)g.s_b % 16) == 0 && (g.bias_fp == nullptr || (uintptr_t)g.bias_fp % (4 * ebytes) == 0)) {
+        r.mode = RING_FP;      // dequantizing output pass fused
+    } else if (r.splits == 1 && plain) {
         if (g.out_kind == NNOPS_OUT_S32 && (g.ldc * 4) % 16 == 0) {
             r.mode = RING_S32;
         } else if (g.out_kind != NNOPS_OUT_S32 && g.s_a == nullptr && g.ldc % 16 == 0 && g.n % 16 == 0) {
@@ -1688,6 +1862,8 @@ void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool fli
         hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S32) {
         hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
+    } else if (mode == RING_FP) {
+        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false>), dim3(blocks), block, 0, s, k, sk);
     } else {
         hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
     }

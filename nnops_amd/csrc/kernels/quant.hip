@@ -1,6 +1,6 @@
 // QuantizeLinear / DequantizeLinear on gfx950: the elementwise steps either
 // side of the int8 GEMM in a QDQ graph, and the activation quantization of
-// the fp-activation int8 MatMul. One thread per 4 consecutive elements of a
+// the fp-activation int8 MatMul. One thread per 16 consecutive elements of a
 // rows x cols view (row strides in elements); the parameter of flat element
 // i = r * cols + c is entry (i / inner) % dim of the scale / zero-point
 // tables (per tensor: dim = 1; per token: inner = cols; per channel: the
@@ -55,75 +55,173 @@ __device__ __forceinline__ int32_t qdq_zero(const QdqKern& p, int64_t j)
     }
 }
 
+__device__ __forceinline__ float qdq_load_x(const QdqKern& p, int64_t xi)
+{
+    return p.x_kind == NNOPS_OUT_F16 ? (float)static_cast<const _Float16*>(p.x)[xi]
+                                     : static_cast<const float*>(p.x)[xi];
+}
+
+__device__ __forceinline__ int32_t quant_one(float x, float inv, float zf, int32_t qmin, int32_t qmax)
+{
+    const float v = __builtin_fmaf(x, inv, zf);
+    int32_t q = qmin;
+    if (__builtin_fabsf(v) < 2147483648.0f) {   // false for NaN
+        q = (int32_t)__builtin_rintf(v);
+        q = q < qmin ? qmin : (q > qmax ? qmax : q);
+    }
+    return q;
+}
+
+// Does the 16-element chunk starting at flat index i share one parameter?
+__device__ __forceinline__ bool qdq_uniform(const QdqKern& p, int64_t i)
+{
+    return p.dim <= 1 || (i / p.inner) == ((i + 15) / p.inner);
+}
+
+// One thread per 16 consecutive elements of a row (a chunk): 16-byte vector
+// loads and stores when the chunk is whole, aligned and under one parameter
+// (every per-tensor and per-token case with 16 | cols, per-channel with
+// 16 | inner), element by element otherwise.
 __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
 {
-    const int64_t groups = (p.cols + 3) / 4;
+    const int64_t chunks = (p.cols + 15) / 16;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= p.rows * groups) {
+    if (t >= p.rows * chunks) {
         return;
     }
-    const int64_t r = t / groups, c0 = (t - r * groups) * 4;
+    const int64_t r = t / chunks, c0 = (t - r * chunks) * 16;
     const bool u8 = p.y_kind == NNOPS_OUT_U8;
     const int32_t qmin = u8 ? 0 : -128, qmax = u8 ? 255 : 127;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int64_t c = c0 + e;
-        if (c >= p.cols) {
-            break;
-        }
-        const int64_t xi = r * p.ld_x + c;
-        const float x = p.x_kind == NNOPS_OUT_F16 ? (float)static_cast<const _Float16*>(p.x)[xi]
-                                                  : static_cast<const float*>(p.x)[xi];
-        const int64_t j = qdq_param(p, r * p.cols + c);
+    const int64_t i0 = r * p.cols + c0;
+    const int64_t xi = r * p.ld_x + c0, yi = r * p.ld_y + c0;
+    const bool f16 = p.x_kind == NNOPS_OUT_F16;
+    const bool vec = c0 + 16 <= p.cols && qdq_uniform(p, i0) &&
+                     ((uintptr_t)p.x + (uintptr_t)xi * (f16 ? 2 : 4)) % 16 == 0 &&
+                     ((uintptr_t)p.y + (uintptr_t)yi) % 16 == 0;
+    if (vec) {
+        const int64_t j = qdq_param(p, i0);
         const float inv = __fdiv_rn(1.0f, qdq_scale(p, j));
-        const float v = __builtin_fmaf(x, inv, (float)qdq_zero(p, j));
-        int32_t q = qmin;
-        if (__builtin_fabsf(v) < 2147483648.0f) {   // false for NaN
-            q = (int32_t)__builtin_rintf(v);
-            q = q < qmin ? qmin : (q > qmax ? qmax : q);
-        }
-        const int64_t yi = r * p.ld_y + c;
-        if (u8) {
-            static_cast<uint8_t*>(p.y)[yi] = (uint8_t)q;
+        const float zf = (float)qdq_zero(p, j);
+        float x[16];
+        if (f16) {
+            const v4i* src = reinterpret_cast<const v4i*>(static_cast<const _Float16*>(p.x) + xi);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const v4i w = src[h];
+                const _Float16* e = reinterpret_cast<const _Float16*>(&w);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    x[8 * h + q] = (float)e[q];
+                }
+            }
         } else {
-            static_cast<int8_t*>(p.y)[yi] = (int8_t)q;
+            const v4i* src = reinterpret_cast<const v4i*>(static_cast<const float*>(p.x) + xi);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const v4i w = src[h];
+                x[4 * h + 0] = __int_as_float(w.x);
+                x[4 * h + 1] = __int_as_float(w.y);
+                x[4 * h + 2] = __int_as_float(w.z);
+                x[4 * h + 3] = __int_as_float(w.w);
+            }
+        }
+        uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            o[e / 4] |= ((uint32_t)quant_one(x[e], inv, zf, qmin, qmax) & 0xffu) << (8 * (e % 4));
+        }
+        *reinterpret_cast<v4i*>(static_cast<int8_t*>(p.y) + yi) = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        return;
+    }
+    for (int e = 0; e < 16 && c0 + e < p.cols; ++e) {
+        const int64_t j = qdq_param(p, i0 + e);
+        const float inv = __fdiv_rn(1.0f, qdq_scale(p, j));
+        const int32_t q = quant_one(qdq_load_x(p, xi + e), inv, (float)qdq_zero(p, j), qmin, qmax);
+        if (u8) {
+            static_cast<uint8_t*>(p.y)[yi + e] = (uint8_t)q;
+        } else {
+            static_cast<int8_t*>(p.y)[yi + e] = (int8_t)q;
         }
     }
 }
 
+// fma(q, s, -zp * s) over each segment's whole 16-element blocks, (q - zp) * s
+// over its last segment % 16 elements.
+__device__ __forceinline__ float dequant_one(const QdqKern& p, int64_t i, int32_t q, float s, float zf)
+{
+    const int64_t body = p.segment - p.segment % 16;
+    if (i % p.segment < body) {
+        return __builtin_fmaf((float)q, s, __fmul_rn(-zf, s));
+    }
+    return __fmul_rn(__fsub_rn((float)q, zf), s);
+}
+
 __global__ __launch_bounds__(256) void dequantize_kernel(QdqKern p)
 {
-    const int64_t groups = (p.cols + 3) / 4;
+    const int64_t chunks = (p.cols + 15) / 16;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= p.rows * groups) {
+    if (t >= p.rows * chunks) {
         return;
     }
-    const int64_t r = t / groups, c0 = (t - r * groups) * 4;
+    const int64_t r = t / chunks, c0 = (t - r * chunks) * 16;
+    const int64_t i0 = r * p.cols + c0;
+    const int64_t xi = r * p.ld_x + c0, yi = r * p.ld_y + c0;
+    const bool f16 = p.y_kind == NNOPS_OUT_F16;
+    const bool u8 = p.x_kind == NNOPS_OUT_U8;
     const int64_t body = p.segment - p.segment % 16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int64_t c = c0 + e;
-        if (c >= p.cols) {
-            break;
-        }
-        const int64_t xi = r * p.ld_x + c;
-        const int32_t q = p.x_kind == NNOPS_OUT_U8 ? (int32_t) static_cast<const uint8_t*>(p.x)[xi]
-                                                   : (int32_t) static_cast<const int8_t*>(p.x)[xi];
-        const int64_t i = r * p.cols + c;
-        const int64_t j = qdq_param(p, i);
-        const float s = qdq_scale(p, j);
+    // whole chunk inside one segment's vector body (or wholly in its tail)
+    const int64_t s0 = i0 % p.segment;
+    const bool one_form = s0 + 15 < p.segment && ((s0 < body) == (s0 + 15 < body));
+    const bool vec = c0 + 16 <= p.cols && qdq_uniform(p, i0) && one_form &&
+                     ((uintptr_t)p.x + (uintptr_t)xi) % 16 == 0 &&
+                     ((uintptr_t)p.y + (uintptr_t)yi * (f16 ? 2 : 4)) % 16 == 0;
+    if (vec) {
+        const int64_t j = qdq_param(p, i0);
+        const float sc = qdq_scale(p, j);
         const float zf = (float)qdq_zero(p, j);
-        float y;
-        if (i % p.segment < body) {
-            y = __builtin_fmaf((float)q, s, __fmul_rn(-zf, s));
-        } else {
-            y = __fmul_rn(__fsub_rn((float)q, zf), s);
+        const bool fused = s0 < body;
+        const float nzs = __fmul_rn(-zf, sc);
+        const v4i w = *reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.x) + xi);
+        const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+        float y[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t b = (wd[e / 4] >> (8 * (e % 4))) & 0xffu;
+            const int32_t q = u8 ? (int32_t)b : (int32_t)(int8_t)b;
+            y[e] = fused ? __builtin_fmaf((float)q, sc, nzs) : __fmul_rn(__fsub_rn((float)q, zf), sc);
         }
-        const int64_t yi = r * p.ld_y + c;
-        if (p.y_kind == NNOPS_OUT_F16) {
-            static_cast<_Float16*>(p.y)[yi] = (_Float16)y;
+        if (f16) {
+            v4i* dst = reinterpret_cast<v4i*>(static_cast<_Float16*>(p.y) + yi);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                _Float16 e8[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    e8[q] = (_Float16)y[8 * h + q];
+                }
+                v4i o;
+                __builtin_memcpy(&o, e8, 16);
+                dst[h] = o;
+            }
         } else {
-            static_cast<float*>(p.y)[yi] = y;
+            v4i* dst = reinterpret_cast<v4i*>(static_cast<float*>(p.y) + yi);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                dst[h] = v4i{__float_as_int(y[4 * h]), __float_as_int(y[4 * h + 1]), __float_as_int(y[4 * h + 2]),
+                             __float_as_int(y[4 * h + 3])};
+            }
+        }
+        return;
+    }
+    for (int e = 0; e < 16 && c0 + e < p.cols; ++e) {
+        const int32_t q = u8 ? (int32_t) static_cast<const uint8_t*>(p.x)[xi + e]
+                             : (int32_t) static_cast<const int8_t*>(p.x)[xi + e];
+        const int64_t j = qdq_param(p, i0 + e);
+        const float y = dequant_one(p, i0 + e, q, qdq_scale(p, j), (float)qdq_zero(p, j));
+        if (f16) {
+            static_cast<_Float16*>(p.y)[yi + e] = (_Float16)y;
+        } else {
+            static_cast<float*>(p.y)[yi + e] = y;
         }
     }
 }
@@ -186,7 +284,7 @@ extern "C" int nnops_hip_quantize_linear(const NnopsQdqArgs* g, void* stream)
     if (rc >= 0) {
         return rc;
     }
-    const int64_t threads = g->rows * ((g->cols + 3) / 4);
+    const int64_t threads = g->rows * ((g->cols + 15) / 16);
     hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), qdq_kern(g));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
@@ -198,7 +296,7 @@ extern "C" int nnops_hip_dequantize_linear(const NnopsQdqArgs* g, void* stream)
     if (rc >= 0) {
         return rc;
     }
-    const int64_t threads = g->rows * ((g->cols + 3) / 4);
+    const int64_t threads = g->rows * ((g->cols + 15) / 16);
     hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), qdq_kern(g));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;

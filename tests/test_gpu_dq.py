@@ -338,3 +338,25 @@ def test_quant_linear_rejects():
     d = na.DequantizeLinear(output_dtype=na.DT_S8)
     _, dt = d.output_desc([na.tensor(q), na.tensor(s), na.tensor(z)])
     assert dt == na.DT_F32
+
+
+@pytest.mark.parametrize("out16", [False, True])
+@pytest.mark.parametrize("act", [na.ACT_NONE, na.ACT_RELU])
+@pytest.mark.parametrize("add_to,residual_pre", [(False, False), (True, True), (True, False)])
+@pytest.mark.parametrize("M,N", [(1024, 1024), (1000, 1020)])
+def test_dq_fused_ring_output_pass(out16, act, add_to, residual_pre, M, N):
+    """Shapes whose ring GEMM runs unsplit take the fused dequantizing output
+    pass (no partials): per-token s_a, per-channel s_b, bias, clip, Relu,
+    pre/post residual, against the oracle bit for bit."""
+    announce(f"dq fused ring f16={out16} act={act} add_to={add_to} pre={residual_pre} M={M} N={N}")
+    K = 512
+    seed = 900 + 2 * out16 + 4 * act + 8 * add_to + 16 * residual_pre
+    a = dg.act_s8(seed, (M, K))
+    b = dg.ints(seed + 1, (N, K), -127, 127)
+    sa = dg.uniform(seed + 2, (M,), 0.01, 0.03)
+    sb = dg.uniform(seed + 3, (N,), 0.001, 0.01)
+    bias = dg.normal(seed + 4, (N,)).astype(np.float16 if out16 else np.float32)
+    c0 = dg.normal(seed + 5, (M, N)).astype(np.float16 if out16 else np.float32)
+    got, want = run_dq(a, b, trans_b=True, out16=out16, bias=bias, s_a=sa, s_b=sb, act=act, lo=-2.5, hi=3.0,
+                       add_to=add_to, residual_pre=residual_pre, c0=c0)
+    check(got, want, act)
