@@ -38,6 +38,45 @@ __device__ __forceinline__ int64_t qdq_param(const QdqKern& p, int64_t i)
     return p.dim <= 1 ? 0 : (i / p.inner) % p.dim;
 }
 
+// The parameter of element (r, c) of the rows x cols view, without a 64-bit
+// division for per-tensor (dim <= 1) and per-token (inner == cols,
+// dim == rows) tables.
+__device__ __forceinline__ int64_t qdq_param_rc(const QdqKern& p, int64_t r, int64_t c)
+{
+    if (p.dim <= 1) {
+        return 0;
+    }
+    if (p.inner == p.cols && p.dim == p.rows) {
+        return r;
+    }
+    return qdq_param(p, r * p.cols + c);
+}
+
+// Does the 16-element chunk at (r, c0) share one parameter?
+__device__ __forceinline__ bool qdq_uniform_rc(const QdqKern& p, int64_t r, int64_t c0)
+{
+    if (p.dim <= 1 || (p.inner == p.cols && p.dim == p.rows)) {
+        return true;                              // one parameter per row (or per tensor)
+    }
+    const int64_t i = r * p.cols + c0;
+    return (i / p.inner) == ((i + 15) / p.inner);
+}
+
+// Chunk t of the launch -> (row, first column), in 32-bit arithmetic when the
+// chunk count allows it.
+__device__ __forceinline__ void qdq_chunk(const QdqKern& p, int64_t t, int64_t chunks, int64_t& r, int64_t& c0)
+{
+    if (p.rows * chunks <= (int64_t)UINT32_MAX) {
+        const uint32_t tt = (uint32_t)t, ch = (uint32_t)chunks;
+        const uint32_t rr = tt / ch;
+        r = rr;
+        c0 = (int64_t)(tt - rr * ch) * 16;
+    } else {
+        r = t / chunks;
+        c0 = (t - r * chunks) * 16;
+    }
+}
+
 __device__ __forceinline__ float qdq_scale(const QdqKern& p, int64_t j)
 {
     return p.scale != nullptr ? p.scale[j] : p.scale_scalar;
@@ -72,11 +111,6 @@ __device__ __forceinline__ int32_t quant_one(float x, float inv, float zf, int32
     return q;
 }
 
-// Does the 16-element chunk starting at flat index i share one parameter?
-__device__ __forceinline__ bool qdq_uniform(const QdqKern& p, int64_t i)
-{
-    return p.dim <= 1 || (i / p.inner) == ((i + 15) / p.inner);
-}
 
 // One thread per 16 consecutive elements of a row (a chunk): 16-byte vector
 // loads and stores when the chunk is whole, aligned and under one parameter
@@ -89,17 +123,18 @@ __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
     if (t >= p.rows * chunks) {
         return;
     }
-    const int64_t r = t / chunks, c0 = (t - r * chunks) * 16;
+    int64_t r, c0;
+    qdq_chunk(p, t, chunks, r, c0);
     const bool u8 = p.y_kind == NNOPS_OUT_U8;
     const int32_t qmin = u8 ? 0 : -128, qmax = u8 ? 255 : 127;
     const int64_t i0 = r * p.cols + c0;
     const int64_t xi = r * p.ld_x + c0, yi = r * p.ld_y + c0;
     const bool f16 = p.x_kind == NNOPS_OUT_F16;
-    const bool vec = c0 + 16 <= p.cols && qdq_uniform(p, i0) &&
+    const bool vec = c0 + 16 <= p.cols && qdq_uniform_rc(p, r, c0) &&
                      ((uintptr_t)p.x + (uintptr_t)xi * (f16 ? 2 : 4)) % 16 == 0 &&
                      ((uintptr_t)p.y + (uintptr_t)yi) % 16 == 0;
     if (vec) {
-        const int64_t j = qdq_param(p, i0);
+        const int64_t j = qdq_param_rc(p, r, c0);
         const float inv = __fdiv_rn(1.0f, qdq_scale(p, j));
         const float zf = (float)qdq_zero(p, j);
         float x[16];
@@ -107,7 +142,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
             const v4i* src = reinterpret_cast<const v4i*>(static_cast<const _Float16*>(p.x) + xi);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const v4i w = src[h];
+                const v4i w = __builtin_nontemporal_load(src + h);
                 const _Float16* e = reinterpret_cast<const _Float16*>(&w);
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
@@ -118,7 +153,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
             const v4i* src = reinterpret_cast<const v4i*>(static_cast<const float*>(p.x) + xi);
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
-                const v4i w = src[h];
+                const v4i w = __builtin_nontemporal_load(src + h);
                 x[4 * h + 0] = __int_as_float(w.x);
                 x[4 * h + 1] = __int_as_float(w.y);
                 x[4 * h + 2] = __int_as_float(w.z);
@@ -130,7 +165,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
         for (int e = 0; e < 16; ++e) {
             o[e / 4] |= ((uint32_t)quant_one(x[e], inv, zf, qmin, qmax) & 0xffu) << (8 * (e % 4));
         }
-        *reinterpret_cast<v4i*>(static_cast<int8_t*>(p.y) + yi) = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        __builtin_nontemporal_store(v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]},
+                                    reinterpret_cast<v4i*>(static_cast<int8_t*>(p.y) + yi));
         return;
     }
     for (int e = 0; e < 16 && c0 + e < p.cols; ++e) {
@@ -163,25 +199,27 @@ __global__ __launch_bounds__(256) void dequantize_kernel(QdqKern p)
     if (t >= p.rows * chunks) {
         return;
     }
-    const int64_t r = t / chunks, c0 = (t - r * chunks) * 16;
+    int64_t r, c0;
+    qdq_chunk(p, t, chunks, r, c0);
     const int64_t i0 = r * p.cols + c0;
     const int64_t xi = r * p.ld_x + c0, yi = r * p.ld_y + c0;
     const bool f16 = p.y_kind == NNOPS_OUT_F16;
     const bool u8 = p.x_kind == NNOPS_OUT_U8;
     const int64_t body = p.segment - p.segment % 16;
-    // whole chunk inside one segment's vector body (or wholly in its tail)
-    const int64_t s0 = i0 % p.segment;
+    // whole chunk inside one segment's vector body (or wholly in its tail);
+    // per token the segment is the row, per tensor the whole view
+    const int64_t s0 = p.segment == p.cols ? c0 : (p.segment == p.rows * p.cols ? i0 : i0 % p.segment);
     const bool one_form = s0 + 15 < p.segment && ((s0 < body) == (s0 + 15 < body));
-    const bool vec = c0 + 16 <= p.cols && qdq_uniform(p, i0) && one_form &&
+    const bool vec = c0 + 16 <= p.cols && qdq_uniform_rc(p, r, c0) && one_form &&
                      ((uintptr_t)p.x + (uintptr_t)xi) % 16 == 0 &&
                      ((uintptr_t)p.y + (uintptr_t)yi * (f16 ? 2 : 4)) % 16 == 0;
     if (vec) {
-        const int64_t j = qdq_param(p, i0);
+        const int64_t j = qdq_param_rc(p, r, c0);
         const float sc = qdq_scale(p, j);
         const float zf = (float)qdq_zero(p, j);
         const bool fused = s0 < body;
         const float nzs = __fmul_rn(-zf, sc);
-        const v4i w = *reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.x) + xi);
+        const v4i w = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.x) + xi));
         const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
         float y[16];
 #pragma unroll
@@ -201,14 +239,15 @@ __global__ __launch_bounds__(256) void dequantize_kernel(QdqKern p)
                 }
                 v4i o;
                 __builtin_memcpy(&o, e8, 16);
-                dst[h] = o;
+                __builtin_nontemporal_store(o, dst + h);
             }
         } else {
             v4i* dst = reinterpret_cast<v4i*>(static_cast<float*>(p.y) + yi);
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
-                dst[h] = v4i{__float_as_int(y[4 * h]), __float_as_int(y[4 * h + 1]), __float_as_int(y[4 * h + 2]),
-                             __float_as_int(y[4 * h + 3])};
+                __builtin_nontemporal_store(v4i{__float_as_int(y[4 * h]), __float_as_int(y[4 * h + 1]),
+                                                 __float_as_int(y[4 * h + 2]), __float_as_int(y[4 * h + 3])},
+                                            dst + h);
             }
         }
         return;
