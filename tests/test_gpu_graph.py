@@ -1,0 +1,83 @@
+"""Calls captured into a HIP graph and replayed (as bench.py times them):
+every replay, with eager work and synchronizations between replays, must
+reproduce the eager result bit for bit -- the routes with split-K partials
+and a reduce, the fused ring passes, the GEMVs and the Q4_1 kernels."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import datagen as dg
+import nnops_amd as na
+from gpu_util import dev, host, announce
+
+pytestmark = pytest.mark.gpu
+
+
+def graph_replays_match(fn, out, replays=3):
+    import torch
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        fn(s)
+    torch.cuda.synchronize()
+    want = host(out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fn(s)
+    for r in range(replays):
+        out.zero_()                       # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(out)
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"replay {r} differs"
+
+
+@pytest.mark.parametrize("M,K,N,out", [(4096, 1024, 1024, "s8"), (333, 14336, 1024, "s8"), (1024, 512, 1024, "f16"),
+                                       (16, 4096, 1024, "s32"), (1, 4096, 2048, "s32")])
+def test_int8_routes_under_graph_replay(M, K, N, out):
+    import torch
+    announce(f"graph int8 {M}x{K}x{N} {out}")
+    a = dev(dg.act_s8(M + K, (M, K)))
+    w = dev(dg.ints(N + 1, (N, K), -127, 127))
+    sb = dev(dg.uniform(3, (N,), 0.001, 0.01))
+    tdt = {"s8": torch.int8, "f16": torch.float16, "s32": torch.int32}[out]
+    c = torch.zeros((M, N), dtype=tdt, device="cuda")
+    kind = {"s8": na.OUT_S8, "f16": na.OUT_F16, "s32": na.OUT_S32}[out]
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+
+    def fn(s):
+        na.gemm_i8(a, w, c, trans_b=True, out_kind=kind, s_a=0.02, s_b=sb, s_out=0.05,
+                   act=na.ACT_RELU if out != "s32" else na.ACT_NONE, workspace=ws, stream=s.cuda_stream)
+    graph_replays_match(fn, c)
+
+
+def test_q4_1_under_graph_replay():
+    import torch
+    announce("graph q4_1")
+    K, N = 4096, 2048
+    blk = dev(dg.q4_1_blocks(5, N, K))
+    for M in (1, 256):
+        a = dev(dg.normal(6 + M, (M, K)).astype(np.float16))
+        c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+
+        def fn(s, a=a, c=c, ws=ws):
+            na.gemm_q4_1(a, blk, c, n=N, trans_b=True, workspace=ws, stream=s.cuda_stream)
+        graph_replays_match(fn, c)
+
+
+def test_quantize_linear_under_graph_replay():
+    import torch
+    announce("graph qdq")
+    x = dev(dg.normal(7, (512, 1024)).astype(np.float16))
+    sc = dev(dg.uniform(8, (512,), 0.01, 0.05))
+    zp = dev(dg.ints(9, (512,), -4, 4, np.int8))
+    q = torch.zeros((512, 1024), dtype=torch.int8, device="cuda")
+    op = na.QuantizeLinear(axis=-1)
+    ins = [na.tensor(x), na.tensor(sc), na.tensor(zp)]
+    outs = [na.tensor(q)]
+
+    def fn(s):
+        assert op.compute(outs, ins, stream=s) == na.OK
+    graph_replays_match(fn, q)
