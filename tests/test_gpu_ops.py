@@ -181,3 +181,23 @@ def test_matmul_rank6_broadcast():
         ib = tuple(i if d > 1 else 0 for i, d in zip(idx, b_shape[:-2]))
         np.testing.assert_array_equal(got[idx], oracle.gemm_i8(np.ascontiguousarray(a[ia]),
                                                                np.ascontiguousarray(b[ib])))
+
+
+def test_linear_rank1_input_f32_out():
+    """A rank-1 X is one row over the same buffers (nnops' linear.cpp:234-246)."""
+    import torch
+    announce("linear rank1")
+    K, N = 640, 96
+    x = dg.act_s8(141, (K,))
+    w = dg.ints(142, (N, K), -127, 127)
+    bias = dg.normal(143, (N,)).astype(np.float32)
+    y = torch.zeros((N,), dtype=torch.float32, device="cuda")
+    op = na.Linear(output_dtype=na.DT_F32, act=na.EP_RELU)
+    ins = [na.tensor(dev(x), scale=0.03), na.tensor(dev(w), scale=0.002), na.tensor(dev(bias))]
+    shape, dt = op.output_desc(ins)
+    assert shape == [N] and dt == na.DT_F32
+    assert op.compute([na.tensor(y)], ins) == na.OK
+    torch.cuda.synchronize()
+    want = oracle.gemm_i8(x.reshape(1, K), w, trans_b=True, out_kind=oracle.OUT_F32, bias=bias, s_a=0.03, s_b=0.002,
+                          act=oracle.ACT_RELU).reshape(N)
+    np.testing.assert_array_equal(host(y).view(np.uint32), want.view(np.uint32))
