@@ -63,6 +63,16 @@ void init_epilogue(NnopsEpilogue& e)
     e.quant_param_count = 0;
 }
 
+QuantLinearAttributes to_qlinear(const NnopsQuantLinearAttrs* a)
+{
+    QuantLinearAttributes attrs;
+    if (a != nullptr) {
+        attrs.axis = a->axis;
+        attrs.output_dtype = static_cast<DataType>(a->output_dtype);
+    }
+    return attrs;
+}
+
 std::vector<TensorDesc> descs(const NnopsTensor* t, int32_t n)
 {
     std::vector<TensorDesc> d;
@@ -144,18 +154,6 @@ void nnops_quant_linear_attrs_init(NnopsQuantLinearAttrs* a)
     a->axis = -1;
     a->output_dtype = static_cast<int32_t>(DataType::s8);
 }
-
-namespace {
-QuantLinearAttributes to_qlinear(const NnopsQuantLinearAttrs* a)
-{
-    QuantLinearAttributes attrs;
-    if (a != nullptr) {
-        attrs.axis = a->axis;
-        attrs.output_dtype = static_cast<DataType>(a->output_dtype);
-    }
-    return attrs;
-}
-}  // namespace
 
 NnopsOp* nnops_quantize_linear_create(const NnopsQuantLinearAttrs* a, int32_t backend)
 {

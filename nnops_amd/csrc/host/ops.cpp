@@ -230,7 +230,7 @@ bool is_fp_quant_pair(DataType a, DataType b)
     return (a == DataType::f32 || a == DataType::f16) && b == DataType::s8;
 }
 
-NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, const QuantCall& q, int32_t out_kind)
+NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, int32_t out_kind)
 {
     NnopsGemmI8Args x{};
     x.m = g.m;
@@ -262,14 +262,14 @@ NnopsGemmQ41Args q41_args_from_geometry(const Geometry& g, const QuantCall& q, i
 
 /// Workspace of the int8 GEMM call: staging for host-side tables, then the
 /// GEMM's own partial-sum / split-K region.
-size_t i8_workspace(const Geometry& g, const QuantCall& q, int32_t out_kind)
+size_t i8_workspace(const Geometry& g, int32_t out_kind)
 {
     // The kernel plan (and so its region) depends on what a descriptor does not
     // carry: zero points, tables, pointer alignment. Size for the largest: the
     // plan of plain operands (the [K,N] column GEMV's partials), the plan with
     // zero points (a staged B^T plus K-split partials) and the plan of an
     // unaligned destination (raw partials for the reduce).
-    NnopsGemmI8Args x = i8_args_from_geometry(g, q, out_kind);
+    NnopsGemmI8Args x = i8_args_from_geometry(g, out_kind);
     size_t need = nnops_hip_gemm_i8_workspace_size(&x);
     x.zp_a_scalar = 1;
     need = std::max(need, nnops_hip_gemm_i8_workspace_size(&x));
@@ -296,13 +296,13 @@ size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDes
         return 0;
     }
     if (is_int8_matmul(a.dtype, b.dtype)) {
-        return i8_workspace(g, q, out_kind_of(out_dtype));
+        return i8_workspace(g, out_kind_of(out_dtype));
     }
     if (is_fp_quant_pair(a.dtype, b.dtype)) {
         if (g.trans_a) {
             return 0;
         }
-        return fp_quant_prefix(g) + i8_workspace(g, q, out_kind_of(a.dtype));
+        return fp_quant_prefix(g) + i8_workspace(g, out_kind_of(a.dtype));
     }
     if (is_q4_1_matmul(a.dtype, b.dtype)) {
         const DataType odt = out != nullptr ? out->dtype : a.dtype;
@@ -361,7 +361,7 @@ Status run_i8(const QuantCall& q, const Geometry& g, TensorView& out, const Tens
     if (q.add_to && ok == NNOPS_OUT_S32) {
         return Status::unsupported;
     }
-    NnopsGemmI8Args x = i8_args_from_geometry(g, q, ok);
+    NnopsGemmI8Args x = i8_args_from_geometry(g, ok);
     x.a_u8 = a.data_type() == DataType::u8;
     x.lda = a.row_stride_elems();
     x.ldb = g.b_packed ? packed_pitch(g.k) : b.row_stride_elems();

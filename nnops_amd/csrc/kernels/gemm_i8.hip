@@ -597,6 +597,7 @@ __device__ __forceinline__ BufRsrc buffer_rsrc(const void* base)
 #if __HIP_DEVICE_COMPILE__
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 #else
+    (void)base;
     return BufRsrc{};
 #endif
 }
@@ -606,6 +607,8 @@ __device__ __forceinline__ void buffer_load_lds16(BufRsrc r, int8_t* lds, int vo
 {
 #if __HIP_DEVICE_COMPILE__
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+#else
+    (void)r, (void)lds, (void)voff, (void)soff;
 #endif
 }
 
@@ -1296,6 +1299,7 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_lds(GemmI8Kern p)
     const BufRsrc rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.b + (int64_t)n0 * p.ldb), 0,
                                                          (int)span, 0x00020000);
 #else
+    (void)span;
     const BufRsrc rs{};
 #endif
     const int arow = lane & 15;

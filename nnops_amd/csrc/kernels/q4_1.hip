@@ -976,6 +976,7 @@ __device__ __forceinline__ QBufRsrc q_buffer_rsrc(const void* base, uint32_t byt
 #if __HIP_DEVICE_COMPILE__
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 #else
+    (void)base, (void)bytes;
     return QBufRsrc{};
 #endif
 }
@@ -984,6 +985,8 @@ __device__ __forceinline__ void q_buffer_load_lds16(QBufRsrc r, uint8_t* lds, in
 {
 #if __HIP_DEVICE_COMPILE__
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+#else
+    (void)r, (void)lds, (void)voff, (void)soff;
 #endif
 }
 
