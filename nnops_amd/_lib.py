@@ -142,6 +142,15 @@ def load(path: str = LIB_PATH):
         if not os.path.exists(path):
             raise RuntimeError(
                 f"nnops_amd native library missing: {path}; build it with `python -m nnops_amd.build`")
+        # One HIP runtime per process: torch ships its own libamdhip64 (same
+        # soname as ROCm's). Loaded after torch, this library binds to that
+        # copy; loaded first, it would bring in ROCm's and torch would then add
+        # its own beside it, so device pointers from one runtime would be
+        # unknown to the other. Import torch first when it is installed.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib_ = C.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib_, name)
