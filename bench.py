@@ -188,9 +188,9 @@ def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbu
             "rotated_weight_bytes": nbuf * K * N}
 
 
-def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=8):
+def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=8, trans_b=True):
     a = torch.from_numpy(dg.normal(401, (M, K)).astype("float16")).cuda()
-    base = torch.from_numpy(dg.q4_1_blocks(402, N, K)).cuda()
+    base = torch.from_numpy(dg.q4_1_blocks(402, N, K) if trans_b else dg.q4_1_blocks(402, K, N)).cuda()
     bufs = [base if i == 0 else torch.roll(base, shifts=20 * i, dims=1).contiguous() for i in range(nbuf)]
     c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     s = stream.cuda_stream
@@ -199,26 +199,33 @@ def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nb
     def step():
         b = bufs[it[0] % nbuf]
         it[0] += 1
-        na.gemm_q4_1(a, b, c, n=N, trans_b=True, stream=s)
+        na.gemm_q4_1(a, b, c, n=N, trans_b=trans_b, workspace=wsp, stream=s)
 
+    probe = na.GemmQ41Args()
+    probe.m, probe.n, probe.k, probe.trans_b, probe.a_f16 = M, N, K, int(trans_b), 1
+    probe.out_kind = na.OUT_F32
+    need = na.lib().nnops_hip_gemm_q4_1_workspace_size(C.byref(probe))
+    wsp = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     t = Timer(stream).time(step, steps, warmup)
     nbytes = N * (K // 32) * 20 + K * M * 2 + N * M * 4
     gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
     return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
-            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]",
+            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
             "rotated_weight_bytes": nbuf * N * (K // 32) * 20}
 
 
-def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336):
+def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, trans_b=True):
+    """Config 4's GEMM; trans_b=False times the literal [K][N/32] layout
+    (blocks along N) instead of the GGUF/Linear [N][K/32] one."""
     a = torch.from_numpy(dg.normal(403, (M, K)).astype("float16")).cuda()
-    b = torch.from_numpy(dg.q4_1_blocks(404, N, K)).cuda()
+    b = torch.from_numpy(dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)).cuda()
     c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     s = stream.cuda_stream
-    t = Timer(stream).time(lambda: na.gemm_q4_1(a, b, c, n=N, trans_b=True, stream=s), steps, warmup)
+    t = Timer(stream).time(lambda: na.gemm_q4_1(a, b, c, n=N, trans_b=trans_b, stream=s), steps, warmup)
     fl = 2.0 * M * N * K
     tf = fl / (t["mean_ms"] * 1e-3) / 1e12
     return {"tflops": tf, "frac_f16_mfma": tf / PEAK_F16_TFLOPS, "us": t["mean_ms"] * 1e3,
-            "M": M, "K": K, "N": N}
+            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]"}
 
 
 def cfg5_case(torch, dg, na, stream, steps, warmup):
@@ -498,6 +505,10 @@ def main():
         secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup)
         secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup,
                                                                 dequant=True)
+        secondary["cfg4_q4_1_gemv_m1_kn"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                          trans_b=False)
+        secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
+                                                            args.warmup, trans_b=False)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, max(5, args.steps // 5), args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {

@@ -13,10 +13,12 @@
 //                  off with the staged block sum. Bound: HBM.
 //   gemv_q4_1_kn   blocks along N ([K][N/32]), small M: a lane owns one
 //                  32-column block, waves split K, partial planes summed by
-//                  reduce_q4_1. Bound: HBM.
-//   gemm_q4_1_ring larger M, f16 A, blocks along K, K % 64 == 0: a 5-stage
-//                  LDS ring filled by DMA (A and the raw Q4_1 bytes), B decoded
-//                  per lane into MFMA operands with packed f16 math,
+//                  reduce_q4_1 (16 threads per output with many splits).
+//                  Bound: HBM.
+//   gemm_q4_1_ring larger M, f16 A, blocks along K, K % 64 == 0: a 4-stage
+//                  LDS ring filled by DMA (A and the raw Q4_1 bytes), 8 waves
+//                  of 128 x 32, B decoded per lane into MFMA operands with
+//                  packed f16 math,
 //                  v_mfma_f32_32x32x16_f16, f32 accumulate. Bound: MFMA.
 //   gemm_q4_1_mfma the other GEMM shapes: B tiles decoded to f16 (d*q + m in
 //                  f32, rounded once) into LDS, A tiles staged k-contiguous.
@@ -741,16 +743,37 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
     }
 }
 
+// Sum of the K-split partials: TPG threads per output element, each summing
+// every TPG-th split with four loads in flight, combined by a fixed shuffle
+// tree (the same order on every run).
+template <int TPG>
 __global__ __launch_bounds__(256) void reduce_q4_1(Q41Kern p)
 {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) / TPG;
+    const int j = threadIdx.x % TPG;
     const int64_t total = (int64_t)p.m * p.n;
-    if (i >= total) {
-        return;
+    const bool in = i < total;
+    const float* src = p.partial + (in ? i : 0);
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    if (in) {
+        int sp = j;
+        for (; sp + 3 * TPG < p.splits; sp += 4 * TPG) {
+            s0 += src[(int64_t)sp * total];
+            s1 += src[(int64_t)(sp + TPG) * total];
+            s2 += src[(int64_t)(sp + 2 * TPG) * total];
+            s3 += src[(int64_t)(sp + 3 * TPG) * total];
+        }
+        for (; sp < p.splits; sp += TPG) {
+            s0 += src[(int64_t)sp * total];
+        }
     }
-    float s = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp) {
-        s += p.partial[(int64_t)sp * total + i];
+    float s = (s0 + s1) + (s2 + s3);
+#pragma unroll
+    for (int off = 1; off < TPG; off <<= 1) {
+        s += __shfl_xor(s, off, TPG);
+    }
+    if (!in || j != 0) {
+        return;
     }
     const int m = (int)(i / p.n);
     const int n = (int)(i - (int64_t)m * p.n);
@@ -1320,7 +1343,11 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     hipLaunchKernelGGL((gemv_q4_1_kn<1, false>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
                 }
                 const int64_t total = (int64_t)kk.m * kk.n;
-                hipLaunchKernelGGL(reduce_q4_1, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
+                if (kk.splits >= 32) {
+                    hipLaunchKernelGGL(reduce_q4_1<16>, dim3((unsigned)((total * 16 + 255) / 256)), dim3(256), 0, s, kk);
+                } else {
+                    hipLaunchKernelGGL(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
+                }
             }
         }
     } else if (g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0) {
