@@ -1218,6 +1218,204 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 }
 
 
+// ---------------------------------------------------------------------------
+// MFMA GEMM, f16 A, B blocks along N ([K][N/32]: each k row holds one 20-byte
+// block per 32 columns), K % 64 == 0. Same 128 x 256 tile, 8 waves of 128 x
+// 32 (wave w owns the tile's block column w) and NS-stage DMA ring as
+// gemm_q4_1_ring; only B's staging and decode differ:
+//   Braw  the stage's 64 k rows x 160 bytes (the tile's 8 blocks of each row,
+//         contiguous in memory), 640 16-byte chunks; row k sits at slot row
+//         k ^ ((k >> 3) & 1), so the two lane halves of a fragment (rows k and
+//         k + 8) land 24 or 40 banks apart.
+// A lane's B operand is column n = lane & 31 of its wave's block at 8
+// consecutive k rows: per row the block's d | m dword (one address per lane
+// half: a broadcast read) and the nibble dword holding byte n & 15, nibble
+// n >> 4. Two rows decode per step: the byte permute pulls the lane's byte of
+// both rows, shift and mask keep the nibble under exponent byte 0x64, and
+// v_pk_fma_f16 applies the two rows' own d and m.
+// ---------------------------------------------------------------------------
+template <bool OUT16, int NS>
+__global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
+{
+    constexpr int W = 8, QA = 2;                    // A: 2 KiB pieces per wave per stage
+    constexpr int BM = 128, BN = 256, FM = 4;
+    constexpr int kRow = BN / 32 * 20;              // 160 bytes of B per k row
+    constexpr int kA = BM * 128, kB = 64 * kRow, kStage = kA + kB;
+    constexpr int kBPieces = kB / 1024;             // 10 x 1 KiB: waves 0, 1 issue two
+    static_assert(NS >= 3 && kBPieces > W && kBPieces <= 2 * W, "stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
+
+    const int tiles_m = (p.m + BM - 1) / BM;
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) {
+        bid = (bid & 7) * (nb >> 3) + (bid >> 3);     // consecutive logical tiles on one XCD
+    }
+    const int tm = bid % tiles_m, tn = bid / tiles_m; // the M tiles of a column band share B in L2
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kt = p.k / 64;
+    const bool two = wave < kBPieces - W;
+
+    const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
+    // this tile's blocks of row 0; a stage's rows start s * 64 * ldb further
+    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * 20;
+    const int64_t b_end = (int64_t)(p.k - 1) * p.ldb + (int64_t)((p.n + 31) / 32) * 20 - (int64_t)(n0 / 32) * 20;
+    int a_off[QA], b_off[2];
+#pragma unroll
+    for (int i = 0; i < QA; ++i) {
+        const int ra = 8 * (QA * wave + i) + (lane >> 3);
+        const int ca = (lane & 7) ^ ((ra >> 1) & 7);
+        a_off[i] = min(ra, p.m - 1 - m0) * (int)p.lda * 2 + ca * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = (wave + W * i) * 64 + lane;     // chunk = LDS slot
+        const int pr = q / 10, c = q - pr * 10;
+        const int k = pr ^ ((pr >> 3) & 1);
+        b_off[i] = k * (int)p.ldb + c * 16;
+    }
+    auto issue = [&](int s) {
+        uint8_t* base = ring + (s % NS) * kStage;
+#pragma unroll
+        for (int i = 0; i < QA; ++i) {
+            q_buffer_load_lds16(rsa, base + (QA * wave + i) * 1024, a_off[i], s * 128);
+        }
+        const int64_t row0 = (int64_t)s * 64 * p.ldb;
+        const QBufRsrc rsb = q_buffer_rsrc(b0 + row0, (uint32_t)std::min<int64_t>(b_end - row0, 0x7fffffff));
+        q_buffer_load_lds16(rsb, base + kA + wave * 1024, b_off[0], 0);
+        if (two) {
+            q_buffer_load_lds16(rsb, base + kA + (wave + W) * 1024, b_off[1], 0);
+        }
+    };
+    auto wait_ring = [&](bool full) {
+        if (full) {
+            wait_vmcnt<0>();
+        } else if (two) {
+            wait_vmcnt<(NS - 2) * (QA + 2)>();
+        } else {
+            wait_vmcnt<(NS - 2) * (QA + 1)>();
+        }
+    };
+
+    const int fr = lane & 31, kh = lane >> 5;
+    auto a_frag = [&](const uint8_t* st, int i, int ks) {
+        const int r = i * 32 + fr;
+        const int c = (2 * ks + kh) ^ ((r >> 1) & 7);
+        return *reinterpret_cast<const v8h*>(st + r * 128 + c * 16);
+    };
+    // per-lane constants of the B decode: the block's byte offset in a row,
+    // the nibble dword, and the permute picking byte n & 3 of two rows into
+    // bytes 0 and 2
+    const int bcol = 20 * wave;
+    const int qdw = bcol + 4 + 4 * ((fr & 15) >> 2);
+    const uint32_t qsel = 0x0c000c00u | ((uint32_t)(4 + (fr & 3)) << 16) | (uint32_t)(fr & 3);
+    // Rows 16 ks + 8 kh + e, e + 1 (e even) sit at slot rows 16 ks + e + 9 kh
+    // and 16 ks + e + 1 + 7 kh: a lane base per row of the pair, the rest are
+    // immediate offsets
+    const int lb0 = kA + 9 * kh * kRow, lb1 = kA + (7 * kh + 1) * kRow;
+    const int bd0 = lb0 + bcol, bq0 = lb0 + qdw, bd1 = lb1 + bcol, bq1 = lb1 + qdw;
+    // Low-nibble lanes keep 0x0f under exponent byte 0x64: f16 1024 + q.
+    // High-nibble lanes keep 0xf0 under 0x54: in [64, 128) a mantissa unit is
+    // 1/16, so the nibble's bits 4-7 read as 64 + q. Each subtracts its own
+    // bias, exactly, and no lane shifts.
+    const bool hi_nib = fr >= 16;
+    const uint32_t kMask = hi_nib ? 0x00f000f0u : 0x000f000fu;
+    const uint32_t kMagic = hi_nib ? 0x54005400u : 0x64006400u;
+    const v2h kBias = __builtin_bit_cast(v2h, kMagic);
+    auto b_frag = [&](const uint8_t* st, int ks) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const int o = (16 * ks + e) * kRow;
+            const uint32_t dm0 = *reinterpret_cast<const uint32_t*>(st + bd0 + o);
+            const uint32_t dm1 = *reinterpret_cast<const uint32_t*>(st + bd1 + o);
+            const uint32_t x0 = *reinterpret_cast<const uint32_t*>(st + bq0 + o);
+            const uint32_t x1 = *reinterpret_cast<const uint32_t*>(st + bq1 + o);
+            uint32_t t;
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(t) : "v"(__builtin_amdgcn_perm(x1, x0, qsel)),
+                "v"(kMask), "v"(kMagic));
+            const v2h q = __builtin_bit_cast(v2h, t) - kBias;
+            const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x05040100u));
+            const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x07060302u));
+            w[e / 2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, d2, m2));
+        }
+        return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+    };
+
+    v16f acc[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        acc[i] = v16f{0.0f};
+    }
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        if (s < kt) {
+            issue(s);
+        }
+    }
+    wait_ring(kt < NS - 1);
+    __syncthreads();
+
+    v8h fa0[FM], fa1[FM], fb0, fb1;
+    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[FM]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            fa[i] = a_frag(st, i, ks);
+        }
+    };
+    auto mfma_slice = [&](const v8h (&fa)[FM], const v8h& fb) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb, acc[i], 0, 0, 0);
+        }
+    };
+    for (int t = 0; t < kt; ++t) {
+        const uint8_t* st = ring + (t % NS) * kStage;
+        const bool more = t + NS - 1 < kt;
+        if (more) {
+            issue(t + NS - 1);
+        }
+        fb0 = b_frag(st, 0);
+        load_a(st, 0, fa0);
+        fb1 = b_frag(st, 1);
+        load_a(st, 1, fa1);
+        mfma_slice(fa0, fb0);
+        fb0 = b_frag(st, 2);
+        load_a(st, 2, fa0);
+        mfma_slice(fa1, fb1);
+        fb1 = b_frag(st, 3);
+        load_a(st, 3, fa1);
+        mfma_slice(fa0, fb0);
+        mfma_slice(fa1, fb1);
+        wait_ring(!more);
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+
+    const int n = n0 + 32 * wave + fr;
+    if (n < p.n) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+                if (m < p.m) {
+                    if constexpr (OUT16) {
+                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)acc[i][r];
+                    } else {
+                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = acc[i][r];
+                    }
+                }
+            }
+        }
+    }
+}
+
+
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -1359,6 +1557,15 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             hipLaunchKernelGGL((gemm_q4_1_ring<true, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         } else {
             hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
+        }
+    } else if (!g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0 &&
+               (g->ldb_bytes % 16) == 0 && ((uintptr_t)g->b & 15) == 0 && g->k * g->ldb_bytes < INT32_MAX) {
+        // blocks along N: the same ring, B rows staged raw and decoded per lane
+        const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
+        if (k.out_f16) {
+            hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4>), dim3(tiles), dim3(512), 0, s, k);
+        } else {
+            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4>), dim3(tiles), dim3(512), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

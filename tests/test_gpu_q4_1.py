@@ -35,6 +35,8 @@ CASES = [
     (1, 4096, 1003), (2, 4096, 77),
     # ring GEMM (K % 64 == 0): ragged M and N tiles, a single k step
     (300, 1024, 520), (7, 64, 256),
+    # blocks-along-N ring (row bytes % 16 == 0): ragged M and N, N not a tile multiple
+    (300, 1024, 1000), (129, 192, 384), (40, 4096, 2048),
 ]
 
 
@@ -86,5 +88,19 @@ def test_config4_full(M):
     got = run_gpu(a, blk, N, trans_b=True)
     rows = (0, M) if M <= 4 else (200, 216)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=True, rows=rows)
+    err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
+    assert err <= TOL, err
+
+
+def test_config4_kn_m512():
+    """Config 4 with the [K][N/32] weight layout (blocks along N), M=512,
+    sampled rows."""
+    announce("config4 kn M=512")
+    M, K, N = 512, 4096, 14336
+    a = dg.normal(612, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(613, K, N)
+    got = run_gpu(a, blk, N, trans_b=False)
+    rows = (120, 136)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
     err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
     assert err <= TOL, err
