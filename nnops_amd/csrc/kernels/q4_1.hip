@@ -1324,22 +1324,32 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     const uint32_t kMask = hi_nib ? 0x00f000f0u : 0x000f000fu;
     const uint32_t kMagic = hi_nib ? 0x54005400u : 0x64006400u;
     const v2h kBias = __builtin_bit_cast(v2h, kMagic);
-    auto b_frag = [&](const uint8_t* st, int ks) {
+    // B fragment of slice ks in two steps, so that the next slice's reads are
+    // in flight while this one decodes: 16 raw dwords, then 8 f16 values
+    struct BRaw {
+        uint32_t dm0[4], dm1[4], x0[4], x1[4];
+    };
+    auto b_read = [&](const uint8_t* st, int ks, BRaw& r) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int o = (16 * ks + 2 * e) * kRow;
+            r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + o);
+            r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + o);
+            r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + o);
+            r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + o);
+        }
+    };
+    auto b_decode = [&](const BRaw& r) {
         uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const int o = (16 * ks + e) * kRow;
-            const uint32_t dm0 = *reinterpret_cast<const uint32_t*>(st + bd0 + o);
-            const uint32_t dm1 = *reinterpret_cast<const uint32_t*>(st + bd1 + o);
-            const uint32_t x0 = *reinterpret_cast<const uint32_t*>(st + bq0 + o);
-            const uint32_t x1 = *reinterpret_cast<const uint32_t*>(st + bq1 + o);
+        for (int e = 0; e < 4; ++e) {
             uint32_t t;
-            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(t) : "v"(__builtin_amdgcn_perm(x1, x0, qsel)),
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(t) : "v"(__builtin_amdgcn_perm(r.x1[e], r.x0[e], qsel)),
                 "v"(kMask), "v"(kMagic));
             const v2h q = __builtin_bit_cast(v2h, t) - kBias;
-            const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x05040100u));
-            const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x07060302u));
-            w[e / 2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, d2, m2));
+            const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(r.dm1[e], r.dm0[e], 0x05040100u));
+            const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(r.dm1[e], r.dm0[e], 0x07060302u));
+            w[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, d2, m2));
         }
         return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
     };
@@ -1378,17 +1388,22 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
         if (more) {
             issue(t + NS - 1);
         }
-        fb0 = b_frag(st, 0);
+        BRaw r0, r1;
+        b_read(st, 0, r0);
         load_a(st, 0, fa0);
-        fb1 = b_frag(st, 1);
+        b_read(st, 1, r1);
+        fb0 = b_decode(r0);
         load_a(st, 1, fa1);
+        b_read(st, 2, r0);
         mfma_slice(fa0, fb0);
-        fb0 = b_frag(st, 2);
+        fb1 = b_decode(r1);
         load_a(st, 2, fa0);
+        b_read(st, 3, r1);
         mfma_slice(fa1, fb1);
-        fb1 = b_frag(st, 3);
+        fb0 = b_decode(r0);
         load_a(st, 3, fa1);
         mfma_slice(fa0, fb0);
+        fb1 = b_decode(r1);
         mfma_slice(fa1, fb1);
         wait_ring(!more);
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
