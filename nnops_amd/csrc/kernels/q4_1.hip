@@ -12,8 +12,10 @@
 //                  and dotted with v_dot2_f32_f16; the 64*sum(a) offset comes
 //                  off with the staged block sum. Bound: HBM.
 //   gemv_q4_1_kn   blocks along N ([K][N/32]), small M: a lane owns one
-//                  32-column block, waves split K, partial planes summed by
-//                  reduce_q4_1 (16 threads per output with many splits).
+//                  nibble dword (8 columns) of a block, 16 rows of loads in
+//                  flight; waves and workgroups split K, partial planes
+//                  summed by reduce_q4_1 (16 threads per output with many
+//                  splits).
 //                  Bound: HBM.
 //   gemm_q4_1_ring larger M, f16 A, blocks along K, K % 64 == 0: a 4-stage
 //                  LDS ring filled by DMA (A and the raw Q4_1 bytes), 8 waves
@@ -668,56 +670,89 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
 template <int MT, bool AF16>
 __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
 {
-    __shared__ float red[3][MT][32][64];
+    // Lane l owns nibble dword l & 3 of block (l >> 2) of the workgroup's 16
+    // blocks: columns 4j .. 4j+3 (low nibbles) and 16+4j .. 16+4j+3 (high)
+    // of the block. The 4 waves take interleaved k rows; per row a lane
+    // loads the block's d|m dword and its nibble dword, 16 rows at a time.
+    constexpr int U = 16;
+    __shared__ float red[3][MT][8][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nblocks = (p.n + 31) / 32;
-    const int bn = blockIdx.x * 64 + lane;           // this lane's n block
+    const int bl = blockIdx.x * 16 + (lane >> 2);
+    const int jq = lane & 3;
     const int split = blockIdx.y;
     const int kper = (p.k + p.splits - 1) / p.splits;
     const int k0 = split * kper;
     const int k1 = min(p.k, k0 + kper);
-    const bool live = bn < nblocks;
-    const uint8_t* col = p.b + (int64_t)min(bn, nblocks - 1) * 20;
+    const bool live = bl < nblocks;
+    const uint8_t* col = p.b + (int64_t)min(bl, nblocks - 1) * 20;
 
-    float acc[MT][32];
+    float acc[MT][8];
     float accm[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         accm[m] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
+        for (int j = 0; j < 8; ++j) {
             acc[m][j] = 0.0f;
         }
     }
-    for (int k = k0 + wave; k < k1; k += 4) {
-        const uint8_t* src = col + (int64_t)k * p.ldb;
-        const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
-        const uint32_t q4 = *reinterpret_cast<const uint32_t*>(src + 16);
-        const uint32_t qs[4] = {(uint32_t)x.y, (uint32_t)x.z, (uint32_t)x.w, q4};
-        const float d = h2f((uint32_t)x.x & 0xffffu);
-        const float mn = h2f((uint32_t)x.x >> 16);
+    auto row = [&](int k, uint32_t dm, uint32_t x, const float (&a)[MT]) {
+        const float d = h2f(dm & 0xffffu);
+        const float mn = h2f(dm >> 16);
+        const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const float a = m < p.m ? load_a<AF16>(p, m, k) : 0.0f;
-            const float ad = a * d;
-            accm[m] = fmaf(a, mn, accm[m]);
+            const float ad = a[m] * d;
+            accm[m] = fmaf(a[m], mn, accm[m]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    acc[m][4 * i + b] = fmaf(ad, (float)((qs[i] >> (8 * b)) & 15u), acc[m][4 * i + b]);
-                    acc[m][16 + 4 * i + b] =
-                        fmaf(ad, (float)((qs[i] >> (8 * b + 4)) & 15u), acc[m][16 + 4 * i + b]);
-                }
+            for (int b = 0; b < 4; ++b) {
+                acc[m][b] = fmaf(ad, (float)((lo >> (8 * b)) & 0xffu), acc[m][b]);
+                acc[m][4 + b] = fmaf(ad, (float)((hi >> (8 * b)) & 0xffu), acc[m][4 + b]);
             }
+        }
+    };
+    // whole batches of U rows, the ones past k1 masked (their A value is 0
+    // and their address clamped), so a wave waits on memory once per batch
+    for (int k = k0 + wave; k < k1; k += 4 * U) {
+        using AT = std::conditional_t<AF16, _Float16, float>;
+        uint32_t dm[U], x[U];
+        AT ar[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kr = k + 4 * u;
+            const uint8_t* src = col + (int64_t)min(kr, k1 - 1) * p.ldb;
+            dm[u] = *reinterpret_cast<const uint32_t*>(src);
+            x[u] = *reinterpret_cast<const uint32_t*>(src + 4 + 4 * jq);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                // unconditional load (clamped row and column), masked below:
+                // a branch or a use here would split the batch
+                ar[u][m] = static_cast<const AT*>(p.a)[(int64_t)min(m, p.m - 1) * p.lda + min(kr, k1 - 1)];
+            }
+        }
+        // keep the scheduler from sinking the loads into the arithmetic
+        // below (it would otherwise keep only two rows in flight)
+        __builtin_amdgcn_sched_barrier(0);
+        float a[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                a[u][m] = (m < p.m && k + 4 * u < k1) ? (float)ar[u][m] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            row(k + 4 * u, dm[u], x[u], a[u]);
         }
     }
     if (wave > 0) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 red[wave - 1][m][j][lane] = acc[m][j] + accm[m];
             }
         }
@@ -731,13 +766,13 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
         if (m >= p.m) {
             continue;
         }
+        float* dst = p.partial + ((int64_t)split * p.m + m) * p.n + bl * 32 + 4 * jq;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const int n = bn * 32 + j;
-            const float v = acc[m][j] + accm[m] + red[0][m][j][lane] + red[1][m][j][lane] +
-                            red[2][m][j][lane];
+        for (int j = 0; j < 8; ++j) {
+            const int n = bl * 32 + 4 * jq + (j & 3) + 16 * (j >> 2);
+            const float v = acc[m][j] + accm[m] + red[0][m][j][lane] + red[1][m][j][lane] + red[2][m][j][lane];
             if (n < p.n) {
-                p.partial[((int64_t)split * p.m + m) * p.n + n] = v;
+                dst[(j & 3) + 16 * (j >> 2)] = v;
             }
         }
     }
@@ -1436,10 +1471,10 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 inline int kn_splits(const NnopsGemmQ41Args& g)
 {
-    // enough blocks to cover the CUs several times, at least 16 k rows per split
-    const int64_t nblk = ((g.n + 31) / 32 + 63) / 64;
-    int64_t s = (1024 + nblk - 1) / nblk;
-    s = std::min<int64_t>(s, std::max<int64_t>(1, g.k / 16));
+    // about 1024 workgroups (16 blocks wide each), at least 64 k rows per split
+    const int64_t ncol = ((g.n + 31) / 32 + 15) / 16;
+    int64_t s = (1024 + ncol - 1) / ncol;
+    s = std::min<int64_t>(s, std::max<int64_t>(1, g.k / 64));
     return (int)std::max<int64_t>(1, std::min<int64_t>(s, 256));
 }
 
@@ -1545,7 +1580,7 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             } else {
                 kk.splits = kn_splits(*g);
                 kk.partial = static_cast<float*>(workspace);
-                const unsigned bx = (unsigned)(((g->n + 31) / 32 + 63) / 64);
+                const unsigned bx = (unsigned)(((g->n + 31) / 32 + 15) / 16);
                 if (g->a_f16) {
                     if (kk.m == 1) {
                         hipLaunchKernelGGL((gemv_q4_1_kn<1, true>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
