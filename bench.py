@@ -228,6 +228,44 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
             "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]"}
 
 
+def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8):
+    """Config 4 with the [K][N/32] weight prepacked (MatMul.prepackWeights:
+    the nibble and d|m planes), through the operator API. M=1 rotates over
+    nbuf packed weights (more than the MALL) so HBM is measured."""
+    a = torch.from_numpy(dg.normal(405, (M, K)).astype("float16")).cuda()
+    base = torch.from_numpy(dg.q4_1_blocks(406, K, N)).cuda()
+    op = na.MatMul(transpose_b=False)
+    nb = nbuf if M <= 2 else 1
+    packed = []
+    for i in range(nb):
+        raw = base if i == 0 else torch.roll(base, shifts=20 * i, dims=1).contiguous()
+        # prepacked on torch's current stream, which also owns raw's memory
+        packed.append(op.prepack(na.tensor(raw, dtype=na.DT_Q4_1, shape=[K, N]))[1])
+        torch.cuda.synchronize()
+    c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    at, ct = na.tensor(a), na.tensor(c)
+    wsn = op.workspace_size([at, packed[0]], [ct])
+    ws = torch.empty(max(wsn, 1), dtype=torch.uint8, device="cuda")
+    s = stream.cuda_stream
+    it = [0]
+
+    def step():
+        w = packed[it[0] % nb]
+        it[0] += 1
+        op.compute([ct], [at, w], stream=s, workspace=ws)
+
+    t = Timer(stream).time(step, steps, warmup)
+    out = {"us": t["mean_ms"] * 1e3, "M": M, "K": K, "N": N, "weight_layout": "[K][N/32 blocks], prepacked planes"}
+    if M <= 2:
+        nbytes = N * (K // 32) * 20 + K * M * 2 + N * M * 4
+        out.update(gbs=nbytes / (t["mean_ms"] * 1e-3) / 1e9, bytes=nbytes)
+        out["frac_hbm"] = out["gbs"] / PEAK_HBM_GBS
+    else:
+        out["tflops"] = 2.0 * M * N * K / (t["mean_ms"] * 1e-3) / 1e12
+        out["frac_f16_mfma"] = out["tflops"] / PEAK_F16_TFLOPS
+    return out
+
+
 def cfg5_case(torch, dg, na, stream, steps, warmup):
     import numpy as np
     M, K, N = 333, 14336, 4096
@@ -509,6 +547,10 @@ def main():
                                                           trans_b=False)
         secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
                                                             args.warmup, trans_b=False)
+        secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, args.steps,
+                                                                      args.warmup, M=1)
+        secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream,
+                                                                        max(5, args.steps // 5), args.warmup, M=512)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, max(5, args.steps // 5), args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {

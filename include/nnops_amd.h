@@ -143,6 +143,24 @@ size_t nnops_hip_prepack_i8_bytes(int64_t k, int64_t n);
 int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int32_t trans_b, void* out,
                          void* stream);
 
+/* Prepacked Q4_1 B with blocks along N (nnops' MatMul::prepackWeights,
+ * src/ops/matmul.cpp:96-141; the CPU path packs no Q4_1 form,
+ * matmul_helper.cpp:695-723, this is the gfx950 one). From B [K][ceil(N/32)]
+ * blocks (trans_b = 0), row pitch ldb_bytes, it writes the same blocks as
+ * two planes, structure of arrays:
+ *   nibbles  [K][nbn * 16] bytes, block j of row k at k * nbn * 16 + 16 j;
+ *   d|m      [K][dmp] u32 (f16 d low, f16 m high), dmp = nbn rounded up to
+ *            4, at byte offset align_up(K * nbn * 16, 256);
+ * nbn = ceil(N / 32). A call then passes b = out, ldb_bytes = nbn * 16,
+ * b_soa = 1, b_dm = out + that offset, ldb_dm = dmp: the GEMV's and GEMM's
+ * lane loads become contiguous 4- and 16-byte runs instead of 20-byte
+ * strides. Blocks along K (trans_b = 1) already stream as whole rows and have
+ * no packed form (NNOPS_UNSUPPORTED). `out` must be 256-byte aligned and hold
+ * nnops_hip_prepack_q4_1_bytes(k, n) bytes. Stream-ordered, no allocation. */
+size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n);
+int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b, void* out,
+                           void* stream);
+
 /* Q4_1-weight GEMM  C[M,N] = A[M,K] x dequant(B).
  * Replaces nnops' fp x q4_1 route: matmul_qblock_fused (small M,
  * src/backend/cpu/matmul/matmul_qblock_fused.cpp:174-197) and FpRoute with
@@ -162,6 +180,12 @@ typedef struct NnopsGemmQ41Args {
     int64_t ldb_bytes;
     int32_t trans_b, a_f16;
     int32_t out_kind;           /* NNOPS_OUT_F32 / NNOPS_OUT_F16 */
+    /* b_soa = 1: B is the prepacked blocks-along-N form (trans_b = 0) of
+     * nnops_hip_prepack_q4_1: b = the nibble plane (row pitch ldb_bytes),
+     * b_dm = the d|m plane (row pitch ldb_dm u32 elements). */
+    int32_t b_soa;
+    const uint32_t* b_dm;
+    int64_t ldb_dm;
 } NnopsGemmQ41Args;
 
 size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* args);

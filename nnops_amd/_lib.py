@@ -53,6 +53,7 @@ class GemmQ41Args(C.Structure):
         ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
         ("lda", C.c_int64), ("ldc", C.c_int64), ("ldb_bytes", C.c_int64),
         ("trans_b", C.c_int32), ("a_f16", C.c_int32), ("out_kind", C.c_int32),
+        ("b_soa", C.c_int32), ("b_dm", C.c_void_p), ("ldb_dm", C.c_int64),
     ]
 
 
@@ -107,6 +108,9 @@ SIGNATURES = {
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
     "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
+    "nnops_hip_prepack_q4_1_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
+    "nnops_hip_prepack_q4_1": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p,
+                                         C.c_void_p]),
     "nnops_hip_prepack_i8": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p,
                                        C.c_void_p]),
     "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),

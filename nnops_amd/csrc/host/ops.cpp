@@ -69,13 +69,27 @@ Status matmul_geometry(const TensorDesc& a, const TensorDesc& b, bool ta, bool t
     g.k = ta ? am : ak;
     if (b.layout == TensorLayout::PackedBHip) {
         // A packed B carries N but no K: K is A's, and the blob must be large
-        // enough for it (nnops: the backend's numel check, matmul.cpp:84-90)
-        if (b.rank != 2 || b.dtype != DataType::s8 ||
-            b0 * b1 < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(g.k, b0))) {
+        // enough for it (nnops: the backend's numel check, matmul.cpp:84-90).
+        // s8: [N][kp] rows (read as transposed); q4_1: the two planes of a
+        // blocks-along-N weight (read as [K, N])
+        if (b.rank != 2) {
+            return Status::invalid_argument;
+        }
+        if (b.dtype == DataType::s8) {
+            if (b0 * b1 < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(g.k, b0))) {
+                return Status::invalid_argument;
+            }
+            g.trans_b = true;
+        } else if (b.dtype == DataType::q4_1) {
+            if (b0 * static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, b1)) <
+                static_cast<int64_t>(nnops_hip_prepack_q4_1_bytes(g.k, b0))) {
+                return Status::invalid_argument;
+            }
+            g.trans_b = false;
+        } else {
             return Status::invalid_argument;
         }
         g.n = b0;
-        g.trans_b = true;
         g.b_packed = true;
     } else {
         const int64_t kb = tb ? b1 : b0;
@@ -251,12 +265,21 @@ NnopsGemmQ41Args q41_args_from_geometry(const Geometry& g, const QuantCall& q, i
     x.m = g.m;
     x.n = g.n;
     x.k = g.k;
-    x.trans_b = q.trans_b;
+    (void)q;
+    x.trans_b = g.trans_b;
     x.a_f16 = 1;
     x.lda = g.k;
     x.ldc = g.n;
-    x.ldb_bytes = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, q.trans_b ? g.k : g.n));
+    x.ldb_bytes = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, g.trans_b ? g.k : g.n));
     x.out_kind = out_kind;
+    if (g.b_packed) {
+        // the planes of nnops_hip_prepack_q4_1: nibble rows of nbn * 16 bytes,
+        // d|m rows of nbn rounded up to 4 dwords (b_dm is set with the pointer)
+        const int64_t nbn = (g.n + 31) / 32;
+        x.b_soa = 1;
+        x.ldb_bytes = nbn * 16;
+        x.ldb_dm = (nbn + 3) / 4 * 4;
+    }
     return x;
 }
 
@@ -597,7 +620,12 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
         x.a_f16 = a.data_type() == DataType::f16;
         x.lda = a.row_stride_elems();
         x.ldc = out.row_stride_elems();
-        x.ldb_bytes = b.pitch();
+        if (g.b_packed) {
+            x.b_dm = reinterpret_cast<const uint32_t*>(
+                b.ptr<const char>() + align_up(static_cast<size_t>(g.k * x.ldb_bytes)));
+        } else {
+            x.ldb_bytes = b.pitch();
+        }
         const size_t need = nnops_hip_gemm_q4_1_workspace_size(&x);
         if (need > 0 && (workspace == nullptr || ws_bytes < need)) {
             return Status::not_initialized;
@@ -888,7 +916,7 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
 }
 
 // ===========================================================================
-// prepackWeights: s8 B -> TensorLayout::PackedBHip
+// prepackWeights: s8 B, and q4_1 B with blocks along N -> TensorLayout::PackedBHip
 // ===========================================================================
 namespace {
 
@@ -896,12 +924,19 @@ namespace {
 /// 96-141): an empty outputs[0] is the query and receives the descriptor
 /// [N, ceil(bytes / N)] (s8, PackedBHip, pitched at its row length, carrying
 /// the weight's QuantParams); a populated one is filled on ctx's stream. A
-/// weight with no packed form (anything but a 2-D s8 B) answers empty.
+/// weight with no packed form (anything but a 2-D s8 B or a 2-D q4_1 B with
+/// blocks along N) answers empty.
+Status prepack_q4_1(const TensorView& raw, std::span<TensorView> outputs, const ComputeContext& ctx);
+
 Status prepack_s8(const TensorView& raw, bool trans_b, std::span<TensorView> outputs, const ComputeContext& ctx,
                   Backend backend)
 {
     if (outputs.empty()) {
         return Status::invalid_argument;
+    }
+    if (backend == Backend::HIP && raw.rank() == 2 && raw.data_type() == DataType::q4_1 && !trans_b &&
+        raw.layout() == TensorLayout::Dense) {
+        return prepack_q4_1(raw, outputs, ctx);
     }
     if (backend != Backend::HIP || raw.rank() != 2 || raw.data_type() != DataType::s8 ||
         raw.layout() != TensorLayout::Dense) {
@@ -934,6 +969,37 @@ Status prepack_s8(const TensorView& raw, bool trans_b, std::span<TensorView> out
     }
     const int rc = nnops_hip_prepack_i8(raw.ptr<const int8_t>(), k, n, raw.row_stride_elems(), trans_b ? 1 : 0,
                                         o.ptr<void>(), ctx.hip_stream);
+    return from_code(rc);
+}
+
+/// A blocks-along-N q4_1 weight [K, N] (values) -> PackedBHip q4_1 [N, cols]:
+/// the blob of nnops_hip_prepack_q4_1, cols the values whose q4_1 row bytes
+/// times N cover it. Blocks along K (transpose_b) have no packed form.
+Status prepack_q4_1(const TensorView& raw, std::span<TensorView> outputs, const ComputeContext& ctx)
+{
+    const int64_t k = raw.shape(0), n = raw.shape(1);
+    if (n <= 0 || k <= 0) {
+        if (outputs[0].is_empty()) {
+            outputs[0] = TensorView{};
+            return Status::ok;
+        }
+        return Status::invalid_argument;
+    }
+    const int64_t bytes = static_cast<int64_t>(nnops_hip_prepack_q4_1_bytes(k, n));
+    const int64_t cols = (bytes + n * 20 - 1) / (n * 20) * 32;
+    const int64_t pitch = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, cols));
+    const int64_t shape[2] = {n, cols};
+    if (outputs[0].is_empty()) {
+        outputs[0] = TensorView(shape, DataType::q4_1, nullptr, pitch, TensorLayout::PackedBHip, raw.quant_params());
+        return Status::ok;
+    }
+    const TensorView& o = outputs[0];
+    if (o.layout() != TensorLayout::PackedBHip || o.data_type() != DataType::q4_1 || o.rank() != 2 ||
+        o.shape(0) != n || o.shape(1) != cols || o.pitch() != pitch) {
+        return Status::invalid_argument;
+    }
+    const int rc = nnops_hip_prepack_q4_1(raw.ptr<const uint8_t>(), k, n, raw.pitch(), 0, o.ptr<void>(),
+                                          ctx.hip_stream);
     return from_code(rc);
 }
 

@@ -43,6 +43,8 @@ struct Q41Kern {
     int64_t lda, ldc, ldb;   // lda/ldc in elements, ldb in bytes
     int out_f16;
     int splits;
+    const uint32_t* bdm; // SoA d|m plane [K][ldbdm] (prepacked blocks along N)
+    int64_t ldbdm;       // u32 elements
 };
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
@@ -667,7 +669,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
 // ---------------------------------------------------------------------------
 // GEMV, blocks along N: partial[split][m][n].
 // ---------------------------------------------------------------------------
-template <int MT, bool AF16>
+template <int MT, bool AF16, bool SOA>
 __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
 {
     // Lane l owns nibble dword l & 3 of block (l >> 2) of the workgroup's 16
@@ -722,9 +724,16 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kr = k + 4 * u;
-            const uint8_t* src = col + (int64_t)min(kr, k1 - 1) * p.ldb;
-            dm[u] = *reinterpret_cast<const uint32_t*>(src);
-            x[u] = *reinterpret_cast<const uint32_t*>(src + 4 + 4 * jq);
+            if constexpr (SOA) {
+                // planes: a block's 16 nibble bytes and its d|m dword
+                const int64_t r = min(kr, k1 - 1);
+                dm[u] = p.bdm[r * p.ldbdm + min(bl, nblocks - 1)];
+                x[u] = *reinterpret_cast<const uint32_t*>(p.b + r * p.ldb + min(bl, nblocks - 1) * 16 + 4 * jq);
+            } else {
+                const uint8_t* src = col + (int64_t)min(kr, k1 - 1) * p.ldb;
+                dm[u] = *reinterpret_cast<const uint32_t*>(src);
+                x[u] = *reinterpret_cast<const uint32_t*>(src + 4 + 4 * jq);
+            }
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 // unconditional load (clamped row and column), masked below:
@@ -1268,13 +1277,21 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 // n >> 4. Two rows decode per step: the byte permute pulls the lane's byte of
 // both rows, shift and mask keep the nibble under exponent byte 0x64, and
 // v_pk_fma_f16 applies the two rows' own d and m.
+// SOA: B is the prepacked form (nibble plane + d|m plane): a stage holds the
+// tile's 64 x 128 nibble bytes (8 pieces, one per wave) and then its 64 x 32
+// d|m bytes (2 pieces, waves 0 and 1), both with the slot-row order above
+// (rows k and k + 8 then sit 32 banks apart in the nibbles and 8 in d|m).
 // ---------------------------------------------------------------------------
-template <bool OUT16, int NS>
+template <bool OUT16, int NS, bool SOA>
 __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 {
     constexpr int W = 8, QA = 2;                    // A: 2 KiB pieces per wave per stage
     constexpr int BM = 128, BN = 256, FM = 4;
     constexpr int kRow = BN / 32 * 20;              // 160 bytes of B per k row
+    // slot-row pitch of the d|m dwords and of the nibble dwords, and where the
+    // d|m rows start within the stage's B
+    constexpr int kRowD = SOA ? BN / 32 * 4 : kRow, kRowQ = SOA ? BN / 32 * 16 : kRow;
+    constexpr int kDmAt = SOA ? 64 * kRowQ : 0;
     constexpr int kA = BM * 128, kB = 64 * kRow, kStage = kA + kB;
     constexpr int kBPieces = kB / 1024;             // 10 x 1 KiB: waves 0, 1 issue two
     static_assert(NS >= 3 && kBPieces > W && kBPieces <= 2 * W, "stages");
@@ -1295,8 +1312,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 
     const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
     // this tile's blocks of row 0; a stage's rows start s * 64 * ldb further
-    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * 20;
-    const int64_t b_end = (int64_t)(p.k - 1) * p.ldb + (int64_t)((p.n + 31) / 32) * 20 - (int64_t)(n0 / 32) * 20;
+    const int nbn = (p.n + 31) / 32;
+    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * (SOA ? 16 : 20);
+    const int64_t b_end = (int64_t)(p.k - 1) * p.ldb + (int64_t)(nbn - n0 / 32) * (SOA ? 16 : 20);
+    const int64_t ldd = p.ldbdm * 4;                // SOA: d|m row pitch in bytes
+    const uint8_t* d0 = reinterpret_cast<const uint8_t*>(p.bdm) + (int64_t)(n0 / 32) * 4;
+    const int64_t d_end = (int64_t)(p.k - 1) * ldd + (int64_t)(nbn - n0 / 32) * 4;
     int a_off[QA], b_off[2];
 #pragma unroll
     for (int i = 0; i < QA; ++i) {
@@ -1307,9 +1328,18 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int q = (wave + W * i) * 64 + lane;     // chunk = LDS slot
-        const int pr = q / 10, c = q - pr * 10;
-        const int k = pr ^ ((pr >> 3) & 1);
-        b_off[i] = k * (int)p.ldb + c * 16;
+        if constexpr (SOA) {
+            // nibble pieces: 8 chunks per row; d|m pieces: 2 chunks per row
+            const int qq = i == 0 ? q : q - W * 64;
+            const int cpr = i == 0 ? 8 : 2;
+            const int pr = qq / cpr, c = qq - pr * cpr;
+            const int k = pr ^ ((pr >> 3) & 1);
+            b_off[i] = k * (int)(i == 0 ? p.ldb : ldd) + c * 16;
+        } else {
+            const int pr = q / 10, c = q - pr * 10;
+            const int k = pr ^ ((pr >> 3) & 1);
+            b_off[i] = k * (int)p.ldb + c * 16;
+        }
     }
     auto issue = [&](int s) {
         uint8_t* base = ring + (s % NS) * kStage;
@@ -1321,7 +1351,14 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
         const QBufRsrc rsb = q_buffer_rsrc(b0 + row0, (uint32_t)std::min<int64_t>(b_end - row0, 0x7fffffff));
         q_buffer_load_lds16(rsb, base + kA + wave * 1024, b_off[0], 0);
         if (two) {
-            q_buffer_load_lds16(rsb, base + kA + (wave + W) * 1024, b_off[1], 0);
+            if constexpr (SOA) {
+                const int64_t drow0 = (int64_t)s * 64 * ldd;
+                const QBufRsrc rsd =
+                    q_buffer_rsrc(d0 + drow0, (uint32_t)std::min<int64_t>(d_end - drow0, 0x7fffffff));
+                q_buffer_load_lds16(rsd, base + kA + (wave + W) * 1024, b_off[1], 0);
+            } else {
+                q_buffer_load_lds16(rsb, base + kA + (wave + W) * 1024, b_off[1], 0);
+            }
         }
     };
     auto wait_ring = [&](bool full) {
@@ -1343,14 +1380,15 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     // per-lane constants of the B decode: the block's byte offset in a row,
     // the nibble dword, and the permute picking byte n & 3 of two rows into
     // bytes 0 and 2
-    const int bcol = 20 * wave;
-    const int qdw = bcol + 4 + 4 * ((fr & 15) >> 2);
+    const int bcol = SOA ? kDmAt + 4 * wave : 20 * wave;
+    const int qdw = SOA ? 16 * wave + 4 * ((fr & 15) >> 2) : bcol + 4 + 4 * ((fr & 15) >> 2);
     const uint32_t qsel = 0x0c000c00u | ((uint32_t)(4 + (fr & 3)) << 16) | (uint32_t)(fr & 3);
     // Rows 16 ks + 8 kh + e, e + 1 (e even) sit at slot rows 16 ks + e + 9 kh
     // and 16 ks + e + 1 + 7 kh: a lane base per row of the pair, the rest are
     // immediate offsets
-    const int lb0 = kA + 9 * kh * kRow, lb1 = kA + (7 * kh + 1) * kRow;
-    const int bd0 = lb0 + bcol, bq0 = lb0 + qdw, bd1 = lb1 + bcol, bq1 = lb1 + qdw;
+    const int sr0 = 9 * kh, sr1 = 7 * kh + 1;
+    const int bd0 = kA + sr0 * kRowD + bcol, bq0 = kA + sr0 * kRowQ + qdw;
+    const int bd1 = kA + sr1 * kRowD + bcol, bq1 = kA + sr1 * kRowQ + qdw;
     // Low-nibble lanes keep 0x0f under exponent byte 0x64: f16 1024 + q.
     // High-nibble lanes keep 0xf0 under 0x54: in [64, 128) a mantissa unit is
     // 1/16, so the nibble's bits 4-7 read as 64 + q. Each subtracts its own
@@ -1367,11 +1405,11 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     auto b_read = [&](const uint8_t* st, int ks, BRaw& r) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int o = (16 * ks + 2 * e) * kRow;
-            r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + o);
-            r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + o);
-            r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + o);
-            r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + o);
+            const int od = (16 * ks + 2 * e) * kRowD, oq = (16 * ks + 2 * e) * kRowQ;
+            r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + od);
+            r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + od);
+            r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + oq);
+            r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + oq);
         }
     };
     auto b_decode = [&](const BRaw& r) {
@@ -1466,6 +1504,31 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 }
 
 
+// ---------------------------------------------------------------------------
+// Prepack of a blocks-along-N weight into its two planes (structure of
+// arrays): thread per block, the 16 nibble bytes as one 16-byte store, the
+// d|m dword into its plane; the plane's row padding is zeroed.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t ldb, int k, int nbn,
+                                                       uint8_t* nib, uint32_t* dm, int64_t dmp)
+{
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)k * nbn) {
+        return;
+    }
+    const int64_t r = idx / nbn;
+    const int j = (int)(idx - r * nbn);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(b + r * ldb + (int64_t)j * 20);
+    const v4i q{(int)src[1], (int)src[2], (int)src[3], (int)src[4]};
+    *reinterpret_cast<v4i*>(nib + idx * 16) = q;
+    dm[r * dmp + j] = src[0];
+    if (j == nbn - 1) {
+        for (int64_t t = nbn; t < dmp; ++t) {
+            dm[r * dmp + t] = 0u;
+        }
+    }
+}
+
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -1483,6 +1546,24 @@ inline bool use_gemv(const NnopsGemmQ41Args& g)
     return g.m <= 2 || !g.a_f16;
 }
 
+// The blocks-along-N ring: f16 A with 16-byte rows, K % 64 == 0, 16-byte B
+// rows, and every stage offset within a buffer resource's 31-bit range
+inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
+{
+    return !g.trans_b && g.a_f16 && g.k % 64 == 0 && (g.lda % 8) == 0 && ((uintptr_t)g.a & 15) == 0 &&
+           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 && g.k * g.ldb_bytes < INT32_MAX &&
+           (!g.b_soa || g.k * g.ldb_dm * 4 < INT32_MAX);
+}
+
+// The GEMV loop (two rows of A per pass) serves every M of a prepacked
+// weight the ring cannot take
+inline bool gemv_route(const NnopsGemmQ41Args& g)
+{
+    return use_gemv(g) || (g.b_soa && !kn_ring_ok(g));
+}
+
+inline int64_t prepack_q41_dmp(int64_t n) { return ((n + 31) / 32 + 3) / 4 * 4; }
+
 }  // namespace
 }  // namespace nnops_amd
 
@@ -1490,7 +1571,9 @@ using namespace nnops_amd;
 
 extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
 {
-    if (g == nullptr || !use_gemv(*g) || g->trans_b) {
+    // a prepacked weight may take the GEMV loop whatever M is (pointer
+    // alignment, which a size query does not see, decides)
+    if (g == nullptr || g->trans_b || !(use_gemv(*g) || g->b_soa)) {
         return 0;
     }
     return align_up((size_t)kn_splits(*g) * (size_t)g->m * (size_t)g->n * sizeof(float));
@@ -1513,9 +1596,14 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
     if (g->m > INT32_MAX || g->n > INT32_MAX || g->k > INT32_MAX) {
         return NNOPS_UNSUPPORTED;
     }
-    const int64_t row_bytes = g->trans_b ? (g->k + 31) / 32 * 20 : (g->n + 31) / 32 * 20;
+    const int64_t nbn = (g->n + 31) / 32;
+    const int64_t row_bytes = g->trans_b ? (g->k + 31) / 32 * 20 : nbn * (g->b_soa ? 16 : 20);
     if (g->lda < g->k || g->ldc < g->n || g->ldb_bytes < row_bytes || (g->ldb_bytes & 3) ||
         ((uintptr_t)g->b & 3)) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    if (g->b_soa && (g->trans_b || g->b_dm == nullptr || (g->ldb_bytes & 15) || ((uintptr_t)g->b & 15) ||
+                     ((uintptr_t)g->b_dm & 15) || (g->ldb_dm & 3) || g->ldb_dm < nbn)) {
         return NNOPS_INVALID_ARGUMENT;
     }
     const size_t need = nnops_hip_gemm_q4_1_workspace_size(g);
@@ -1534,8 +1622,11 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
     k.ldc = g->ldc;
     k.ldb = g->ldb_bytes;
     k.out_f16 = g->out_kind == NNOPS_OUT_F16;
+    k.bdm = g->b_soa ? g->b_dm : nullptr;
+    k.ldbdm = g->b_soa ? g->ldb_dm : 0;
+    const bool soa = g->b_soa != 0;
 
-    if (use_gemv(*g)) {
+    if (gemv_route(*g)) {
         // rows of A handled per pass: 2 (f16 pairs), 1 for f32 A
         const int mt = g->a_f16 ? 2 : 1;
         for (int m0 = 0; m0 < k.m; m0 += mt) {
@@ -1581,14 +1672,23 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 kk.splits = kn_splits(*g);
                 kk.partial = static_cast<float*>(workspace);
                 const unsigned bx = (unsigned)(((g->n + 31) / 32 + 15) / 16);
-                if (g->a_f16) {
-                    if (kk.m == 1) {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                const dim3 grid(bx, kk.splits);
+                if (g->a_f16 && kk.m == 1) {
+                    if (soa) {
+                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true, true>), grid, dim3(256), 0, s, kk);
                     } else {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true, false>), grid, dim3(256), 0, s, kk);
                     }
+                } else if (g->a_f16) {
+                    if (soa) {
+                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true, true>), grid, dim3(256), 0, s, kk);
+                    } else {
+                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true, false>), grid, dim3(256), 0, s, kk);
+                    }
+                } else if (soa) {
+                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false, true>), grid, dim3(256), 0, s, kk);
                 } else {
-                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false>), dim3(bx, kk.splits), dim3(256), 0, s, kk);
+                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false, false>), grid, dim3(256), 0, s, kk);
                 }
                 const int64_t total = (int64_t)kk.m * kk.n;
                 if (kk.splits >= 32) {
@@ -1608,14 +1708,19 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         } else {
             hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         }
-    } else if (!g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0 &&
-               (g->ldb_bytes % 16) == 0 && ((uintptr_t)g->b & 15) == 0 && g->k * g->ldb_bytes < INT32_MAX) {
+    } else if (kn_ring_ok(*g)) {
         // blocks along N: the same ring, B rows staged raw and decoded per lane
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
         if (k.out_f16) {
-            hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4>), dim3(tiles), dim3(512), 0, s, k);
+            if (soa) {
+                hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4, true>), dim3(tiles), dim3(512), 0, s, k);
+            } else {
+                hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4, false>), dim3(tiles), dim3(512), 0, s, k);
+            }
+        } else if (soa) {
+            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4, true>), dim3(tiles), dim3(512), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4>), dim3(tiles), dim3(512), 0, s, k);
+            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4, false>), dim3(tiles), dim3(512), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
@@ -1625,6 +1730,36 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
         }
     }
+    return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+}
+
+extern "C" size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n)
+{
+    if (k <= 0 || n <= 0) {
+        return 0;
+    }
+    return align_up((size_t)k * (size_t)((n + 31) / 32) * 16) + (size_t)k * (size_t)prepack_q41_dmp(n) * 4;
+}
+
+extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b,
+                                      void* out, void* stream)
+{
+    if (trans_b) {
+        return NNOPS_UNSUPPORTED;  // blocks along K: no packed form
+    }
+    if (b == nullptr || out == nullptr || k <= 0 || n <= 0 || k > INT32_MAX || n > INT32_MAX) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    const int64_t nbn = (n + 31) / 32;
+    if (ldb_bytes < nbn * 20 || (ldb_bytes & 3) || ((uintptr_t)b & 3) || ((uintptr_t)out & 255)) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    uint8_t* nib = static_cast<uint8_t*>(out);
+    uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)k * (size_t)nbn * 16));
+    const int64_t blocks = k * nbn;
+    hipLaunchKernelGGL(prepack_q4_1_kn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), b, ldb_bytes, (int)k, (int)nbn, nib, dm,
+                       prepack_q41_dmp(n));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
 

@@ -238,6 +238,36 @@ def test_prepack_query_descriptor():
     out = (L.Tensor * 1)()
     assert lib.nnops_op_prepack_weights(op._h, ins, 1, out, 1, None) == na.OK
     assert out[0].rank == 0
+    # q4_1 with blocks along N ([K, N], transpose_b false): PackedBHip q4_1
+    # [N, cols], cols the values whose row bytes times N cover the two planes
+    q_bytes = lib.nnops_hip_prepack_q4_1_bytes(256, 100)
+    nbn = 4
+    assert q_bytes == ((256 * nbn * 16 + 255) // 256) * 256 + 256 * 4 * 4
+    qop = na.MatMul(transpose_b=False)
+    ins = (L.Tensor * 1)(desc([256, 100], na.DT_Q4_1))
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(qop._h, ins, 1, out, 1, None) == na.OK
+    cols = -(-q_bytes // (100 * 20)) * 32
+    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == cols
+    assert out[0].dtype == na.DT_Q4_1 and out[0].layout == L.LAYOUT_PACKED_B_HIP
+    assert out[0].pitch == cols // 32 * 20
+    qpacked = out[0]
+    shape, dt = qop.output_desc([desc([7, 256], na.DT_F16), qpacked])
+    assert shape == [7, 100] and dt == na.DT_F16
+    # A with a larger K than the blob was packed for
+    assert qop.validate([desc([7, 4096], na.DT_F16), qpacked], [desc([7, 100], na.DT_F16)]) \
+        == na.INVALID_ARGUMENT
+    # blocks along K (transpose_b, and Linear's [N, K] weight): no packed form
+    tb = na.MatMul(transpose_b=True)
+    ins = (L.Tensor * 1)(desc([100, 256], na.DT_Q4_1))
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(tb._h, ins, 1, out, 1, None) == na.OK
+    assert out[0].rank == 0
+    lq = na.Linear()
+    out = (L.Tensor * 1)()
+    assert lib.nnops_op_prepack_weights(lq._h, ins, 1, out, 1, None) == na.OK
+    assert out[0].rank == 0
+    assert lib.nnops_hip_prepack_q4_1(None, 256, 100, 80, 1, None, None) == na.UNSUPPORTED
     # a packed B: output descriptor from its N and A's K; a blob too small for K is rejected
     packed = desc([100, -(-nbytes // 100)], na.DT_S8)
     packed.layout = L.LAYOUT_PACKED_B_HIP

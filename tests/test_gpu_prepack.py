@@ -2,7 +2,9 @@
 gives bit-for-bit the result of the raw weight on every route (GEMV, small-M
 MFMA, ring GEMM, split K), for [K,N] and [N,K] raw forms, with the precomputed
 column sums standing in for the per-call pass (u8 A, A zero points), and
-through the fp-activation and dequantizing routes."""
+through the fp-activation and dequantizing routes; and the packed q4_1
+weight with blocks along N (two planes) gives bit-for-bit the raw weight's
+result on the GEMV and ring routes, within the Q4_1 tolerance elsewhere."""
 from __future__ import annotations
 
 import numpy as np
@@ -97,3 +99,64 @@ def test_prepack_rejects_mismatched_buffer_and_k():
     a = dg.act_s8(92, (4, 512))
     c = torch.zeros((4, N), dtype=torch.int32, device="cuda")
     assert op.compute([na.tensor(c)], [na.tensor(dev(a)), packed]) == na.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("M,K,N,a_f16", [(1, 4096, 1000, True), (2, 1024, 300, True), (40, 4096, 2048, True),
+                                         (300, 1024, 1000, True), (129, 192, 384, True), (3, 512, 256, False)])
+def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
+    import torch
+    announce(f"prepack q4_1 {M}x{K}x{N} f16={a_f16}")
+    seed = 7 * M + K + N
+    a = dg.normal(seed, (M, K)).astype(np.float16 if a_f16 else np.float32)
+    blk = dg.q4_1_blocks(seed + 1, K, N)                 # [K][N/32] blocks
+    op = na.MatMul(transpose_b=False)
+    wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
+    buf, packed = op.prepack(wt)
+    assert packed is not None and packed.layout == na.LAYOUT_PACKED_B_HIP and packed.dtype == na.DT_Q4_1
+    at = na.tensor(dev(a))
+    got_p = run(op, at, packed, torch.float32, (M, N))
+    got_r = run(op, at, wt, torch.float32, (M, N))
+    np.testing.assert_array_equal(got_p, got_r)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
+    err = float(np.max(np.abs(got_p - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
+    assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40)])
+def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
+    """K % 64 != 0 with M > 2: the packed weight takes the GEMV loop (two rows
+    of A per pass), the raw one the generic MFMA kernel; both within the
+    Q4_1 tolerance of the oracle."""
+    import torch
+    announce(f"prepack q4_1 ragged {M}x{K}x{N}")
+    a = dg.normal(M + K, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(N + K, K, N)
+    op = na.MatMul(transpose_b=False)
+    wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
+    _, packed = op.prepack(wt)
+    got = run(op, na.tensor(dev(a)), packed, torch.float32, (M, N))
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
+    err = float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
+    assert err <= 2e-3, err
+
+
+def test_matmul_q4_1_prepacked_config4_kn():
+    """Config 4 with the [K][N/32] weight prepacked: M=1 in full, M=512 on
+    sampled rows, each equal to the raw weight's result."""
+    import torch
+    announce("prepack q4_1 config4")
+    K, N = 4096, 14336
+    blk = dg.q4_1_blocks(6101, K, N)
+    op = na.MatMul(transpose_b=False)
+    wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
+    _, packed = op.prepack(wt)
+    for M, rows in ((1, (0, 1)), (512, (300, 316))):
+        a = dg.normal(6102 + M, (M, K)).astype(np.float16)
+        at = na.tensor(dev(a))
+        got_p = run(op, at, packed, torch.float32, (M, N))
+        got_r = run(op, at, wt, torch.float32, (M, N))
+        np.testing.assert_array_equal(got_p, got_r)
+        want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
+        g, w = got_p[rows[0]:rows[1]], want[rows[0]:rows[1]]
+        err = float(np.max(np.abs(g - w)) / max(np.max(np.abs(w)), np.sqrt(np.mean(w ** 2))))
+        assert err <= 2e-3, err
