@@ -37,7 +37,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy", "ceilings"])
+    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy", "ceilings",
+                                                           "vendor"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -263,6 +264,38 @@ def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nb
     else:
         out["tflops"] = 2.0 * M * N * K / (t["mean_ms"] * 1e-3) / 1e12
         out["frac_f16_mfma"] = out["tflops"] / PEAK_F16_TFLOPS
+    return out
+
+
+def vendor_reference(torch, steps=50, warmup=10):
+    """The vendor libraries on the same shapes, as a yardstick for the
+    hand-written kernels: hipBLASLt's int8 GEMM (torch._int_mm, int32 out)
+    at config 2's 4096^3 with B row- and column-major, and its f16 GEMM at
+    config 4's 512 x 4096 x 14336 (no dequantization) and at 4096^3. Eager
+    launches on the current stream, HIP events around `steps` calls."""
+    def t(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e3
+    out = {}
+    a = torch.randint(-127, 127, (4096, 4096), dtype=torch.int8, device="cuda")
+    b = torch.randint(-127, 127, (4096, 4096), dtype=torch.int8, device="cuda")
+    bt = b.t().contiguous().t()
+    for name, bb in (("int8_4096_b_row_major", b), ("int8_4096_b_col_major", bt)):
+        us = t(lambda: torch._int_mm(a, bb))
+        out[name] = {"us": us, "tops": 2 * 4096 ** 3 / us / 1e6}
+    for name, (m, k, n) in (("f16_512x4096x14336", (512, 4096, 14336)), ("f16_4096", (4096, 4096, 4096))):
+        x = torch.randn(m, k, dtype=torch.float16, device="cuda")
+        w = torch.randn(k, n, dtype=torch.float16, device="cuda")
+        us = t(lambda: x @ w)
+        out[name] = {"us": us, "tflops": 2 * m * k * n / us / 1e6}
     return out
 
 
@@ -505,6 +538,12 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"workload": "copy", "bytes_per_copy": 2 ** 28, "copies": 3}))
+        return
+    if args.workload == "vendor":
+        ours = {"cfg2_s8_ring": run_cfg2(args, torch, dg, na, stream)["ms"] * 1e3,
+                "cfg4_q4_1_gemm_m512": q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
+                                                     args.warmup)["us"]}
+        print(json.dumps({"workload": "vendor", "vendor": vendor_reference(torch), "ours_us": ours}))
         return
     if args.workload == "ceilings":
         print(json.dumps({"workload": "ceilings", **ceilings(torch, na, stream)}))
