@@ -700,7 +700,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
             acc[m][j] = 0.0f;
         }
     }
-    auto row = [&](int k, uint32_t dm, uint32_t x, const float (&a)[MT]) {
+    auto row = [&](uint32_t dm, uint32_t x, const float (&a)[MT]) {
         const float d = h2f(dm & 0xffffu);
         const float mn = h2f(dm >> 16);
         const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
@@ -754,7 +754,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            row(k + 4 * u, dm[u], x[u], a[u]);
+            row(dm[u], x[u], a[u]);
         }
     }
     if (wave > 0) {
