@@ -160,3 +160,27 @@ def test_matmul_q4_1_prepacked_config4_kn():
         g, w = got_p[rows[0]:rows[1]], want[rows[0]:rows[1]]
         err = float(np.max(np.abs(g - w)) / max(np.max(np.abs(w)), np.sqrt(np.mean(w ** 2))))
         assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("M", [2, 40])
+def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
+    """f16 A -> f16 C (nnops: the output follows A) through the packed
+    planes, equal to the raw weight's result on the GEMV (M=2) and ring
+    (M=40) routes; and a batched A [2, M, K] against the one packed weight."""
+    import torch
+    announce(f"prepack q4_1 f16 out / batched M={M}")
+    K, N = 1024, 512
+    a = dg.normal(900 + M, (2, M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(901 + M, K, N)
+    op = na.MatMul(transpose_b=False)
+    wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
+    _, packed = op.prepack(wt)
+    at = na.tensor(dev(a))
+    got_p = run(op, at, packed, torch.float16, (2, M, N))
+    got_r = run(op, at, wt, torch.float16, (2, M, N))
+    np.testing.assert_array_equal(got_p.view(np.uint16), got_r.view(np.uint16))
+    for bi in range(2):
+        want = oracle.gemm_q4_1(a[bi], blk, N, trans_b=False, w_round_f16=True, c_f16=True).astype(np.float32)
+        g = got_p[bi].astype(np.float32)
+        err = float(np.max(np.abs(g - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
+        assert err <= 2e-3, err
