@@ -122,11 +122,12 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     assert err <= 2e-3, err
 
 
-@pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40)])
+@pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200)])
 def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
-    """K % 64 != 0 with M > 2: the packed weight takes the GEMV loop (two rows
-    of A per pass), the raw one the generic MFMA kernel; both within the
-    Q4_1 tolerance of the oracle."""
+    """Ragged shapes. K % 64 != 0 with M > 2: the packed weight takes the GEMV
+    loop (two rows of A per pass). N = 200 (7 blocks per row, d|m rows padded
+    to 8): the packed weight takes the ring. The raw one takes the generic
+    MFMA kernel in both cases; all within the Q4_1 tolerance of the oracle."""
     import torch
     announce(f"prepack q4_1 ragged {M}x{K}x{N}")
     a = dg.normal(M + K, (M, K)).astype(np.float16)
