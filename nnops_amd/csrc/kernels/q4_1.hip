@@ -3,27 +3,30 @@
 // and the high nibble of byte j-16 otherwise).
 //
 // Kernels
-//   gemv_q4_1_nk   blocks along K ([N][K/32], Linear/GGUF form), small M.
-//                  A (a K-chunk of it) is staged in LDS once per block with its
-//                  per-block sums; every lane streams whole 20-byte blocks
-//                  (one dwordx4 + one dword, 64 consecutive blocks per wave
-//                  instruction pair = 1280 contiguous bytes). f16 A: nibbles are
-//                  widened with the 0x54 exponent trick (f16 0x54qq = 64 + q/16)
-//                  and dotted with v_dot2_f32_f16; the 64*sum(a) offset comes
-//                  off with the staged block sum. Bound: HBM.
-//   gemv_q4_1_kn   blocks along N ([K][N/32]), small M: a lane owns one
-//                  nibble dword (8 columns) of a block, 16 rows of loads in
-//                  flight; waves and workgroups split K, partial planes
-//                  summed by reduce_q4_1 (16 threads per output with many
-//                  splits).
-//                  Bound: HBM.
-//   gemm_q4_1_ring larger M, f16 A, blocks along K, K % 64 == 0: a 4-stage
-//                  LDS ring filled by DMA (A and the raw Q4_1 bytes), 8 waves
-//                  of 128 x 32, B decoded per lane into MFMA operands with
-//                  packed f16 math,
-//                  v_mfma_f32_32x32x16_f16, f32 accumulate. Bound: MFMA.
-//   gemm_q4_1_mfma the other GEMM shapes: B tiles decoded to f16 (d*q + m in
-//                  f32, rounded once) into LDS, A tiles staged k-contiguous.
+//   gemv_q4_1_pipe  blocks along K ([N][K/32], Linear/GGUF form), K = 4096,
+//                   M <= 2 per launch: each wave DMAs its 4 rows (one
+//                   contiguous 10 KiB span) into LDS and decodes each (row,
+//                   block half) as its pieces land; nibbles widened with the
+//                   0x54 exponent trick (f16 0x54qq = 64 + q/16) and dotted
+//                   with v_dot2_f32_f16 against A. Bound: HBM.
+//   gemv_q4_1_lds,  the same decode for the other [N][K/32] GEMV shapes (rows
+//   gemv_q4_1_rows, staged in LDS, or read straight from HBM; f32 A).
+//   gemv_q4_1_nk
+//   gemv_q4_1_kn    blocks along N ([K][N/32]) or its prepacked planes, small
+//                   M: a lane owns one nibble dword (8 columns) of a block, 16
+//                   rows of loads in flight; waves and workgroups split K,
+//                   partial planes summed by reduce_q4_1. Bound: HBM.
+//   gemm_q4_1_ring  larger M, f16 A, blocks along K, K % 64 == 0: a 4-stage
+//                   LDS ring filled by DMA (A and the raw Q4_1 bytes), 8 waves
+//                   of 128 x 32, B decoded per lane into MFMA operands with
+//                   packed f16 math, v_mfma_f32_32x32x16_f16. Bound: MFMA.
+//   gemm_q4_1_kn_ring  the same ring for blocks along N (raw rows or the
+//                   prepacked planes), each lane decoding its column at 8
+//                   consecutive k rows.
+//   gemm_q4_1_mfma  the other GEMM shapes: B tiles decoded to f16 (d*q + m in
+//                   f32, rounded once) into LDS, A tiles staged k-contiguous.
+//   prepack_q4_1_kn prepackWeights of a blocks-along-N weight: its nibble
+//                   plane and its d|m plane.
 #include "common.hpp"
 
 
