@@ -185,3 +185,27 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
         g = got_p[bi].astype(np.float32)
         err = float(np.max(np.abs(g - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
         assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("K,N", [(64, 200), (96, 1024)])
+def test_q4_1_packed_blob_layout(K, N):
+    """The packed q4_1 blob byte for byte: nibble plane [K][nbn*16], then at
+    align_up(K*nbn*16, 256) the d|m plane [K][nbn rounded up to 4] (padding
+    zeroed), restated here with numpy from the raw [K][nbn] 20-byte blocks."""
+    announce(f"prepack q4_1 blob layout {K}x{N}")
+    blk = dg.q4_1_blocks(K * 7 + N, K, N)                # uint8 [K, nbn*20]
+    nbn = (N + 31) // 32
+    op = na.MatMul(transpose_b=False)
+    buf, packed = op.prepack(na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N]))
+    import torch
+    torch.cuda.synchronize()
+    got = host(buf)
+    b3 = blk.reshape(K, nbn, 20)
+    nib = b3[:, :, 4:].reshape(-1)
+    dmp = (nbn + 3) // 4 * 4
+    dm = np.zeros((K, dmp, 4), np.uint8)
+    dm[:, :nbn, :] = b3[:, :, :4]
+    off = (K * nbn * 16 + 255) // 256 * 256
+    assert na.lib().nnops_hip_prepack_q4_1_bytes(K, N) == off + K * dmp * 4
+    np.testing.assert_array_equal(got[:nib.size], nib)
+    np.testing.assert_array_equal(got[off:off + dm.size], dm.reshape(-1))
