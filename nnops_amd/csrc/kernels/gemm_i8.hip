@@ -926,27 +926,40 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         const bool f16 = ep.out_kind == NNOPS_OUT_F16;
         const bool relu = ep.act == NNOPS_ACT_RELU;
         const bool pre = ep.add_to && ep.residual_pre, post = ep.add_to && !ep.residual_pre;
+        // per 4-column group (j, g): the columns' scales and bias, loaded once
+        // for the FM row fragments that share them
+        struct ColFp {
+            v4f sb, bias;
+            int n;
+        };
+        auto col_fp = [&](int j, int g) {
+            ColFp cp;
+            cp.n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+            cp.sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+            cp.bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (cp.n < p.n) {
+                if (ep.s_b != nullptr) {
+                    cp.sb = *reinterpret_cast<const v4f*>(ep.s_b + cp.n);
+                }
+                if (ep.bias_fp != nullptr) {
+                    if (f16) {
+                        const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + cp.n;
+                        cp.bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
+                    } else {
+                        cp.bias = *reinterpret_cast<const v4f*>(static_cast<const float*>(ep.bias_fp) + cp.n);
+                    }
+                }
+            }
+            return cp;
+        };
         // the 4 values of (i, j, g) for this lane: row wm0 + 32 i + (lane & 31),
-        // columns wn0 + 32 j + 8 g + 4 (lane >> 5) .. + 3
-        auto values = [&](int i, int j, int g, float sa) {
-            const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+        // columns cp.n .. + 3
+        auto values = [&](int i, int j, int g, const ColFp& cp, float sa) {
+            const int n = cp.n;
             const int m = m0 + wm0 + i * 32 + (lane & 31);
             v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             if (n >= p.n || m >= p.m) {
                 return o;
-            }
-            v4f sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
-            if (ep.s_b != nullptr) {
-                sb = *reinterpret_cast<const v4f*>(ep.s_b + n);
-            }
-            v4f bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (ep.bias_fp != nullptr) {
-                if (f16) {
-                    const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + n;
-                    bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
-                } else {
-                    bias = *reinterpret_cast<const v4f*>(static_cast<const float*>(ep.bias_fp) + n);
-                }
             }
             v4f old = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             if (ep.add_to) {
@@ -960,9 +973,9 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float f = __fmul_rn((float)acc[i][j][4 * g + e], __fmul_rn(sa, sb[e]));
+                float f = __fmul_rn((float)acc[i][j][4 * g + e], __fmul_rn(sa, cp.sb[e]));
                 if (ep.bias_fp != nullptr) {
-                    f = __fadd_rn(f, bias[e]);
+                    f = __fadd_rn(f, cp.bias[e]);
                 }
                 if (pre) {
                     f = __fadd_rn(f, old[e]);
@@ -1009,10 +1022,11 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
                         for (int g = 0; g < 4; ++g) {
                             const int q = jj * 8 + 2 * g + (lane >> 5);
+                            const ColFp cp = col_fp(j, g);
 #pragma unroll
                             for (int i = 0; i < FM; ++i) {
                                 const int r = i * 32 + (lane & 31);
-                                const v4f o = values(i, j, g, sa_i[i]);
+                                const v4f o = values(i, j, g, cp, sa_i[i]);
                                 int8_t* dst = tile + r * RB + ((q ^ (r % GPS)) * E);
                                 if constexpr (ESZ == 4) {
                                     *reinterpret_cast<v4f*>(dst) = o;
@@ -1065,13 +1079,14 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                    const ColFp cp = col_fp(j, g);
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
                         const int m = m0 + wm0 + i * 32 + (lane & 31);
                         if (m >= p.m || n >= p.n) {
                             continue;
                         }
-                        const v4f o = values(i, j, g, sa_i[i]);
+                        const v4f o = values(i, j, g, cp, sa_i[i]);
                         char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
                         if (f16) {
                             _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
