@@ -1155,6 +1155,27 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     const int nb = in ? (int)(gid - (int64_t)m * groups) * 4 : 0;
     const int64_t slab = (int64_t)p.m * p.n;
     const int32_t* src = sk.part + (int64_t)m * p.n + nb;
+    // the output pass's row / column constants and the residual word, loaded
+    // with the partials rather than after them
+    const EpiParams& ep = p.ep;
+    const bool s32 = ep.out_kind == NNOPS_OUT_S32;
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+    int8_t* c8 = reinterpret_cast<int8_t*>(crow) + nb;
+    const bool word8 = !epi_is_fp(ep) && !s32 && ((uintptr_t)c8 & 3) == 0;
+    EpiRow row{};
+    EpiCol cols[4]{};
+    uint32_t oldw = 0u;
+    if (in && j == 0) {
+        row = epi_row(ep, m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            cols[e] = epi_col(ep, nb + e);
+        }
+        if (word8 && ep.add_to) {
+            oldw = *reinterpret_cast<const uint32_t*>(c8);
+        }
+    }
     v4i raw = v4i{0, 0, 0, 0};
     if (in) {
         int s = j;
@@ -1179,36 +1200,29 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     if (!in || j != 0) {
         return;
     }
-    const EpiParams& ep = p.ep;
-    const EpiRow row = epi_row(ep, m);
-    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
     if (epi_is_fp(ep)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            epi_store(ep, row, epi_col(ep, nb + e), raw[e], crow, nb + e);
+            epi_store(ep, row, cols[e], raw[e], crow, nb + e);
         }
         return;
     }
-    const bool s32 = ep.out_kind == NNOPS_OUT_S32;
-    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
     if (s32) {
         int32_t* c32 = reinterpret_cast<int32_t*>(crow) + nb;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            c32[e] = epi_value(ep, row, epi_col(ep, nb + e), raw[e], 0);
+            c32[e] = epi_value(ep, row, cols[e], raw[e], 0);
         }
         return;
     }
-    int8_t* c8 = reinterpret_cast<int8_t*>(crow) + nb;
-    if (((uintptr_t)c8 & 3) == 0) {
-        // one 4-byte read of the residual and one 4-byte store
-        const uint32_t oldw = ep.add_to ? *reinterpret_cast<const uint32_t*>(c8) : 0u;
+    if (word8) {
+        // one 4-byte read of the residual (above) and one 4-byte store
         uint32_t outw = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
             const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
-            outw |= ((uint32_t)epi_value(ep, row, epi_col(ep, nb + e), raw[e], old) & 0xffu) << (8 * e);
+            outw |= ((uint32_t)epi_value(ep, row, cols[e], raw[e], old) & 0xffu) << (8 * e);
         }
         *reinterpret_cast<uint32_t*>(c8) = outw;
         return;
@@ -1216,7 +1230,7 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int32_t old = ep.add_to ? (u8 ? (int32_t)((const uint8_t*)c8)[e] : (int32_t)c8[e]) : 0;
-        c8[e] = (int8_t)epi_value(ep, row, epi_col(ep, nb + e), raw[e], old);
+        c8[e] = (int8_t)epi_value(ep, row, cols[e], raw[e], old);
     }
 }
 
