@@ -69,9 +69,10 @@ public:
     Status compute(std::span<TensorView> outputs, std::span<const TensorView> inputs,
                    const ComputeContext& ctx = {}, void* workspace = nullptr) override;
     /// Query (empty outputs[0]: the packed descriptor is written back) or fill
-    /// the prepacked weight (src/ops/matmul.cpp:96-141). An s8 weight packs
-    /// into TensorLayout::PackedBHip; any other weight answers the query with
-    /// an empty view (no packed form).
+    /// the prepacked weight (src/ops/matmul.cpp:96-141). An s8 weight, and a
+    /// q4_1 weight with blocks along N (transpose_b false), pack into
+    /// TensorLayout::PackedBHip; any other weight answers the query with an
+    /// empty view (no packed form).
     void prepackWeights(std::span<const TensorView> inputs, std::span<TensorView> outputs,
                         const ComputeContext& ctx = {}) override;
     /// prepackWeights with its status (nnops asserts where this returns).
