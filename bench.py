@@ -519,7 +519,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(sharding is described in DESIGN.md, not implemented)"}))
+                                   "(multi-GPU sharding is designed, not implemented)"}))
         sys.exit(2)
     import torch
     sys.path.insert(0, os.path.join(ROOT, "tests"))
