@@ -148,9 +148,11 @@ int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int
  * matmul_helper.cpp:695-723, this is the gfx950 one). From B [K][ceil(N/32)]
  * blocks (trans_b = 0), row pitch ldb_bytes, it writes the same blocks as
  * two planes, structure of arrays:
- *   nibbles  [K][nbn * 16] bytes, block j of row k at k * nbn * 16 + 16 j;
+ *   nibbles  k-blocked: per group of 8 rows, per block, per nibble dword
+ *            d, the 8 rows' dwords: dword d of row k, block j at byte
+ *            ((k / 8) * nbn + j) * 128 + 32 d + 4 (k % 8) (rows past K zero);
  *   d|m      [K][dmp] u32 (f16 d low, f16 m high), dmp = nbn rounded up to
- *            4, at byte offset align_up(K * nbn * 16, 256);
+ *            4, at byte offset align_up(ceil(K / 8) * 8 * nbn * 16, 256);
  * nbn = ceil(N / 32). A call then passes b = out, ldb_bytes = nbn * 16,
  * b_soa = 1, b_dm = out + that offset, ldb_dm = dmp: the GEMV's and GEMM's
  * lane loads become contiguous 4- and 16-byte runs instead of 20-byte
@@ -181,7 +183,8 @@ typedef struct NnopsGemmQ41Args {
     int32_t trans_b, a_f16;
     int32_t out_kind;           /* NNOPS_OUT_F32 / NNOPS_OUT_F16 */
     /* b_soa = 1: B is the prepacked blocks-along-N form (trans_b = 0) of
-     * nnops_hip_prepack_q4_1: b = the nibble plane (row pitch ldb_bytes),
+     * nnops_hip_prepack_q4_1: b = the k-blocked nibble plane (ldb_bytes =
+     * nbn * 16, one group of 8 rows every 8 * ldb_bytes),
      * b_dm = the d|m plane (row pitch ldb_dm u32 elements). */
     int32_t b_soa;
     const uint32_t* b_dm;

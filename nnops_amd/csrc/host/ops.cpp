@@ -622,7 +622,7 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
         x.ldc = out.row_stride_elems();
         if (g.b_packed) {
             x.b_dm = reinterpret_cast<const uint32_t*>(
-                b.ptr<const char>() + align_up(static_cast<size_t>(g.k * x.ldb_bytes)));
+                b.ptr<const char>() + align_up(static_cast<size_t>((g.k + 7) / 8 * 8 * x.ldb_bytes)));
         } else {
             x.ldb_bytes = b.pitch();
         }

@@ -687,7 +687,8 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
     const int bl = blockIdx.x * 16 + (lane >> 2);
     const int jq = lane & 3;
     const int split = blockIdx.y;
-    const int kper = (p.k + p.splits - 1) / p.splits;
+    // SOA splits start on a group of 8 rows
+    const int kper = SOA ? ((p.k + p.splits - 1) / p.splits + 7) / 8 * 8 : (p.k + p.splits - 1) / p.splits;
     const int k0 = split * kper;
     const int k1 = min(p.k, k0 + kper);
     const bool live = bl < nblocks;
@@ -718,25 +719,64 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
             }
         }
     };
+    using AT = std::conditional_t<AF16, _Float16, float>;
+    if constexpr (SOA) {
+        // the k-blocked nibble plane: per group of 8 rows a lane's dword of
+        // its block is 32 contiguous bytes (two 16-byte loads); wave w takes
+        // groups w, w + 4, ..., U / 8 groups per batch, rows past k1 masked
+        constexpr int GB = U / 8;
+        const int bc = min(bl, nblocks - 1);
+        for (int g0 = k0 / 8 + wave; 8 * g0 < k1; g0 += 4 * GB) {
+            v4i xq[GB][2];
+            uint32_t dmw[GB][8];
+            AT ar[GB][8][MT];
+#pragma unroll
+            for (int gg = 0; gg < GB; ++gg) {
+                const int64_t grp = min(g0 + 4 * gg, (k1 - 1) / 8);
+                const v4i* xs = reinterpret_cast<const v4i*>(p.b + (grp * nblocks + bc) * 128 + jq * 32);
+                xq[gg][0] = xs[0];
+                xq[gg][1] = xs[1];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t r = 8 * grp + e < k1 ? 8 * grp + e : k1 - 1;
+                    dmw[gg][e] = p.bdm[r * p.ldbdm + bc];
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        ar[gg][e][m] = static_cast<const AT*>(p.a)[(int64_t)min(m, p.m - 1) * p.lda + r];
+                    }
+                }
+            }
+            // keep the scheduler from sinking the loads into the arithmetic
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int gg = 0; gg < GB; ++gg) {
+                const uint32_t xv[8] = {(uint32_t)xq[gg][0].x, (uint32_t)xq[gg][0].y, (uint32_t)xq[gg][0].z,
+                                        (uint32_t)xq[gg][0].w, (uint32_t)xq[gg][1].x, (uint32_t)xq[gg][1].y,
+                                        (uint32_t)xq[gg][1].z, (uint32_t)xq[gg][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int r = 8 * (g0 + 4 * gg) + e;
+                    float a[MT];
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        a[m] = (m < p.m && r < k1) ? (float)ar[gg][e][m] : 0.0f;
+                    }
+                    row(dmw[gg][e], xv[e], a);
+                }
+            }
+        }
+    } else {
     // whole batches of U rows, the ones past k1 masked (their A value is 0
     // and their address clamped), so a wave waits on memory once per batch
     for (int k = k0 + wave; k < k1; k += 4 * U) {
-        using AT = std::conditional_t<AF16, _Float16, float>;
         uint32_t dm[U], x[U];
         AT ar[U][MT];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kr = k + 4 * u;
-            if constexpr (SOA) {
-                // planes: a block's 16 nibble bytes and its d|m dword
-                const int64_t r = min(kr, k1 - 1);
-                dm[u] = p.bdm[r * p.ldbdm + min(bl, nblocks - 1)];
-                x[u] = *reinterpret_cast<const uint32_t*>(p.b + r * p.ldb + min(bl, nblocks - 1) * 16 + 4 * jq);
-            } else {
-                const uint8_t* src = col + (int64_t)min(kr, k1 - 1) * p.ldb;
-                dm[u] = *reinterpret_cast<const uint32_t*>(src);
-                x[u] = *reinterpret_cast<const uint32_t*>(src + 4 + 4 * jq);
-            }
+            const uint8_t* src = col + (int64_t)min(kr, k1 - 1) * p.ldb;
+            dm[u] = *reinterpret_cast<const uint32_t*>(src);
+            x[u] = *reinterpret_cast<const uint32_t*>(src + 4 + 4 * jq);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 // unconditional load (clamped row and column), masked below:
@@ -759,6 +799,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
         for (int u = 0; u < U; ++u) {
             row(dm[u], x[u], a[u]);
         }
+    }
     }
     if (wave > 0) {
 #pragma unroll
@@ -1294,8 +1335,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     // slot-row pitch of the d|m dwords and of the nibble dwords, and where the
     // d|m rows start within the stage's B
     constexpr int kRowD = SOA ? BN / 32 * 4 : kRow, kRowQ = SOA ? BN / 32 * 16 : kRow;
-    constexpr int kDmAt = SOA ? 64 * kRowQ : 0;
-    constexpr int kA = BM * 128, kB = 64 * kRow, kStage = kA + kB;
+    // SOA nibbles: one 1 KiB piece per group of 8 rows (the tile's 8 blocks x
+    // 128 bytes), pieces 1040 bytes apart so that the two lane halves' groups
+    // (2 ks and 2 ks + 1) sit 4 banks apart; the d|m rows follow
+    constexpr int kGrp = 1040;
+    constexpr int kDmAt = SOA ? 8 * kGrp : 0;
+    constexpr int kA = BM * 128, kB = SOA ? kDmAt + 64 * kRowD : 64 * kRow, kStage = kA + kB;
     constexpr int kBPieces = kB / 1024;             // 10 x 1 KiB: waves 0, 1 issue two
     static_assert(NS >= 3 && kBPieces > W && kBPieces <= 2 * W, "stages");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
@@ -1316,8 +1361,9 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
     // this tile's blocks of row 0; a stage's rows start s * 64 * ldb further
     const int nbn = (p.n + 31) / 32;
-    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * (SOA ? 16 : 20);
-    const int64_t b_end = (int64_t)(p.k - 1) * p.ldb + (int64_t)(nbn - n0 / 32) * (SOA ? 16 : 20);
+    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * (SOA ? 128 : 20);
+    const int64_t b_end = SOA ? (int64_t)(p.k / 8 - 1) * 8 * p.ldb + (int64_t)(nbn - n0 / 32) * 128
+                              : (int64_t)(p.k - 1) * p.ldb + (int64_t)(nbn - n0 / 32) * 20;
     const int64_t ldd = p.ldbdm * 4;                // SOA: d|m row pitch in bytes
     const uint8_t* d0 = reinterpret_cast<const uint8_t*>(p.bdm) + (int64_t)(n0 / 32) * 4;
     const int64_t d_end = (int64_t)(p.k - 1) * ldd + (int64_t)(nbn - n0 / 32) * 4;
@@ -1332,12 +1378,16 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     for (int i = 0; i < 2; ++i) {
         const int q = (wave + W * i) * 64 + lane;     // chunk = LDS slot
         if constexpr (SOA) {
-            // nibble pieces: 8 chunks per row; d|m pieces: 2 chunks per row
-            const int qq = i == 0 ? q : q - W * 64;
-            const int cpr = i == 0 ? 8 : 2;
-            const int pr = qq / cpr, c = qq - pr * cpr;
-            const int k = pr ^ ((pr >> 3) & 1);
-            b_off[i] = k * (int)(i == 0 ? p.ldb : ldd) + c * 16;
+            // nibble piece: the wave's group of 8 rows, 1 KiB contiguous;
+            // d|m pieces: 2 chunks per row, slot-row order
+            if (i == 0) {
+                b_off[i] = wave * 8 * (int)p.ldb + lane * 16;
+            } else {
+                const int qq = q - W * 64;
+                const int pr = qq / 2, c = qq - pr * 2;
+                const int k = pr ^ ((pr >> 3) & 1);
+                b_off[i] = k * (int)ldd + c * 16;
+            }
         } else {
             const int pr = q / 10, c = q - pr * 10;
             const int k = pr ^ ((pr >> 3) & 1);
@@ -1352,13 +1402,13 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
         }
         const int64_t row0 = (int64_t)s * 64 * p.ldb;
         const QBufRsrc rsb = q_buffer_rsrc(b0 + row0, (uint32_t)std::min<int64_t>(b_end - row0, 0x7fffffff));
-        q_buffer_load_lds16(rsb, base + kA + wave * 1024, b_off[0], 0);
+        q_buffer_load_lds16(rsb, base + kA + wave * (SOA ? kGrp : 1024), b_off[0], 0);
         if (two) {
             if constexpr (SOA) {
                 const int64_t drow0 = (int64_t)s * 64 * ldd;
                 const QBufRsrc rsd =
                     q_buffer_rsrc(d0 + drow0, (uint32_t)std::min<int64_t>(d_end - drow0, 0x7fffffff));
-                q_buffer_load_lds16(rsd, base + kA + (wave + W) * 1024, b_off[1], 0);
+                q_buffer_load_lds16(rsd, base + kA + kDmAt + wave * 1024, b_off[1], 0);
             } else {
                 q_buffer_load_lds16(rsb, base + kA + (wave + W) * 1024, b_off[1], 0);
             }
@@ -1390,6 +1440,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     // and 16 ks + e + 1 + 7 kh: a lane base per row of the pair, the rest are
     // immediate offsets
     const int sr0 = 9 * kh, sr1 = 7 * kh + 1;
+    const int bxs = kA + kh * kGrp + 128 * wave + 32 * ((fr & 15) >> 2);   // SOA nibbles
     const int bd0 = kA + sr0 * kRowD + bcol, bq0 = kA + sr0 * kRowQ + qdw;
     const int bd1 = kA + sr1 * kRowD + bcol, bq1 = kA + sr1 * kRowQ + qdw;
     // Low-nibble lanes keep 0x0f under exponent byte 0x64: f16 1024 + q.
@@ -1411,8 +1462,17 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
             const int od = (16 * ks + 2 * e) * kRowD, oq = (16 * ks + 2 * e) * kRowQ;
             r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + od);
             r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + od);
-            r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + oq);
-            r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + oq);
+            if constexpr (!SOA) {
+                r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + oq);
+                r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + oq);
+            }
+        }
+        if constexpr (SOA) {
+            // the lane's dword of its block for the 8 rows of group 2 ks + kh
+            const v4i* xs = reinterpret_cast<const v4i*>(st + bxs + 2 * ks * kGrp);
+            const v4i lo = xs[0], hi = xs[1];
+            r.x0[0] = (uint32_t)lo.x, r.x1[0] = (uint32_t)lo.y, r.x0[1] = (uint32_t)lo.z, r.x1[1] = (uint32_t)lo.w;
+            r.x0[2] = (uint32_t)hi.x, r.x1[2] = (uint32_t)hi.y, r.x0[3] = (uint32_t)hi.z, r.x1[3] = (uint32_t)hi.w;
         }
     };
     auto b_decode = [&](const BRaw& r) {
@@ -1509,8 +1569,9 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 
 // ---------------------------------------------------------------------------
 // Prepack of a blocks-along-N weight into its two planes (structure of
-// arrays): thread per block, the 16 nibble bytes as one 16-byte store, the
-// d|m dword into its plane; the plane's row padding is zeroed.
+// arrays): thread per block; the nibble plane is k-blocked (per 8 rows, per
+// block, per nibble dword: the 8 rows' dwords, 32 bytes), the d|m dword goes
+// into its plane; padding is zeroed.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t ldb, int k, int nbn,
                                                        uint8_t* nib, uint32_t* dm, int64_t dmp)
@@ -1522,8 +1583,22 @@ __global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t
     const int64_t r = idx / nbn;
     const int j = (int)(idx - r * nbn);
     const uint32_t* src = reinterpret_cast<const uint32_t*>(b + r * ldb + (int64_t)j * 20);
-    const v4i q{(int)src[1], (int)src[2], (int)src[3], (int)src[4]};
-    *reinterpret_cast<v4i*>(nib + idx * 16) = q;
+    // nibble dword d of row r at ((r / 8) * nbn + j) * 128 + 32 d + 4 (r % 8):
+    // a block's 8 consecutive rows of one dword are 32 contiguous bytes
+    uint32_t* g = reinterpret_cast<uint32_t*>(nib + (((r >> 3) * nbn + j) * 128));
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        g[8 * d + (r & 7)] = src[1 + d];
+    }
+    if (r == k - 1) {
+        // the last group's rows past K
+        for (int rr = (int)(r & 7) + 1; rr < 8; ++rr) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                g[8 * d + rr] = 0u;
+            }
+        }
+    }
     dm[r * dmp + j] = src[0];
     if (j == nbn - 1) {
         for (int64_t t = nbn; t < dmp; ++t) {
@@ -1741,7 +1816,8 @@ extern "C" size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n)
     if (k <= 0 || n <= 0) {
         return 0;
     }
-    return align_up((size_t)k * (size_t)((n + 31) / 32) * 16) + (size_t)k * (size_t)prepack_q41_dmp(n) * 4;
+    return align_up((size_t)((k + 7) / 8 * 8) * (size_t)((n + 31) / 32) * 16) +
+           (size_t)k * (size_t)prepack_q41_dmp(n) * 4;
 }
 
 extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b,
@@ -1758,7 +1834,7 @@ extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, in
         return NNOPS_INVALID_ARGUMENT;
     }
     uint8_t* nib = static_cast<uint8_t*>(out);
-    uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)k * (size_t)nbn * 16));
+    uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)((k + 7) / 8 * 8) * (size_t)nbn * 16));
     const int64_t blocks = k * nbn;
     hipLaunchKernelGGL(prepack_q4_1_kn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), b, ldb_bytes, (int)k, (int)nbn, nib, dm,

@@ -4,7 +4,9 @@ MFMA, ring GEMM, split K), for [K,N] and [N,K] raw forms, with the precomputed
 column sums standing in for the per-call pass (u8 A, A zero points), and
 through the fp-activation and dequantizing routes; and the packed q4_1
 weight with blocks along N (two planes) gives bit-for-bit the raw weight's
-result on the GEMV and ring routes, within the Q4_1 tolerance elsewhere."""
+result on the ring route, the same up to f32 summation order on the GEMV
+(which walks the planes in groups of 8 rows), within the Q4_1 tolerance
+elsewhere."""
 from __future__ import annotations
 
 import numpy as np
@@ -116,13 +118,18 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     at = na.tensor(dev(a))
     got_p = run(op, at, packed, torch.float32, (M, N))
     got_r = run(op, at, wt, torch.float32, (M, N))
-    np.testing.assert_array_equal(got_p, got_r)
+    if M > 2 and a_f16:
+        np.testing.assert_array_equal(got_p, got_r)    # the ring: same decode, same order
+    else:
+        # the GEMV walks the planes in groups of 8 rows: another f32 summation order
+        np.testing.assert_allclose(got_p, got_r, rtol=0, atol=1e-5 * float(np.max(np.abs(got_r))))
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
     err = float(np.max(np.abs(got_p - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
     assert err <= 2e-3, err
 
 
-@pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200)])
+@pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200), (3, 37, 72),
+                                   (1, 97, 40)])
 def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
     """Ragged shapes. K % 64 != 0 with M > 2: the packed weight takes the GEMV
     loop (two rows of A per pass). N = 200 (7 blocks per row, d|m rows padded
@@ -156,7 +163,10 @@ def test_matmul_q4_1_prepacked_config4_kn():
         at = na.tensor(dev(a))
         got_p = run(op, at, packed, torch.float32, (M, N))
         got_r = run(op, at, wt, torch.float32, (M, N))
-        np.testing.assert_array_equal(got_p, got_r)
+        if M > 2:
+            np.testing.assert_array_equal(got_p, got_r)
+        else:
+            np.testing.assert_allclose(got_p, got_r, rtol=0, atol=1e-5 * float(np.max(np.abs(got_r))))
         want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
         g, w = got_p[rows[0]:rows[1]], want[rows[0]:rows[1]]
         err = float(np.max(np.abs(g - w)) / max(np.max(np.abs(w)), np.sqrt(np.mean(w ** 2))))
@@ -179,7 +189,10 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
     at = na.tensor(dev(a))
     got_p = run(op, at, packed, torch.float16, (2, M, N))
     got_r = run(op, at, wt, torch.float16, (2, M, N))
-    np.testing.assert_array_equal(got_p.view(np.uint16), got_r.view(np.uint16))
+    if M > 2:
+        np.testing.assert_array_equal(got_p.view(np.uint16), got_r.view(np.uint16))
+    else:
+        np.testing.assert_allclose(got_p.astype(np.float32), got_r.astype(np.float32), rtol=2e-3, atol=1e-3)
     for bi in range(2):
         want = oracle.gemm_q4_1(a[bi], blk, N, trans_b=False, w_round_f16=True, c_f16=True).astype(np.float32)
         g = got_p[bi].astype(np.float32)
@@ -187,11 +200,13 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
         assert err <= 2e-3, err
 
 
-@pytest.mark.parametrize("K,N", [(64, 200), (96, 1024)])
+@pytest.mark.parametrize("K,N", [(64, 200), (96, 1024), (37, 72)])
 def test_q4_1_packed_blob_layout(K, N):
-    """The packed q4_1 blob byte for byte: nibble plane [K][nbn*16], then at
-    align_up(K*nbn*16, 256) the d|m plane [K][nbn rounded up to 4] (padding
-    zeroed), restated here with numpy from the raw [K][nbn] 20-byte blocks."""
+    """The packed q4_1 blob byte for byte: the k-blocked nibble plane (per 8
+    rows, per block, per nibble dword the 8 rows' dwords; rows past K zero),
+    then at align_up(ceil(K/8)*8*nbn*16, 256) the d|m plane [K][nbn rounded
+    up to 4] (padding zeroed), restated here with numpy from the raw [K][nbn]
+    20-byte blocks."""
     announce(f"prepack q4_1 blob layout {K}x{N}")
     blk = dg.q4_1_blocks(K * 7 + N, K, N)                # uint8 [K, nbn*20]
     nbn = (N + 31) // 32
@@ -201,11 +216,14 @@ def test_q4_1_packed_blob_layout(K, N):
     torch.cuda.synchronize()
     got = host(buf)
     b3 = blk.reshape(K, nbn, 20)
-    nib = b3[:, :, 4:].reshape(-1)
+    kg = (K + 7) // 8
+    q32 = np.zeros((kg * 8, nbn, 4), np.uint32)
+    q32[:K] = np.ascontiguousarray(b3[:, :, 4:]).view(np.uint32).reshape(K, nbn, 4)
+    nib = q32.reshape(kg, 8, nbn, 4).transpose(0, 2, 3, 1).reshape(-1).view(np.uint8)
     dmp = (nbn + 3) // 4 * 4
     dm = np.zeros((K, dmp, 4), np.uint8)
     dm[:, :nbn, :] = b3[:, :, :4]
-    off = (K * nbn * 16 + 255) // 256 * 256
+    off = (kg * 8 * nbn * 16 + 255) // 256 * 256
     assert na.lib().nnops_hip_prepack_q4_1_bytes(K, N) == off + K * dmp * 4
     np.testing.assert_array_equal(got[:nib.size], nib)
     np.testing.assert_array_equal(got[off:off + dm.size], dm.reshape(-1))
