@@ -41,18 +41,23 @@ def parse():
                                                            "vendor"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline of the headline config")
+    p.add_argument("--cpu-seconds-each", type=float, default=2.0, help="CPU baseline of each secondary line")
     return p.parse_args()
 
 
 class Timer:
-    """Times K steps with HIP events on the stream the kernels run on.
+    """Times K steps with HIP events on the stream the kernels run on, two ways:
 
-    The K steps are captured once into a HIP graph and the graph is replayed
-    for the timed region, so the figure is the device's throughput on the
-    path, not the Python/ctypes launch cost of this harness (a C++ caller
-    launches in microseconds). The eager per-step time (events around each
-    call, host launch included) is reported beside it.
+    - eager: the K calls issued back to back, one event pair around all of
+      them (the device queue stays ahead as long as a call's host cost is
+      below its kernel time);
+    - graph: the K calls captured once into a HIP graph and replayed, which
+      removes the Python/ctypes launch cost of this harness for the short
+      kernels (a C++ caller launches in microseconds).
+
+    The step time is the faster of the two; both are reported. Per-call events
+    (eager, host launch included) are kept as the call-to-call spread.
     """
 
     def __init__(self, stream):
@@ -60,24 +65,30 @@ class Timer:
         self.torch = torch
         self.stream = stream
 
+    def _span(self, body):
+        torch = self.torch
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        body()
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
     def time(self, fn, steps, warmup):
         torch = self.torch
         with torch.cuda.stream(self.stream):
             for _ in range(warmup):
                 fn()
         torch.cuda.synchronize()
-        # eager: events around every call
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        with torch.cuda.stream(self.stream):
-            for i in range(steps):
-                starts[i].record(self.stream)
-                fn()
-                ends[i].record(self.stream)
-        torch.cuda.synchronize()
-        eager = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-        out = {"eager_mean_ms": sum(eager) / len(eager), "eager_median_ms": eager[len(eager) // 2]}
-        # graph of K steps, replayed (one warm replay first)
+
+        def eager_all():
+            with torch.cuda.stream(self.stream):
+                for _ in range(steps):
+                    fn()
+        t0 = time.perf_counter()
+        out = {"eager_ms": self._span(eager_all) / steps}
+        out["wall_s"] = time.perf_counter() - t0
         try:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=self.stream):
@@ -85,21 +96,52 @@ class Timer:
                     fn()
             g.replay()
             torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
+
+            def replay():
+                with torch.cuda.stream(self.stream):
+                    g.replay()
             t0 = time.perf_counter()
-            e0.record(self.stream)
-            with torch.cuda.stream(self.stream):
-                g.replay()
-            e1.record(self.stream)
-            torch.cuda.synchronize()
-            out["wall_s"] = time.perf_counter() - t0
-            out["mean_ms"] = e0.elapsed_time(e1) / steps
-            out["timing"] = "hip-graph of K steps"
-        except Exception as exc:  # capture unsupported: fall back to eager
-            out["mean_ms"] = out["eager_mean_ms"]
-            out["timing"] = f"eager (graph capture failed: {type(exc).__name__})"
+            out["graph_ms"] = self._span(replay) / steps
+            out["wall_s"] += time.perf_counter() - t0
+        except Exception as exc:  # capture unsupported: eager only
+            out["graph_error"] = type(exc).__name__
+        if out.get("graph_ms", float("inf")) < out["eager_ms"]:
+            out["mean_ms"], out["timing"] = out["graph_ms"], "hip-graph of K steps (faster than eager)"
+        else:
+            out["mean_ms"], out["timing"] = out["eager_ms"], "K eager steps back to back (faster than the graph)"
+        out["eager_mean_ms"] = out["eager_ms"]
         return out
+
+
+_MEMO = {}
+
+
+def memo(key, make):
+    """Host operands shared by several bench lines (generated once)."""
+    if key not in _MEMO:
+        _MEMO[key] = make()
+    return _MEMO[key]
+
+
+def cpu_time(fn, seconds):
+    """Repeat fn until `seconds` have passed (at least once); seconds per call."""
+    reps = 0
+    t0 = time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < seconds:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_cores():
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def nnops_cpu():
+    """nnops' own CPU MatMul (compiled from the reference sources into
+    oracle/_ref/libnnops_cpu.so), or None where this host cannot load it."""
+    import oracle
+    return oracle.cpu_lib()
 
 
 def make_cfg2(torch, dg, na, M=4096, N=4096, K=4096):
@@ -145,14 +187,19 @@ def run_cfg2(args, torch, dg, na, stream):
 
 
 def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbuf=8, trans_b=False,
-                 prepacked=False):
+                 prepacked=False, out_s8=False, cpu_seconds=0.0):
     """Config 3: int8 GEMV with `nbuf` rotated weight buffers (> MALL).
     `prepacked`: each weight goes through prepackWeights first (outside the
-    timed region, once at load time), and the call reads the packed form."""
+    timed region, once at load time), and the call reads the packed form.
+    `out_s8`: the requantizing variant (per-channel scales as config 2).
+    `cpu_seconds` > 0: nnops' own CPU MatMul on the same problem beside it."""
     import numpy as np
-    a = torch.from_numpy(dg.ints(301, (M, K), -127, 127)).cuda()
+    a_h = dg.ints(301, (M, K), -127, 127)
+    w_h = memo(("w", trans_b, K, N), lambda: dg.ints(302, (N, K) if trans_b else (K, N), -127, 127))
+    sb_h = dg.uniform(303, (N,), 0.001, 0.01)
+    a = torch.from_numpy(a_h).cuda()
     ws_list = []
-    base = torch.from_numpy(dg.ints(302, (N, K) if trans_b else (K, N), -127, 127)).cuda()
+    base = torch.from_numpy(w_h).cuda()
     for i in range(nbuf):
         ws_list.append(base if i == 0 else torch.roll(base, shifts=i, dims=1).contiguous())
     if prepacked:
@@ -166,32 +213,92 @@ def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbu
             packed.append(blob[:N * kp].view(torch.int8).view(N, kp))
         stream.synchronize()
         ws_list = packed
-        trans_b = True
-    c = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    kern_tb = trans_b or prepacked
+    c = torch.zeros((M, N), dtype=torch.int8 if out_s8 else torch.int32, device="cuda")
+    sb = torch.from_numpy(sb_h).cuda()
     s = stream.cuda_stream
     probe = na.GemmI8Args()
-    probe.m, probe.n, probe.k, probe.trans_b = M, N, K, int(trans_b)
+    probe.m, probe.n, probe.k, probe.trans_b = M, N, K, int(kern_tb)
+    probe.out_kind = na.OUT_S8 if out_s8 else na.OUT_S32
     need = na.lib().nnops_hip_gemm_i8_workspace_size(C.byref(probe))
     wsp = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     it = [0]
+    kw = dict(out_kind=na.OUT_S8, s_a=0.02, s_b=sb, s_out=0.05) if out_s8 else {}
 
     def step():
         b = ws_list[it[0] % nbuf]
         it[0] += 1
-        na.gemm_i8(a, b, c, trans_b=trans_b, workspace=wsp, stream=s)
+        na.gemm_i8(a, b, c, trans_b=kern_tb, workspace=wsp, stream=s, **kw)
 
     t = Timer(stream).time(step, steps, warmup)
-    nbytes = K * N + K * M + N * M * 4
+    nbytes = K * N + K * M + N * M * (1 if out_s8 else 4) + (4 * N if out_s8 else 0)
     gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
-    return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3,
-            "bytes": nbytes, "M": M, "K": K, "N": N,
-            "weight_layout": "prepacked [K,N] -> [N][kp]" if prepacked else ("[N,K]" if trans_b else "[K,N]"),
-            "rotated_weight_bytes": nbuf * K * N}
+    out = {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3,
+           "bytes": nbytes, "M": M, "K": K, "N": N, "out": "s8 (requant)" if out_s8 else "s32",
+           "weight_layout": "prepacked [K,N] -> [N][kp]" if prepacked else ("[N,K]" if trans_b else "[K,N]"),
+           "rotated_weight_bytes": nbuf * K * N, "timing": t["timing"]}
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_i8(a_h, w_h, trans_b, out_s8, sb_h, nbytes, cpu_seconds, "GB/s",
+                                     f"config 3 M={M} ({'s8' if out_s8 else 's32'} out, weight "
+                                     f"{'[N,K]' if trans_b else '[K,N]'})")
+    return out
 
 
-def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=8, trans_b=True):
-    a = torch.from_numpy(dg.normal(401, (M, K)).astype("float16")).cuda()
-    base = torch.from_numpy(dg.q4_1_blocks(402, N, K) if trans_b else dg.q4_1_blocks(402, K, N)).cuda()
+def cpu_i8(a, w, trans_b, out_s8, sb, nbytes, seconds, unit, what):
+    """nnops' CPU MatMul on one int8 problem, timed in full; `unit` GB/s (the
+    GPU line's algorithmic bytes per second) or TOPS."""
+    import numpy as np
+    cpu = nnops_cpu()
+    if cpu is None:
+        return {"value": None, "unit": unit, "cores": 0, "kind": "reference",
+                "sample": "n/a: oracle/_ref/libnnops_cpu.so not loadable on this host (no AVX-512 VNNI)"}
+    M, K = a.shape
+    N = w.shape[0] if trans_b else w.shape[1]
+    c = np.zeros((M, N), np.int8 if out_s8 else np.int32)
+    cores = cpu_cores()
+
+    def call():
+        rc = cpu.ref_cpu_matmul_i8(a.ctypes.data, w.ctypes.data, None, c.ctypes.data, M, N, K, int(trans_b),
+                                   int(out_s8), 0.02, sb.ctypes.data if out_s8 else None, 0.05, 0, 0, cores)
+        if rc != 0:
+            raise RuntimeError(f"nnops CPU MatMul failed: status {rc}")
+    sec, reps = cpu_time(call, seconds)
+    v = nbytes / sec / 1e9 if unit == "GB/s" else 2.0 * M * N * K / sec / 1e12
+    return {"value": v, "unit": unit, "cores": cores, "kind": "reference", "us": sec * 1e6,
+            "sample": f"{what} in full, {reps} calls; nnops' CPU MatMul (src/backend/cpu/matmul, AVX-512-VNNI) "
+                      f"compiled from source, {cores} threads"}
+
+
+def cpu_q4_1(a, blk, N, trans_b, nbytes, seconds, what):
+    """nnops' CPU fp x q4_1 MatMul (f16 A -> f16 C: its output dtype follows A,
+    src/ops/matmul.cpp:49-58; matmul_qblock_fused at small M) on one problem."""
+    import numpy as np
+    cpu = nnops_cpu()
+    unit = "GB/s" if a.shape[0] <= 16 else "TFLOPS"
+    if cpu is None:
+        return {"value": None, "unit": unit, "cores": 0, "kind": "reference",
+                "sample": "n/a: oracle/_ref/libnnops_cpu.so not loadable on this host (no AVX-512 VNNI)"}
+    M, K = a.shape
+    c = np.zeros((M, N), np.float16)
+    cores = cpu_cores()
+
+    def call():
+        rc = cpu.ref_cpu_matmul_q4_1(a.ctypes.data, blk.ctypes.data, c.ctypes.data, M, N, K, int(trans_b), cores)
+        if rc != 0:
+            raise RuntimeError(f"nnops CPU q4_1 MatMul failed: status {rc}")
+    sec, reps = cpu_time(call, seconds)
+    v = nbytes / sec / 1e9 if unit == "GB/s" else 2.0 * M * N * K / sec / 1e12
+    return {"value": v, "unit": unit, "cores": cores, "kind": "reference", "us": sec * 1e6,
+            "sample": f"{what} in full, {reps} calls; nnops' CPU fp x q4_1 MatMul with f16 output (its route for "
+                      f"an f16 A) compiled from source, {cores} threads"}
+
+
+def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=8, trans_b=True,
+                  cpu_seconds=0.0):
+    a_h = dg.normal(401, (M, K)).astype("float16")
+    b_h = dg.q4_1_blocks(402, N, K) if trans_b else dg.q4_1_blocks(402, K, N)
+    a = torch.from_numpy(a_h).cuda()
+    base = torch.from_numpy(b_h).cuda()
     bufs = [base if i == 0 else torch.roll(base, shifts=20 * i, dims=1).contiguous() for i in range(nbuf)]
     c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     s = stream.cuda_stream
@@ -210,23 +317,34 @@ def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nb
     t = Timer(stream).time(step, steps, warmup)
     nbytes = N * (K // 32) * 20 + K * M * 2 + N * M * 4
     gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
-    return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
-            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
-            "rotated_weight_bytes": nbuf * N * (K // 32) * 20}
+    out = {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
+           "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
+           "rotated_weight_bytes": nbuf * N * (K // 32) * 20, "timing": t["timing"]}
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, N * (K // 32) * 20 + K * M * 2 + N * M * 2,
+                                       cpu_seconds, f"config 4 M={M} (weight {out['weight_layout']})")
+    return out
 
 
-def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, trans_b=True):
+def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, trans_b=True, cpu_seconds=0.0):
     """Config 4's GEMM; trans_b=False times the literal [K][N/32] layout
     (blocks along N) instead of the GGUF/Linear [N][K/32] one."""
-    a = torch.from_numpy(dg.normal(403, (M, K)).astype("float16")).cuda()
-    b = torch.from_numpy(dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)).cuda()
+    a_h = dg.normal(403, (M, K)).astype("float16")
+    b_h = dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)
+    a = torch.from_numpy(a_h).cuda()
+    b = torch.from_numpy(b_h).cuda()
     c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
     s = stream.cuda_stream
     t = Timer(stream).time(lambda: na.gemm_q4_1(a, b, c, n=N, trans_b=trans_b, stream=s), steps, warmup)
     fl = 2.0 * M * N * K
     tf = fl / (t["mean_ms"] * 1e-3) / 1e12
-    return {"tflops": tf, "frac_f16_mfma": tf / PEAK_F16_TFLOPS, "us": t["mean_ms"] * 1e3,
-            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]"}
+    out = {"tflops": tf, "frac_f16_mfma": tf / PEAK_F16_TFLOPS, "us": t["mean_ms"] * 1e3,
+           "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
+           "timing": t["timing"]}
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, 0, cpu_seconds,
+                                       f"config 4 M={M} (weight {out['weight_layout']})")
+    return out
 
 
 def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8):
@@ -264,6 +382,29 @@ def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nb
     else:
         out["tflops"] = 2.0 * M * N * K / (t["mean_ms"] * 1e-3) / 1e12
         out["frac_f16_mfma"] = out["tflops"] / PEAK_F16_TFLOPS
+    return out
+
+
+def cfg1_case(torch, dg, na, stream, steps, warmup, cpu_seconds=0.0):
+    """Config 1: s8 x s8 -> s32, A [128,1024], B [1024,1024] ([K,N], the
+    MatMul form), no bias, no epilogue, dense; launch/latency bound."""
+    M, K, N = 128, 1024, 1024
+    a_h = dg.ints(101, (M, K), -127, 127)
+    b_h = dg.ints(102, (K, N), -127, 127)
+    a, b = torch.from_numpy(a_h).cuda(), torch.from_numpy(b_h).cuda()
+    c = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    s = stream.cuda_stream
+    probe = na.GemmI8Args()
+    probe.m, probe.n, probe.k = M, N, K
+    wsp = torch.empty(max(na.lib().nnops_hip_gemm_i8_workspace_size(C.byref(probe)), 1), dtype=torch.uint8,
+                      device="cuda")
+    t = Timer(stream).time(lambda: na.gemm_i8(a, b, c, workspace=wsp, stream=s), steps, warmup)
+    ops = 2.0 * M * N * K
+    out = {"tops": ops / (t["mean_ms"] * 1e-3) / 1e12, "us": t["mean_ms"] * 1e3, "M": M, "K": K, "N": N,
+           "weight_layout": "[K,N]", "out": "s32", "timing": t["timing"]}
+    out["frac_int8_mfma"] = out["tops"] / PEAK_INT8_TOPS
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_i8(a_h, b_h, False, False, None, 0, cpu_seconds, "TOPS", "config 1")
     return out
 
 
@@ -325,7 +466,11 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
     ops = 2.0 * M * N * K
     tops = ops / (t["mean_ms"] * 1e-3) / 1e12
     return {"tops": tops, "frac_int8_mfma": tops / PEAK_INT8_TOPS, "us": t["mean_ms"] * 1e3,
-            "M": M, "K": K, "N": N, "a_pitch": 14400, "c_pitch": 4160, "weight_layout": "[N,K]"}
+            "M": M, "K": K, "N": N, "a_pitch": 14400, "c_pitch": 4160, "weight_layout": "[N,K]",
+            "timing": t["timing"],
+            "cpu_baseline": {"value": None, "unit": "TOPS", "cores": 0, "kind": "reference",
+                             "sample": "n/a: nnops has no route for an s8 add_to destination "
+                                       "(src/backend/cpu/matmul/linear.cpp:226) nor a GELU on an integer one"}}
 
 
 def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False):
@@ -392,7 +537,8 @@ def ceilings(torch, na, stream):
     and 180 MiB rotated over 8 buffers (the cfg3/cfg4 GEMV sizes; the fixed
     per-launch cost is the difference of the two), and an empty launch, each
     timed as a HIP graph of back-to-back launches like the workloads."""
-    lib = na.lib()
+    from nnops_amd import _lib as L
+    lib = L.diag_lib()
     s = stream.cuda_stream
     out = torch.zeros(2048 * 256, dtype=torch.int32, device="cuda")
     src = torch.randint(-2 ** 31, 2 ** 31 - 1, (2048 * 256 * 24,), dtype=torch.int32, device="cuda")
@@ -548,11 +694,11 @@ def main():
     if args.workload == "ceilings":
         print(json.dumps({"workload": "ceilings", **ceilings(torch, na, stream)}))
         return
+    cs = 0.0 if args.no_cpu_baseline else args.cpu_seconds_each
     if args.workload != "cfg2":
-        res = {"cfg1": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=128, K=1024, N=1024,
-                                            nbuf=1),
-               "cfg3": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup),
-               "cfg4": lambda: gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup),
+        res = {"cfg1": lambda: cfg1_case(torch, dg, na, stream, args.steps, args.warmup, cs),
+               "cfg3": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, cpu_seconds=cs),
+               "cfg4": lambda: gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup, cpu_seconds=cs),
                "cfg5": lambda: cfg5_case(torch, dg, na, stream, args.steps, args.warmup)}[args.workload]()
         print(json.dumps({"workload": args.workload, **res}))
         return
@@ -560,37 +706,30 @@ def main():
     main_res = run_cfg2(args, torch, dg, na, stream)
     secondary = {}
     if not args.no_secondary:
-        secondary["cfg3_int8_gemv_m1_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, trans_b=True)
-        secondary["cfg3_int8_gemv_m1_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, trans_b=False)
-        secondary["cfg3_int8_gemv_m4_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=4,
-                                                         trans_b=True)
-        secondary["cfg3_int8_gemv_m16_nk"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
-                                                          trans_b=True)
-        secondary["cfg3_int8_gemv_m16_kn"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, M=16,
-                                                          trans_b=False)
-        secondary["cfg3_int8_gemv_m1_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup,
-                                                                   prepacked=True)
-        secondary["cfg3_int8_gemv_m16_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, args.steps,
-                                                                    args.warmup, M=16, prepacked=True)
-        secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup)
-        secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
-                                                         args.warmup)
-        secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, max(5, args.steps // 5),
-                                                        args.warmup, dq_only=True)
-        secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, max(5, args.steps // 5),
-                                                          args.warmup)
-        secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup)
-        secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, args.steps, args.warmup,
-                                                                dequant=True)
-        secondary["cfg4_q4_1_gemv_m1_kn"] = gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup,
-                                                          trans_b=False)
-        secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, max(5, args.steps // 5),
-                                                            args.warmup, trans_b=False)
-        secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, args.steps,
-                                                                      args.warmup, M=1)
-        secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream,
-                                                                        max(5, args.steps // 5), args.warmup, M=512)
-        secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, max(5, args.steps // 5), args.warmup)
+        st, wu = args.steps, args.warmup
+        few = max(5, st // 5)
+        secondary["cfg1_s32_128x1024x1024"] = cfg1_case(torch, dg, na, stream, st, wu, cs)
+        for M in (1, 4, 16):
+            for s8 in (False, True):
+                secondary[f"cfg3_int8_gemv_m{M}_kn_{'s8' if s8 else 's32'}"] = gemv_i8_case(
+                    torch, dg, na, stream, st, wu, M=M, trans_b=False, out_s8=s8, cpu_seconds=cs)
+            secondary[f"cfg3_int8_gemv_m{M}_nk_s32"] = gemv_i8_case(torch, dg, na, stream, st, wu, M=M, trans_b=True)
+        for M in (1, 16):
+            secondary[f"cfg3_int8_gemv_m{M}_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, st, wu, M=M,
+                                                                         prepacked=True)
+        secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, st, wu, cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, few, wu, cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemv_m1_kn"] = gemv_q41_case(torch, dg, na, stream, st, wu, trans_b=False,
+                                                          cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, few, wu, trans_b=False,
+                                                            cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
+        secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
+        secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, few, wu)
+        secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, few, wu, dq_only=True)
+        secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, few, wu)
+        secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu)
+        secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu, dequant=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC, "value": main_res["value"], "unit": main_res["unit"], "n_gpus": 1,
@@ -599,6 +738,7 @@ def main():
         "dtype": main_res["dtype"], "data": "synthetic (seeded xorshift128+, BASELINE config 2 distributions)",
         "config": main_res["config"], "roofline": main_res["roofline"], "cpu_baseline": cpu,
         "timing": main_res["timing"], "eager_ms_per_step": main_res["eager_ms_per_step"],
+        "graph_ms_per_step": main_res["t"].get("graph_ms"),
         "secondary": secondary,
     }
     print(json.dumps(line))

@@ -163,6 +163,24 @@ size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n);
 int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b, void* out,
                            void* stream);
 
+/* Q4_1 codec over rows x cols values (each row its own run of blocks; a
+ * partial last block takes d and m from the values that exist and leaves the
+ * missing nibbles zero).
+ * nnops_hip_q4_1_quantize replaces quantize_q4 (include/nnops/detail/q4_1.hpp:
+ *   92-149, llama.cpp's quantize_row_q4_1_ref): src f32 (src_f16 = 0) or f16,
+ *   row stride ld_src elements -> dst rows of ceil(cols / 32) 20-byte blocks,
+ *   ld_dst_bytes apart (a multiple of 4, 4-byte-aligned dst). Byte-identical to
+ *   the reference: d = (max - min) / 15, m = min (f16, nearest even),
+ *   q = min(trunc((x - min) * (1 / d) + 0.5), 15).
+ * nnops_hip_q4_1_dequantize replaces pack_q4 (q4_1.hpp:155-183): blocks ->
+ *   f32 / f16 (dst_f16) rows, ld_dst elements apart; y = d * q + m in f32, f16
+ *   rounded to nearest even.
+ * Stream-ordered, no allocation, no workspace. */
+int nnops_hip_q4_1_quantize(const void* src, int32_t src_f16, int64_t rows, int64_t cols, int64_t ld_src,
+                            void* dst, int64_t ld_dst_bytes, void* stream);
+int nnops_hip_q4_1_dequantize(const void* src, int64_t ld_src_bytes, int64_t rows, int64_t cols, void* dst,
+                              int32_t dst_f16, int64_t ld_dst, void* stream);
+
 /* Q4_1-weight GEMM  C[M,N] = A[M,K] x dequant(B).
  * Replaces nnops' fp x q4_1 route: matmul_qblock_fused (small M,
  * src/backend/cpu/matmul/matmul_qblock_fused.cpp:174-197) and FpRoute with
@@ -234,16 +252,6 @@ int nnops_hip_dequantize_linear(const NnopsQdqArgs* args, void* stream);
 /* Library version and build target, for the caller's diagnostics. */
 const char* nnops_hip_build_info(void);
 
-/* Machine ceilings for the bench's roofline context; no counterpart in nnops.
- * nnops_hip_diag_mfma_i8: `blocks` x 4 waves, each `iters` x 8 independent
- *   v_mfma_i32_32x32x32_i8 from register operands (src: blocks*256*24 random
- *   ints, ignored when `constant`; out: blocks*256 ints); 65536 ops per MFMA.
- * nnops_hip_diag_stream_read: non-temporal 16-byte streaming read of `bytes`
- *   (16-byte aligned, a multiple of 16); out: 256 ints.
- * nnops_hip_diag_empty: an empty launch (the per-launch fixed cost). */
-int nnops_hip_diag_mfma_i8(const int* src, int* out, int blocks, int iters, int constant, void* stream);
-int nnops_hip_diag_stream_read(const void* buf, int64_t bytes, int* out, int blocks, void* stream);
-int nnops_hip_diag_empty(int* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@ import ctypes as C
 import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnnops_amd.so")
+DIAG_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnnops_amd_diag.so")
 
 OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_INITIALIZED, OUT_OF_MEMORY, INTERNAL = range(6)
 OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16 = range(5)
@@ -113,9 +114,10 @@ SIGNATURES = {
                                          C.c_void_p]),
     "nnops_hip_prepack_i8": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p,
                                        C.c_void_p]),
-    "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
-    "nnops_hip_diag_stream_read": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
-    "nnops_hip_diag_empty": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "nnops_hip_q4_1_quantize": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
+                                          C.c_int64, C.c_void_p]),
+    "nnops_hip_q4_1_dequantize": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int32,
+                                            C.c_int64, C.c_void_p]),
     "nnops_hip_quantize_linear": (C.c_int, [C.POINTER(QdqArgs), C.c_void_p]),
     "nnops_hip_dequantize_linear": (C.c_int, [C.POINTER(QdqArgs), C.c_void_p]),
     "nnops_matmul_attrs_init": (None, [C.POINTER(MatMulAttrs)]),
@@ -166,3 +168,28 @@ def load(path: str = LIB_PATH):
 
 def lib():
     return load()
+
+
+# include/nnops_amd_diag.h: measurement probes in their own library (bench only)
+DIAG_SIGNATURES = {
+    "nnops_hip_diag_mfma_i8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "nnops_hip_diag_stream_read": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
+    "nnops_hip_diag_empty": (C.c_int, [C.c_void_p, C.c_void_p]),
+}
+_diag = None
+
+
+def diag_lib():
+    """The probe library (libnnops_amd_diag.so), loaded after the product one."""
+    global _diag
+    if _diag is None:
+        load()
+        if not os.path.exists(DIAG_PATH):
+            raise RuntimeError(f"probe library missing: {DIAG_PATH}; build it with `python -m nnops_amd.build`")
+        d = C.CDLL(DIAG_PATH)
+        for name, (res, args) in DIAG_SIGNATURES.items():
+            fn = getattr(d, name)
+            fn.restype = res
+            fn.argtypes = args
+        _diag = d
+    return _diag

@@ -21,11 +21,14 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libnnops_amd.so")
+# measurement probes (include/nnops_amd_diag.h), kept out of the product library
+DIAG_SOURCES = ["csrc/kernels/diag.hip"]
+DIAG_LIB = os.path.join(PKG, "libnnops_amd_diag.so")
 
 SOURCES = [
     "csrc/kernels/gemm_i8.hip",
     "csrc/kernels/q4_1.hip",
-    "csrc/kernels/diag.hip",
+    "csrc/kernels/q4_1_codec.hip",
     "csrc/kernels/quant.hip",
     "csrc/host/ops.cpp",
     "csrc/host/quant_linear.cpp",
@@ -44,7 +47,7 @@ def hipcc() -> str:
 
 def _flags(src: str) -> list[str]:
     common = [
-        "-std=c++20", "-O3", "-fPIC", f"--offload-arch={ARCH}",
+        "-std=c++23", "-O3", "-fPIC", f"--offload-arch={ARCH}",
         "-I", os.path.join(ROOT, "include"),
         "-I", os.path.join(PKG, "include"),
         "-Wall", "-Wno-unused-function",
@@ -91,18 +94,19 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     than their source or any header)."""
     os.makedirs(BUILD, exist_ok=True)
     hdr = _headers_mtime()
-    todo = [s for s in SOURCES if not incremental or _stale(s, hdr)]
+    todo = [s for s in SOURCES + DIAG_SOURCES if not incremental or _stale(s, hdr)]
     with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(todo)))) as ex:
         list(ex.map(_compile, todo))
-    objs = [os.path.join(BUILD, os.path.basename(s) + ".o") for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}")
+    for srcs, lib in ((SOURCES, LIB), (DIAG_SOURCES, DIAG_LIB)):
+        objs = [os.path.join(BUILD, os.path.basename(s) + ".o") for s in srcs]
+        tmp = lib + ".tmp"
+        cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        os.replace(tmp, lib)
+        if verbose:
+            print(f"built {lib}")
     return LIB
 
 

@@ -44,7 +44,7 @@ struct Geometry {
     int64_t m = 0, n = 0, k = 0;
     int64_t batch = 1;
     bool trans_a = false, trans_b = false;
-    bool b_packed = false;  // B is a PackedBHip blob (always [N][kp])
+    bool b_packed = false;  // B is a PackedBHip blob (described as [N, K])
     // leading (batch) dims, broadcast
     int64_t nd = 0;
     int64_t out_batch[TensorDesc::kMaxRank]{};
@@ -68,21 +68,25 @@ Status matmul_geometry(const TensorDesc& a, const TensorDesc& b, bool ta, bool t
     g.m = ta ? ak : am;
     g.k = ta ? am : ak;
     if (b.layout == TensorLayout::PackedBHip) {
-        // A packed B carries N but no K: K is A's, and the blob must be large
-        // enough for it (nnops: the backend's numel check, matmul.cpp:84-90).
-        // s8: [N][kp] rows (read as transposed); q4_1: the two planes of a
-        // blocks-along-N weight (read as [K, N])
-        if (b.rank != 2) {
+        // A packed B is described as [N, K] with a row pitch that makes N rows
+        // cover the whole blob (prepack_s8 / prepack_q4_1 below): K must be
+        // A's exactly (the column-sum and d|m plane offsets depend on it) and
+        // the blob large enough for it (nnops: the backend's numel check,
+        // matmul.cpp:84-90). s8: [N][kp] rows (read as transposed); q4_1: the
+        // two planes of a blocks-along-N weight (read as [K, N])
+        if (b.rank != 2 || b1 != g.k) {
             return Status::invalid_argument;
         }
+        const int64_t unit = static_cast<int64_t>(data_type_stride_unit(b.dtype));
+        const int64_t pitch = b.row_stride_elems > 0 ? b.row_stride_elems * unit
+                                                     : static_cast<int64_t>(data_type_row_bytes(b.dtype, b1));
         if (b.dtype == DataType::s8) {
-            if (b0 * b1 < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(g.k, b0))) {
+            if (b0 * pitch < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(g.k, b0))) {
                 return Status::invalid_argument;
             }
             g.trans_b = true;
         } else if (b.dtype == DataType::q4_1) {
-            if (b0 * static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, b1)) <
-                static_cast<int64_t>(nnops_hip_prepack_q4_1_bytes(g.k, b0))) {
+            if (b0 * pitch < static_cast<int64_t>(nnops_hip_prepack_q4_1_bytes(g.k, b0))) {
                 return Status::invalid_argument;
             }
             g.trans_b = false;
@@ -826,8 +830,10 @@ Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const Tens
         return Status::invalid_argument;
     }
     if (w.layout == TensorLayout::PackedBHip) {
-        if (w.dtype != DataType::s8 ||
-            w.dims[0] * w.dims[1] < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(x2.dims[1], w.dims[0]))) {
+        // [N, K] with a pitch covering the blob (prepack_s8)
+        const int64_t pitch = w.row_stride_elems > 0 ? w.row_stride_elems : w.dims[1];
+        if (w.dtype != DataType::s8 || w.dims[1] != x2.dims[1] ||
+            w.dims[0] * pitch < static_cast<int64_t>(nnops_hip_prepack_i8_bytes(x2.dims[1], w.dims[0]))) {
             return Status::invalid_argument;
         }
     } else if (x2.dims[1] != w.dims[1]) {
@@ -922,8 +928,8 @@ namespace {
 
 /// The query / fill contract of nnops' prepackWeights (src/ops/matmul.cpp:
 /// 96-141): an empty outputs[0] is the query and receives the descriptor
-/// [N, ceil(bytes / N)] (s8, PackedBHip, pitched at its row length, carrying
-/// the weight's QuantParams); a populated one is filled on ctx's stream. A
+/// [N, K] (s8, PackedBHip, its row pitch ceil(bytes / N) so that N rows cover
+/// the blob, carrying the weight's QuantParams); a populated one is filled on ctx's stream. A
 /// weight with no packed form (anything but a 2-D s8 B or a 2-D q4_1 B with
 /// blocks along N) answers empty.
 Status prepack_q4_1(const TensorView& raw, std::span<TensorView> outputs, const ComputeContext& ctx);
@@ -955,16 +961,18 @@ Status prepack_s8(const TensorView& raw, bool trans_b, std::span<TensorView> out
         }
         return Status::invalid_argument;
     }
+    // described as [N, K] (K exact, so a call can check A against it) with a
+    // row pitch large enough for N rows to cover the blob
     const int64_t bytes = static_cast<int64_t>(nnops_hip_prepack_i8_bytes(k, n));
-    const int64_t cols = (bytes + n - 1) / n;
-    const int64_t shape[2] = {n, cols};
+    const int64_t pitch = std::max(k, (bytes + n - 1) / n);
+    const int64_t shape[2] = {n, k};
     if (outputs[0].is_empty()) {
-        outputs[0] = TensorView(shape, DataType::s8, nullptr, cols, TensorLayout::PackedBHip, raw.quant_params());
+        outputs[0] = TensorView(shape, DataType::s8, nullptr, pitch, TensorLayout::PackedBHip, raw.quant_params());
         return Status::ok;
     }
     const TensorView& o = outputs[0];
     if (o.layout() != TensorLayout::PackedBHip || o.data_type() != DataType::s8 || o.rank() != 2 ||
-        o.shape(0) != n || o.shape(1) != cols) {
+        o.shape(0) != n || o.shape(1) != k || o.pitch() != pitch) {
         return Status::invalid_argument;  // the packed buffer does not match the geometry
     }
     const int rc = nnops_hip_prepack_i8(raw.ptr<const int8_t>(), k, n, raw.row_stride_elems(), trans_b ? 1 : 0,
@@ -972,9 +980,8 @@ Status prepack_s8(const TensorView& raw, bool trans_b, std::span<TensorView> out
     return from_code(rc);
 }
 
-/// A blocks-along-N q4_1 weight [K, N] (values) -> PackedBHip q4_1 [N, cols]:
-/// the blob of nnops_hip_prepack_q4_1, cols the values whose q4_1 row bytes
-/// times N cover it. Blocks along K (transpose_b) have no packed form.
+/// A blocks-along-N q4_1 weight [K, N] (values) -> PackedBHip q4_1 [N, K]:
+/// the blob of nnops_hip_prepack_q4_1, with a row pitch whose N rows cover it. Blocks along K (transpose_b) have no packed form.
 Status prepack_q4_1(const TensorView& raw, std::span<TensorView> outputs, const ComputeContext& ctx)
 {
     const int64_t k = raw.shape(0), n = raw.shape(1);
@@ -985,17 +992,18 @@ Status prepack_q4_1(const TensorView& raw, std::span<TensorView> outputs, const 
         }
         return Status::invalid_argument;
     }
+    // described as [N, K] (K exact) with a row pitch of whole blocks large
+    // enough for N rows to cover the two planes
     const int64_t bytes = static_cast<int64_t>(nnops_hip_prepack_q4_1_bytes(k, n));
-    const int64_t cols = (bytes + n * 20 - 1) / (n * 20) * 32;
-    const int64_t pitch = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, cols));
-    const int64_t shape[2] = {n, cols};
+    const int64_t pitch = 20 * std::max((k + 31) / 32, (bytes + n * 20 - 1) / (n * 20));
+    const int64_t shape[2] = {n, k};
     if (outputs[0].is_empty()) {
         outputs[0] = TensorView(shape, DataType::q4_1, nullptr, pitch, TensorLayout::PackedBHip, raw.quant_params());
         return Status::ok;
     }
     const TensorView& o = outputs[0];
     if (o.layout() != TensorLayout::PackedBHip || o.data_type() != DataType::q4_1 || o.rank() != 2 ||
-        o.shape(0) != n || o.shape(1) != cols || o.pitch() != pitch) {
+        o.shape(0) != n || o.shape(1) != k || o.pitch() != pitch) {
         return Status::invalid_argument;
     }
     const int rc = nnops_hip_prepack_q4_1(raw.ptr<const uint8_t>(), k, n, raw.pitch(), 0, o.ptr<void>(),

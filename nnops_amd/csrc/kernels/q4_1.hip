@@ -1680,7 +1680,7 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         ((uintptr_t)g->b & 3)) {
         return NNOPS_INVALID_ARGUMENT;
     }
-    if (g->b_soa && (g->trans_b || g->b_dm == nullptr || (g->ldb_bytes & 15) || ((uintptr_t)g->b & 15) ||
+    if (g->b_soa && (g->trans_b || g->b_dm == nullptr || g->ldb_bytes != nbn * 16 || ((uintptr_t)g->b & 15) ||
                      ((uintptr_t)g->b_dm & 15) || (g->ldb_dm & 3) || g->ldb_dm < nbn)) {
         return NNOPS_INVALID_ARGUMENT;
     }

@@ -311,3 +311,33 @@ def gemm_q4_1(a, b, c, *, n, trans_b=True, ldb_bytes=None, workspace=None, strea
     if check and rc != 0:
         raise RuntimeError(f"nnops_hip_gemm_q4_1 failed: status {rc}")
     return rc
+
+
+def q4_1_quantize(x, out=None, *, stream=None):
+    """quantize_q4 on the device: ``x`` a 2-D f32/f16 torch tensor (rows of
+    values, any row stride) -> uint8 [rows, ceil(cols/32)*20] llama.cpp
+    block_q4_1 rows (``out`` if given). Raises on a rejected call."""
+    import torch
+    rows, cols = x.shape
+    nbb = (cols + 31) // 32 * 20
+    if out is None:
+        out = torch.empty((rows, nbb), dtype=torch.uint8, device=x.device)
+    rc = L.lib().nnops_hip_q4_1_quantize(x.data_ptr(), int(x.dtype == torch.float16), rows, cols, x.stride(0),
+                                         out.data_ptr(), out.stride(0), _stream_ptr(stream))
+    if rc != 0:
+        raise RuntimeError(f"nnops_hip_q4_1_quantize failed: status {rc}")
+    return out
+
+
+def q4_1_dequantize(blocks, cols, out=None, *, dtype=None, stream=None):
+    """pack_q4 on the device: uint8 [rows, nb*20] block rows -> f32 (or
+    ``dtype`` f16) [rows, cols] (``out`` if given)."""
+    import torch
+    rows = blocks.shape[0]
+    if out is None:
+        out = torch.empty((rows, cols), dtype=dtype or torch.float32, device=blocks.device)
+    rc = L.lib().nnops_hip_q4_1_dequantize(blocks.data_ptr(), blocks.stride(0), rows, cols, out.data_ptr(),
+                                           int(out.dtype == torch.float16), out.stride(0), _stream_ptr(stream))
+    if rc != 0:
+        raise RuntimeError(f"nnops_hip_q4_1_dequantize failed: status {rc}")
+    return out

@@ -139,6 +139,13 @@ def cpu_lib():
                                            C.c_int64, C.c_float, C.c_void_p, C.c_float, C.c_int32, C.c_int,
                                            C.c_int]
         _cpu.ref_cpu_matmul_s8.restype = C.c_int
+        _cpu.ref_cpu_matmul_i8.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
+                                           C.c_int64, C.c_int, C.c_int, C.c_float, C.c_void_p, C.c_float,
+                                           C.c_int32, C.c_int, C.c_int]
+        _cpu.ref_cpu_matmul_i8.restype = C.c_int
+        _cpu.ref_cpu_matmul_q4_1.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
+                                             C.c_int, C.c_int]
+        _cpu.ref_cpu_matmul_q4_1.restype = C.c_int
     return _cpu
 
 

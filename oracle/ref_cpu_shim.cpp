@@ -109,15 +109,7 @@ private:
     int busy_ = 0;
 };
 
-}  // namespace
-
-extern "C" {
-
-// s8 A [M,K] x s8 W [N,K] (the Linear weight) -> s8 C [M,N]: per-tensor A
-// scale, per-channel W scales, int32 bias, Relu, per-tensor output scale and
-// zero point (nnops' requant, half away from zero). `threads` workers.
-int ref_cpu_matmul_s8(const int8_t* a, const int8_t* w, const int32_t* bias, int8_t* c, int64_t M, int64_t N,
-                      int64_t K, float s_a, const float* s_b, float s_out, int32_t zp_out, int relu, int threads)
+Pool* pool_of(int threads)
 {
     static std::mutex pm;
     static std::unique_ptr<Pool> pool;
@@ -126,37 +118,90 @@ int ref_cpu_matmul_s8(const int8_t* a, const int8_t* w, const int32_t* bias, int
         pool.reset();
         pool = std::make_unique<Pool>(threads);
     }
-    Pool* p = pool.get();
+    return pool.get();
+}
 
-    QuantParams qa;
-    qa.scale = s_a;
-    QuantParams qb;
-    qb.granularity = QuantGranularity::PerChannel;
-    qb.scale_data = s_b;
-    qb.num_scales = N;
-    QuantParams qc;
-    qc.scale = s_out;
-    qc.zero_point = zp_out;
-    const int64_t ashape[] = {M, K}, wshape[] = {N, K}, cshape[] = {M, N}, bshape[] = {N};
-    TensorView av(ashape, DataType::s8, const_cast<int8_t*>(a), TensorLayout::Dense, qa);
-    TensorView wv(wshape, DataType::s8, const_cast<int8_t*>(w), TensorLayout::Dense, qb);
-    TensorView bv(bshape, DataType::s32, const_cast<int32_t*>(bias));
-    TensorView cv(cshape, DataType::s8, c, TensorLayout::Dense, qc);
-
-    MatMulAttributes attrs{};
-    attrs.transpose_b = true;
-    attrs.output_dtype = DataType::s8;
-    if (relu) {
-        attrs.epilogue.type = EpilogueActivateType::Relu;
-    }
-    auto op = MatMul::create(attrs, Backend::CPU);
+ComputeContext context_on(Pool* p)
+{
     ComputeContext ctx{};
     ctx.cpu.parallel_for = [p](int64_t b, int64_t e, const ParallelForBody& body) { p->run(b, e, body); };
     ctx.cpu.num_threads = [p] { return p->size(); };
     ctx.cpu.thread_id = [] { return Pool::tid(); };
+    return ctx;
+}
+
+}  // namespace
+
+extern "C" {
+
+// s8 A [M,K] x s8 W ([N,K] with trans_b, else [K,N]) -> s32 (out_s8 = 0) or
+// s8 C [M,N]: per-tensor A scale, per-channel W scales (or s_b = NULL: 1),
+// int32 bias (or NULL), Relu, per-tensor output scale and zero point (nnops'
+// requant, half away from zero). `threads` workers.
+int ref_cpu_matmul_i8(const int8_t* a, const int8_t* w, const int32_t* bias, void* c, int64_t M, int64_t N,
+                      int64_t K, int trans_b, int out_s8, float s_a, const float* s_b, float s_out, int32_t zp_out,
+                      int relu, int threads)
+{
+    Pool* p = pool_of(threads);
+    QuantParams qa;
+    qa.scale = s_a;
+    QuantParams qb;
+    if (s_b != nullptr) {
+        qb.granularity = QuantGranularity::PerChannel;
+        qb.scale_data = s_b;
+        qb.num_scales = N;
+    }
+    QuantParams qc;
+    qc.scale = s_out;
+    qc.zero_point = zp_out;
+    const int64_t ashape[] = {M, K}, wshape_t[] = {N, K}, wshape[] = {K, N}, cshape[] = {M, N}, bshape[] = {N};
+    TensorView av(ashape, DataType::s8, const_cast<int8_t*>(a), TensorLayout::Dense, qa);
+    TensorView wv(trans_b ? std::span<const int64_t>(wshape_t) : std::span<const int64_t>(wshape), DataType::s8,
+                  const_cast<int8_t*>(w), TensorLayout::Dense, qb);
+    TensorView bv(bshape, DataType::s32, const_cast<int32_t*>(bias));
+    const DataType odt = out_s8 ? DataType::s8 : DataType::s32;
+    TensorView cv(cshape, odt, c, TensorLayout::Dense, out_s8 ? qc : QuantParams{});
+
+    MatMulAttributes attrs{};
+    attrs.transpose_b = trans_b != 0;
+    attrs.output_dtype = odt;
+    if (relu) {
+        attrs.epilogue.type = EpilogueActivateType::Relu;
+    }
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
     const TensorView ins[] = {av, wv, bv};
     TensorView outs[] = {cv};
     const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, bias ? 3 : 2), ctx);
+    return static_cast<int>(st);
+}
+
+int ref_cpu_matmul_s8(const int8_t* a, const int8_t* w, const int32_t* bias, int8_t* c, int64_t M, int64_t N,
+                      int64_t K, float s_a, const float* s_b, float s_out, int32_t zp_out, int relu, int threads)
+{
+    return ref_cpu_matmul_i8(a, w, bias, c, M, N, K, 1, 1, s_a, s_b, s_out, zp_out, relu, threads);
+}
+
+// f16 A [M,K] x q4_1 W -> f16 C [M,N] (nnops' fp x q4_1 route: the output
+// dtype follows A; matmul_qblock_fused for small M, src/ops/matmul.cpp:49-58).
+// W is [N][ceil(K/32)] blocks with trans_b (the Linear/GGUF form), else
+// [K][ceil(N/32)] blocks.
+int ref_cpu_matmul_q4_1(const uint16_t* a, const uint8_t* w, uint16_t* c, int64_t M, int64_t N, int64_t K,
+                        int trans_b, int threads)
+{
+    Pool* p = pool_of(threads);
+    const int64_t ashape[] = {M, K}, wshape_t[] = {N, K}, wshape[] = {K, N}, cshape[] = {M, N};
+    TensorView av(ashape, DataType::f16, const_cast<uint16_t*>(a));
+    TensorView wv(trans_b ? std::span<const int64_t>(wshape_t) : std::span<const int64_t>(wshape), DataType::q4_1,
+                  const_cast<uint8_t*>(w));
+    TensorView cv(cshape, DataType::f16, c);
+    MatMulAttributes attrs{};
+    attrs.transpose_b = trans_b != 0;
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {av, wv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 2), ctx);
     return static_cast<int>(st);
 }
 

@@ -35,6 +35,19 @@ def test_library_exports_every_declared_symbol():
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
 
 
+def test_probe_library_is_separate():
+    """The measurement probes live in libnnops_amd_diag.so, declared by
+    nnops_amd_diag.h; the product library exports none of them."""
+    text = open(os.path.join(ROOT, "include", "nnops_amd_diag.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = {m.group(1) for m in re.finditer(r"\b(nnops_\w+)\s*\(", text)}
+    assert names == set(L.DIAG_SIGNATURES)
+    d = L.diag_lib()
+    for n in names:
+        assert hasattr(d, n), n
+        assert not hasattr(na.lib(), n), n
+
+
 def test_build_info():
     assert b"gfx950" in na.lib().nnops_hip_build_info()
 
@@ -91,6 +104,16 @@ def test_gemm_q4_1_rejects_before_any_launch():
     g.ldb_bytes = 39  # shorter than one row of blocks
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
     g.ldb_bytes = 42  # not a multiple of 4
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    # the prepacked planes (b_soa) have one nibble-row pitch, nbn * 16: the
+    # GEMV and the ring place the 8-row groups by it, so a padded pitch is
+    # rejected rather than read two different ways
+    g.trans_b, g.b_soa, g.b_dm, g.ldb_dm = 0, 1, 4096, 4
+    g.ldb_bytes = 32
+    g.m = 0  # an empty problem returns before the argument checks: ok
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.OK
+    g.m = 2
+    g.ldb_bytes = 48
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
 
 
@@ -214,7 +237,7 @@ def test_quant_linear_descriptors_and_validate():
 
 
 def test_prepack_query_descriptor():
-    # query: [N, ceil(bytes / N)] s8 PackedBHip (no launch); non-s8 answers empty
+    # query: [N, K] s8 PackedBHip pitched at ceil(bytes / N) (no launch); non-s8 answers empty
     lib = na.lib()
     op = na.MatMul(output_dtype=na.DT_S8)             # B [K, N]
     w = desc([300, 100], na.DT_S8)
@@ -223,23 +246,28 @@ def test_prepack_query_descriptor():
     assert lib.nnops_op_prepack_weights(op._h, ins, 1, out, 1, None) == na.OK
     kp = 384
     nbytes = ((100 * kp + 255) // 256) * 256 + 4 * 100
-    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == -(-nbytes // 100)
+    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == 300
     assert out[0].dtype == na.DT_S8 and out[0].layout == L.LAYOUT_PACKED_B_HIP
-    assert out[0].pitch == out[0].dims[1]
+    assert out[0].pitch == -(-nbytes // 100)
+    s8packed = out[0]
+    # K must be A's exactly: a smaller K in the same 128-padded row is rejected too
+    assert op.validate([desc([7, 300], na.DT_S8), s8packed], [desc([7, 100], na.DT_S32)]) == na.OK
+    assert op.validate([desc([7, 290], na.DT_S8), s8packed], [desc([7, 100], na.DT_S32)]) \
+        == na.INVALID_ARGUMENT
     assert lib.nnops_hip_prepack_i8_bytes(300, 100) == nbytes
     # Linear: the weight is [N, K]
     lop = na.Linear(output_dtype=na.DT_S8)
     ins = (L.Tensor * 1)(desc([100, 300], na.DT_S8))
     out = (L.Tensor * 1)()
     assert lib.nnops_op_prepack_weights(lop._h, ins, 1, out, 1, None) == na.OK
-    assert out[0].dims[0] == 100 and out[0].dims[1] == -(-nbytes // 100)
+    assert out[0].dims[0] == 100 and out[0].dims[1] == 300 and out[0].pitch == -(-nbytes // 100)
     # q4_1 / f32 weights: no packed form
     ins = (L.Tensor * 1)(desc([64, 16], na.DT_F32))
     out = (L.Tensor * 1)()
     assert lib.nnops_op_prepack_weights(op._h, ins, 1, out, 1, None) == na.OK
     assert out[0].rank == 0
     # q4_1 with blocks along N ([K, N], transpose_b false): PackedBHip q4_1
-    # [N, cols], cols the values whose row bytes times N cover the two planes
+    # [N, K], pitched at whole blocks so that N rows cover the two planes
     q_bytes = lib.nnops_hip_prepack_q4_1_bytes(256, 100)
     nbn = 4
     assert q_bytes == ((256 * nbn * 16 + 255) // 256) * 256 + 256 * 4 * 4
@@ -247,15 +275,17 @@ def test_prepack_query_descriptor():
     ins = (L.Tensor * 1)(desc([256, 100], na.DT_Q4_1))
     out = (L.Tensor * 1)()
     assert lib.nnops_op_prepack_weights(qop._h, ins, 1, out, 1, None) == na.OK
-    cols = -(-q_bytes // (100 * 20)) * 32
-    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == cols
+    assert out[0].rank == 2 and out[0].dims[0] == 100 and out[0].dims[1] == 256
     assert out[0].dtype == na.DT_Q4_1 and out[0].layout == L.LAYOUT_PACKED_B_HIP
-    assert out[0].pitch == cols // 32 * 20
+    assert out[0].pitch == 20 * max(256 // 32, -(-q_bytes // (100 * 20)))
     qpacked = out[0]
     shape, dt = qop.output_desc([desc([7, 256], na.DT_F16), qpacked])
     assert shape == [7, 100] and dt == na.DT_F16
-    # A with a larger K than the blob was packed for
+    # A with a larger or a smaller K than the blob was packed for (the d|m
+    # plane's offset depends on K)
     assert qop.validate([desc([7, 4096], na.DT_F16), qpacked], [desc([7, 100], na.DT_F16)]) \
+        == na.INVALID_ARGUMENT
+    assert qop.validate([desc([7, 248], na.DT_F16), qpacked], [desc([7, 100], na.DT_F16)]) \
         == na.INVALID_ARGUMENT
     # blocks along K (transpose_b, and Linear's [N, K] weight): no packed form
     tb = na.MatMul(transpose_b=True)
@@ -268,10 +298,23 @@ def test_prepack_query_descriptor():
     assert lib.nnops_op_prepack_weights(lq._h, ins, 1, out, 1, None) == na.OK
     assert out[0].rank == 0
     assert lib.nnops_hip_prepack_q4_1(None, 256, 100, 80, 1, None, None) == na.UNSUPPORTED
-    # a packed B: output descriptor from its N and A's K; a blob too small for K is rejected
-    packed = desc([100, -(-nbytes // 100)], na.DT_S8)
+    # a packed B: output descriptor from its N and A's K; a K other than the
+    # packed one, or a pitch too small for the blob, is rejected
+    packed = desc([100, 300], na.DT_S8)
     packed.layout = L.LAYOUT_PACKED_B_HIP
+    packed.pitch = -(-nbytes // 100)
     shape, dt = op.output_desc([desc([7, 300], na.DT_S8), packed])
     assert shape == [7, 100] and dt == na.DT_S8
     assert op.validate([desc([7, 300], na.DT_S8), packed], [desc([7, 100], na.DT_S8)]) == na.OK
     assert op.validate([desc([7, 600], na.DT_S8), packed], [desc([7, 100], na.DT_S8)]) == na.INVALID_ARGUMENT
+    packed.pitch = 300
+    assert op.validate([desc([7, 300], na.DT_S8), packed], [desc([7, 100], na.DT_S8)]) == na.INVALID_ARGUMENT
+
+
+def test_q4_1_codec_rejects_before_any_launch():
+    lib = na.lib()
+    assert lib.nnops_hip_q4_1_quantize(16, 0, 2, 64, 32, 16, 40, None) == na.INVALID_ARGUMENT   # ld_src < cols
+    assert lib.nnops_hip_q4_1_quantize(16, 0, 2, 64, 64, 16, 38, None) == na.INVALID_ARGUMENT   # pitch < 40
+    assert lib.nnops_hip_q4_1_quantize(None, 0, 2, 64, 64, 16, 40, None) == na.INVALID_ARGUMENT
+    assert lib.nnops_hip_q4_1_quantize(None, 0, 0, 64, 64, None, 40, None) == na.OK              # empty
+    assert lib.nnops_hip_q4_1_dequantize(16, 36, 2, 64, 16, 0, 64, None) == na.INVALID_ARGUMENT

@@ -33,16 +33,19 @@ def scal_or_dev(x):
 def run_gpu(a, b, out_kind, *, trans_b, bias=None, s_a=1.0, zp_a=0, s_b=1.0, zp_b=0, s_out=1.0,
             zp_out=0, relu=False, round_even=False, trans_a=False, lda=None, ldc=None, c_init=None,
             float_ep=False, act=None, add_to=False, residual_pre=False, s_out_rows=None,
-            zp_out_rows=None):
+            zp_out_rows=None, c_dev=None):
     import torch
     odt = {0: np.int32, 1: np.int8, 2: np.uint8}[out_kind]
     M = a.shape[1] if trans_a else a.shape[0]
     N = b.shape[0] if trans_b else b.shape[1]
     da = pitched(a, lda) if lda else dev(a)
     db = dev(b)
-    if c_init is None:
-        c_init = np.zeros((M, N), odt)
-    dc = pitched(c_init, ldc) if ldc else dev(c_init)
+    if c_dev is not None:
+        dc = c_dev
+    else:
+        if c_init is None:
+            c_init = np.zeros((M, N), odt)
+        dc = pitched(c_init, ldc) if ldc else dev(c_init)
     kw = dict(trans_a=trans_a, trans_b=trans_b, out_kind=out_kind, bias=None if bias is None else dev(bias),
               s_a=scal_or_dev(s_a), zp_a=scal_or_dev(zp_a), s_b=scal_or_dev(s_b), zp_b=scal_or_dev(zp_b),
               s_out=float(s_out), zp_out=int(zp_out), round_even=round_even, float_ep=float_ep,
@@ -223,3 +226,39 @@ def test_kn_gemv_weight_zero_point_and_tables(M):
     np.testing.assert_array_equal(got, want)
     got = run_gpu(a, b, na.OUT_S32, trans_b=False, zp_b=zpb)
     np.testing.assert_array_equal(got, oracle.gemm_i8(a, b, zp_b=zpb))
+
+
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("s_out", [0.05, 2.0])
+def test_config5_full_workload_sampled_rows(trans_b, s_out):
+    """BASELINE config 5 at its real workload: M=333, K=14336, N=4096, A row
+    pitch 14400 B, C row pitch 4160 B (sentinel-filled padding), s8 add_to
+    residual into a pre-filled C, GELU through the f32 epilogue, requant.
+    s_out 0.05 is the config's literal scale (mostly saturated outputs);
+    2.0 keeps most outputs inside (-128, 127). The weight is the MatMul's
+    [K,N] (trans_b False) or the Linear's [N,K]. Three bands of 8 rows, which
+    cover the first, a middle and the last (ragged) row tile, are compared
+    bit for bit with the oracle; the padding must be untouched."""
+    announce(f"config5 full trans_b={trans_b} s_out={s_out}")
+    M, K, N, LDA, LDC = 333, 14336, 4096, 14400, 4160
+    a = dg.act_s8(501, (M, K))
+    w = dg.ints(502, (K, N), -127, 127)
+    if trans_b:
+        w = np.ascontiguousarray(w.T)
+    sb = dg.uniform(503, (N,), 0.001, 0.01)
+    bias = dg.ints(504, (N,), -5000, 5000, np.int32)
+    c0 = dg.ints(505, (M, N), -128, 127)
+    import torch
+    dc = pitched(c0, LDC)
+    got = run_gpu(a, w, na.OUT_S8, trans_b=trans_b, bias=bias, s_a=0.02, s_b=sb, s_out=s_out, lda=LDA,
+                  c_init=None, ldc=None, float_ep=True, act=na.ACT_GELU, add_to=True, residual_pre=False,
+                  c_dev=dc)
+    pad = host(dc.as_strided((M, LDC - N), (LDC, 1), dc.storage_offset() + N))
+    assert np.all(pad == 0x5A), "C padding written"
+    for r0 in (0, 160, 325):
+        want = oracle.gemm_i8(a, w, trans_b=trans_b, bias=bias, out_kind=oracle.OUT_S8, s_a=0.02, s_b=sb,
+                              s_out=s_out, float_ep=True, act=oracle.ACT_GELU, add_to=True,
+                              residual_pre=False, c=c0.copy(), rows=(r0, r0 + 8))
+        np.testing.assert_array_equal(got[r0:r0 + 8], want[r0:r0 + 8])
+    if s_out == 2.0:
+        assert np.mean((got > -128) & (got < 127)) > 0.5

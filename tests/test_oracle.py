@@ -259,3 +259,154 @@ def test_oracle_matches_nnops_cpu_matmul(M, N, K, relu, zp):
     want = oracle.gemm_i8(a, w, trans_b=True, bias=bias, out_kind=oracle.OUT_S8, s_a=0.02, s_b=sb, s_out=0.05,
                           zp_out=zp, act=oracle.ACT_RELU if relu else oracle.ACT_NONE)
     np.testing.assert_array_equal(c, want)
+
+
+# --- the float epilogue on s8/u8 destinations (no reference route) -----------
+#
+# nnops rejects an s8 add_to and ignores GELU on integer destinations
+# (src/backend/cpu/matmul/linear.cpp:226, matmul_i8.cpp:100-103), so the
+# composite is defined here:  f = float(acc + bias) * (s_a * s_b);
+# r = float(C_old - zp) * s_out;  y = act(clip(f [+ r pre])) [+ r post];
+# q = sat(round_half_away(y / s_out)) + zp.  Each check below is chosen so a
+# plausible slip (residual scaled by the wrong scale, added on the wrong side
+# of the activation, a zero point applied twice, the bias outside the
+# accumulator) fails it.
+
+def _round_away64(x):
+    return np.trunc(x + np.copysign(0.5, x))
+
+
+def _float_ep_case(seed, M=23, N=41, K=37):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    old = rng.integers(-128, 128, (M, N)).astype(np.int8)
+    return rng, a, w, old
+
+
+@ref_only
+@pytest.mark.parametrize("zp_out", [0, 7, -5])
+def test_float_ep_without_residual_is_requant_of_reference_dq(zp_out):
+    """add_to off, no activation: the float epilogue equals the half-away
+    requant (f32 division by s_out) of the f32 output of nnops' own dq GEMM
+    (tests/reference/matmul_dq_ref.cpp:178-190, compiled in oracle/_ref). A is
+    handed to the reference as floats a * s_a with a power-of-two s_a, which
+    its QuantizeLinear maps back to the same integers exactly."""
+    rng, a, w, _ = _float_ep_case(11 + zp_out)
+    M, K = a.shape
+    N = w.shape[0]
+    s_a = np.float32(2.0 ** -5)
+    s_b = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    s_out = np.float32(0.37)
+    af = (a.astype(np.float32) * s_a).astype(np.float32)
+    f = np.zeros((M, N), np.float32)
+    oracle.ref_lib().ref_matmul_dq(af.ctypes.data, 0, w.ctypes.data, None, f.ctypes.data, M, N, K,
+                                   af.strides[0], w.strides[0], f.strides[0], 1, 0,
+                                   None, float(s_a), None, 0, s_b.ctypes.data, 1.0, None, 0,
+                                   oracle.ACT_NONE, 0.0, 1.0, -np.inf, np.inf)
+    x = (f / s_out).astype(np.float64)              # f32 quotient, as the epilogue divides
+    want = np.clip(_round_away64(x) + zp_out, -128, 127).astype(np.int8)
+    got = oracle.gemm_i8(a, w, trans_b=True, out_kind=oracle.OUT_S8, s_a=float(s_a), s_b=s_b,
+                         s_out=float(s_out), zp_out=zp_out, float_ep=True)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("act,pre", [(oracle.ACT_NONE, False), (oracle.ACT_NONE, True),
+                                     (oracle.ACT_RELU, False), (oracle.ACT_RELU, True)])
+def test_float_ep_residual_closed_form_power_of_two(act, pre):
+    """Power-of-two scales and small K keep every f32 step exact, so the
+    epilogue must equal the float64 closed form
+    round((acc + bias) * s_a * s_b + (C_old - zp) * s_out) / s_out) + zp
+    with the residual before or after Relu. The Relu cases must differ
+    between the two orders somewhere, or the check would not tell them apart."""
+    rng, a, w, old = _float_ep_case(5)
+    N = w.shape[0]
+    s_a, s_out, zp = 2.0 ** -4, 2.0 ** -3, 3
+    s_b = (2.0 ** -rng.integers(6, 10, N)).astype(np.float32)
+    bias = rng.integers(-3000, 3000, N).astype(np.int32)
+    acc = a.astype(np.int64) @ w.astype(np.int64).T + bias
+    f = acc * s_a * s_b.astype(np.float64)
+    r = (old.astype(np.float64) - zp) * s_out
+    relu = (lambda v: np.maximum(v, 0.0)) if act == oracle.ACT_RELU else (lambda v: v)
+    y = relu(f + r) if pre else relu(f) + r
+    want = np.clip(_round_away64(y / s_out) + zp, -128, 127).astype(np.int8)
+    got = oracle.gemm_i8(a, w, trans_b=True, bias=bias, out_kind=oracle.OUT_S8, s_a=s_a, s_b=s_b,
+                         s_out=s_out, zp_out=zp, act=act, float_ep=True, add_to=True, residual_pre=pre,
+                         c=old.copy())
+    np.testing.assert_array_equal(got, want)
+    if act == oracle.ACT_RELU:
+        other = relu(f) + r if pre else relu(f + r)
+        assert np.any(np.clip(_round_away64(other / s_out) + zp, -128, 127) != want)
+    # the unsaturated bulk carries the information: most outputs inside (-128, 127)
+    assert np.mean((want > -128) & (want < 127)) > 0.5
+
+
+def test_float_ep_gelu_residual_against_float64():
+    """GELU with a post-activation residual against a float64 evaluation of
+    nnops' GELU formula (simd_epilogue.hpp:76-79): outputs agree exactly except
+    where the f32 value lies within a rounding step of a .5 boundary (at most
+    1 apart there), and adding the residual before GELU instead would differ."""
+    rng, a, w, old = _float_ep_case(9, M=40, N=64, K=200)
+    N = w.shape[0]
+    s_a, s_out, zp = 0.02, 0.05, -2
+    s_b = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.integers(-5000, 5000, N).astype(np.int32)
+    acc = a.astype(np.int64) @ w.astype(np.int64).T + bias
+    f = acc * (np.float64(np.float32(s_a) * s_b))
+    r = (old.astype(np.float64) - zp) * np.float64(np.float32(s_out))
+
+    def gelu(x):
+        return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+
+    x = (gelu(f) + r) / np.float64(np.float32(s_out))
+    want = np.clip(_round_away64(x) + zp, -128, 127)
+    got = oracle.gemm_i8(a, w, trans_b=True, bias=bias, out_kind=oracle.OUT_S8, s_a=s_a, s_b=s_b,
+                         s_out=s_out, zp_out=zp, act=oracle.ACT_GELU, float_ep=True, add_to=True,
+                         residual_pre=False, c=old.copy()).astype(np.int64)
+    diff = np.abs(got - want)
+    near_tie = np.abs(np.abs(x - np.trunc(x)) - 0.5) < 1e-4
+    assert diff.max() <= 1 and np.all(diff[~near_tie] == 0)
+    assert np.mean((want > -128) & (want < 127)) > 0.5
+    wrong = np.clip(_round_away64((gelu(f + r)) / np.float64(np.float32(s_out))) + zp, -128, 127)
+    assert np.mean(wrong != want) > 0.1
+
+
+@cpu_only
+@pytest.mark.parametrize("M,N,K,trans_b,out_s8", [(128, 1024, 1024, False, False), (128, 1024, 1024, True, False),
+                                                  (1, 1000, 4096, False, True), (4, 300, 4096, False, False),
+                                                  (16, 260, 512, True, True)])
+def test_oracle_matches_nnops_cpu_matmul_layouts(M, N, K, trans_b, out_s8):
+    """The routes bench.py's CPU baselines time (config 1: s32, no bias;
+    config 3: the [K,N] weight, M in {1,4,16}, s32 and s8), bit for bit
+    against the oracle."""
+    a = dg.act_s8(M + 5, (M, K))
+    w = dg.ints(N + 6, (N, K) if trans_b else (K, N), -127, 127)
+    sb = dg.uniform(K + 7, (N,), 0.001, 0.01) if out_s8 else None
+    c = np.zeros((M, N), np.int8 if out_s8 else np.int32)
+    rc = oracle.cpu_lib().ref_cpu_matmul_i8(a.ctypes.data, w.ctypes.data, None, c.ctypes.data, M, N, K, int(trans_b),
+                                            int(out_s8), 0.02, None if sb is None else sb.ctypes.data, 0.05, 0, 0, 4)
+    assert rc == 0
+    if out_s8:
+        want = oracle.gemm_i8(a, w, trans_b=trans_b, out_kind=oracle.OUT_S8, s_a=0.02, s_b=sb, s_out=0.05)
+    else:
+        want = oracle.gemm_i8(a, w, trans_b=trans_b)
+    np.testing.assert_array_equal(c, want)
+
+
+@cpu_only
+@pytest.mark.parametrize("M,trans_b", [(1, True), (1, False), (5, True)])
+def test_oracle_q4_1_close_to_nnops_cpu_matmul(M, trans_b):
+    """nnops' own fp x q4_1 MatMul (f16 A -> f16 C, the config-4 CPU
+    baseline's route) against the oracle's dequant GEMM with the nnops
+    rounding of the decoded weight to f16 and an f16 output: within one f16
+    rounding of the output plus the f32 summation order."""
+    K, N = 1024, 256
+    a = dg.normal(61 + M, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(62, N, K) if trans_b else dg.q4_1_blocks(62, K, N)
+    c = np.zeros((M, N), np.float16)
+    rc = oracle.cpu_lib().ref_cpu_matmul_q4_1(a.ctypes.data, blk.ctypes.data, c.ctypes.data, M, N, K, int(trans_b), 4)
+    assert rc == 0
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b, w_round_f16=True)
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    err = np.abs(c.astype(np.float64) - want) / np.maximum(np.abs(want), rms)
+    assert err.max() < 2e-3
