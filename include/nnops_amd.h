@@ -128,6 +128,19 @@ size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* args);
 int nnops_hip_gemm_i8(const NnopsGemmI8Args* args, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* No counterpart in nnops. nnops_hip_gemm_i8 for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same kernels and results, with the workspace taken from a
+ * fixed device array of NNOPS_HIP_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends. A call whose plan needs
+ * more (nnops_hip_gemm_i8_workspace_size > the limit, e.g. a raw [K,N] B of
+ * 64 MiB that is staged transposed) returns NNOPS_OUT_OF_MEMORY and enqueues
+ * nothing. Calls on one GPU share the array: calls that may overlap on one
+ * GPU (two streams, two threads) race. `stream` must belong to the current
+ * device. Nothing is allocated, no host sync. */
+#define NNOPS_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+int nnops_hip_gemm_i8_noalloc(const NnopsGemmI8Args* args, void* stream);
+
 /* Prepacked s8 B for the HIP kernels (nnops' MatMul::prepackWeights,
  * src/ops/matmul.cpp:96-141, with a gfx950 layout in place of the CPU
  * panels). From B [K,N] (trans_b = 0) or [N,K] (trans_b = 1), row stride ldb,

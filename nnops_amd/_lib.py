@@ -105,6 +105,7 @@ class LinearAttrs(C.Structure):
 SIGNATURES = {
     "nnops_hip_gemm_i8_workspace_size": (C.c_size_t, [C.POINTER(GemmI8Args)]),
     "nnops_hip_gemm_i8": (C.c_int, [C.POINTER(GemmI8Args), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "nnops_hip_gemm_i8_noalloc": (C.c_int, [C.POINTER(GemmI8Args), C.c_void_p]),
     "nnops_hip_gemm_q4_1_workspace_size": (C.c_size_t, [C.POINTER(GemmQ41Args)]),
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),

@@ -27,6 +27,7 @@ DIAG_LIB = os.path.join(PKG, "libnnops_amd_diag.so")
 
 SOURCES = [
     "csrc/kernels/gemm_i8.hip",
+    "csrc/kernels/gemm_i8_noalloc.hip",
     "csrc/kernels/q4_1.hip",
     "csrc/kernels/q4_1_codec.hip",
     "csrc/kernels/quant.hip",

@@ -253,10 +253,12 @@ def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_
             zp_out_rows=None, act=L.ACT_NONE, round_even=False, float_ep=False,
             min_clip=-math.inf, max_clip=math.inf, add_to=False, residual_pre=False,
             bias_fp=None, act_alpha=0.0, act_beta=1.0,
-            m=None, n=None, k=None, workspace=None, stream=None, check=True):
+            m=None, n=None, k=None, workspace=None, stream=None, check=True, noalloc=False):
     """Direct call of nnops_hip_gemm_i8 on torch device tensors. Scales/zero
     points are python scalars or device tensors (per row / per column). An
-    f32/f16 destination (OUT_F32 / OUT_F16) takes its bias as `bias_fp`."""
+    f32/f16 destination (OUT_F32 / OUT_F16) takes its bias as `bias_fp`.
+    noalloc: call nnops_hip_gemm_i8_noalloc instead (the library's own fixed
+    scratch; `workspace` is ignored)."""
     import torch
     g = L.GemmI8Args()
     M = m if m is not None else (a.shape[1] if trans_a else a.shape[0])
@@ -282,6 +284,11 @@ def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_
     g.add_to, g.residual_pre = int(add_to), int(residual_pre)
     g.bias_fp, g.act_alpha, g.act_beta = _ptr(bias_fp), act_alpha, act_beta
     lib = L.lib()
+    if noalloc:
+        rc = lib.nnops_hip_gemm_i8_noalloc(C.byref(g), _stream_ptr(stream))
+        if check and rc != 0:
+            raise RuntimeError(f"nnops_hip_gemm_i8_noalloc failed: status {rc}")
+        return rc
     need = lib.nnops_hip_gemm_i8_workspace_size(C.byref(g))
     if workspace is None:
         workspace = _workspace(need, a.device)
