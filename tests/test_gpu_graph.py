@@ -52,18 +52,21 @@ def test_int8_routes_under_graph_replay(M, K, N, out):
     graph_replays_match(fn, c)
 
 
-def test_q4_1_under_graph_replay():
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_q4_1_under_graph_replay(trans_b):
+    """Both Q4_1 layouts; blocks along N at M <= 2 is the one-launch GEMV whose
+    arrival counters carry the launch epoch baked into the graph."""
     import torch
-    announce("graph q4_1")
+    announce(f"graph q4_1 trans_b={trans_b}")
     K, N = 4096, 2048
-    blk = dev(dg.q4_1_blocks(5, N, K))
-    for M in (1, 256):
+    blk = dev(dg.q4_1_blocks(5, N, K) if trans_b else dg.q4_1_blocks(5, K, N))
+    for M in (1, 2, 256):
         a = dev(dg.normal(6 + M, (M, K)).astype(np.float16))
         c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
         ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
 
         def fn(s, a=a, c=c, ws=ws):
-            na.gemm_q4_1(a, blk, c, n=N, trans_b=True, workspace=ws, stream=s.cuda_stream)
+            na.gemm_q4_1(a, blk, c, n=N, trans_b=trans_b, workspace=ws, stream=s.cuda_stream)
         graph_replays_match(fn, c)
 
 

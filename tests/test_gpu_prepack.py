@@ -120,12 +120,14 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     got_r = run(op, at, wt, torch.float32, (M, N))
     if M > 2 and a_f16:
         np.testing.assert_array_equal(got_p, got_r)    # the ring: same decode, same order
-    else:
-        # the GEMV walks the planes in groups of 8 rows: another f32 summation order
-        np.testing.assert_allclose(got_p, got_r, rtol=0, atol=1e-5 * float(np.max(np.abs(got_r))))
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
-    err = float(np.max(np.abs(got_p - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
+    scale = max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2)))
+    err = float(np.max(np.abs(got_p - want)) / scale)
     assert err <= 2e-3, err
+    # the GEMVs differ: the planes' kernel sums f32 products, the raw rows'
+    # one-launch kernel dots f16 (a d) pairs, so each meets the oracle's bar
+    err_r = float(np.max(np.abs(got_r - want)) / scale)
+    assert err_r <= 2e-3, err_r
 
 
 @pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200), (3, 37, 72),
@@ -150,7 +152,8 @@ def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
 
 def test_matmul_q4_1_prepacked_config4_kn():
     """Config 4 with the [K][N/32] weight prepacked: M=1 in full, M=512 on
-    sampled rows, each equal to the raw weight's result."""
+    sampled rows; at M=512 equal to the raw weight's result bit for bit, at
+    M=1 both within the Q4_1 bar of the oracle."""
     import torch
     announce("prepack q4_1 config4")
     K, N = 4096, 14336
@@ -165,19 +168,21 @@ def test_matmul_q4_1_prepacked_config4_kn():
         got_r = run(op, at, wt, torch.float32, (M, N))
         if M > 2:
             np.testing.assert_array_equal(got_p, got_r)
-        else:
-            np.testing.assert_allclose(got_p, got_r, rtol=0, atol=1e-5 * float(np.max(np.abs(got_r))))
         want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
-        g, w = got_p[rows[0]:rows[1]], want[rows[0]:rows[1]]
-        err = float(np.max(np.abs(g - w)) / max(np.max(np.abs(w)), np.sqrt(np.mean(w ** 2))))
-        assert err <= 2e-3, err
+        w = want[rows[0]:rows[1]]
+        scale = max(np.max(np.abs(w)), np.sqrt(np.mean(w ** 2)))
+        # at M <= 2 the two GEMVs round differently (see above): each within the bar
+        for got in (got_p, got_r):
+            err = float(np.max(np.abs(got[rows[0]:rows[1]] - w)) / scale)
+            assert err <= 2e-3, err
 
 
 @pytest.mark.parametrize("M", [2, 40])
 def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
     """f16 A -> f16 C (nnops: the output follows A) through the packed
-    planes, equal to the raw weight's result on the GEMV (M=2) and ring
-    (M=40) routes; and a batched A [2, M, K] against the one packed weight."""
+    planes, equal to the raw weight's result on the ring (M=40) route and,
+    like it, within the Q4_1 bar on the GEMV (M=2) route; and a batched A
+    [2, M, K] against the one packed weight."""
     import torch
     announce(f"prepack q4_1 f16 out / batched M={M}")
     K, N = 1024, 512
@@ -191,13 +196,13 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
     got_r = run(op, at, wt, torch.float16, (2, M, N))
     if M > 2:
         np.testing.assert_array_equal(got_p.view(np.uint16), got_r.view(np.uint16))
-    else:
-        np.testing.assert_allclose(got_p.astype(np.float32), got_r.astype(np.float32), rtol=2e-3, atol=1e-3)
     for bi in range(2):
         want = oracle.gemm_q4_1(a[bi], blk, N, trans_b=False, w_round_f16=True, c_f16=True).astype(np.float32)
-        g = got_p[bi].astype(np.float32)
-        err = float(np.max(np.abs(g - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
-        assert err <= 2e-3, err
+        scale = max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2)))
+        # at M = 2 the two GEMVs round differently: each within the bar
+        for got in (got_p, got_r):
+            err = float(np.max(np.abs(got[bi].astype(np.float32) - want)) / scale)
+            assert err <= 2e-3, err
 
 
 @pytest.mark.parametrize("K,N", [(64, 200), (96, 1024), (37, 72)])

@@ -104,3 +104,46 @@ def test_config4_kn_m512():
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
     err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_config4_kn_gemv_full(M):
+    """Config 4's literal [K][N/32] weight at M = 1 and 2, every output
+    checked: the one-launch GEMV whose K splits meet in the last-arriving
+    workgroup of each column group."""
+    announce(f"config4 kn gemv M={M}")
+    K, N = 4096, 14336
+    a = dg.normal(700 + M, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(702, K, N)
+    got = run_gpu(a, blk, N, trans_b=False)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
+    err = norm_err(got, want)
+    print(f"config4 kn gemv M={M}: normalized error {err:.3e}")
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 3000), (2, 96, 1056), (1, 4160, 512)])
+def test_kn_gemv_padded_rows_and_repeat(M, K, N):
+    """Blocks along N with a padded row pitch (16-byte multiple, wider than the
+    blocks) and a last, narrower column group; a second call on the same
+    workspace (counters left by the first) gives the same bits."""
+    import torch
+    announce(f"q4_1 kn padded {M}x{K}x{N}")
+    a = dg.normal(710 + K, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(711 + N, K, N)
+    row = blk.shape[1]
+    pitch = (row + 16 + 15) // 16 * 16
+    padded = np.full((K, pitch), 0xA5, dtype=np.uint8)
+    padded[:, :row] = blk
+    bp = dev(padded)
+    ad = dev(a)
+    ws = torch.empty(8 << 20, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+        na.gemm_q4_1(ad, bp, c, n=N, trans_b=False, ldb_bytes=pitch, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(host(c))
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
+    assert norm_err(outs[0].astype(np.float32), want) <= TOL
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
