@@ -226,6 +226,45 @@ size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* args);
 int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* args, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Output pass of the fp x q4_1 routes over the GEMM's f32 results:
+ * bias, the residual (add_to) and the epilogue (clip, activation), and the
+ * gated combine of Linear's gated form. Replaces the fp epilogue of nnops'
+ * FpRoute / matmul_qblock_fused output (apply_epilogue,
+ * src/backend/cpu/simd_kernel/simd_epilogue.hpp:56-90; Linear's residual
+ * order, src/backend/cpu/matmul/linear.cpp:276-301) and linear_gated_impl +
+ * gated_combine_act (src/backend/cpu/matmul/linear.cpp:84-170, the combine
+ * of src/backend/cpu/common/gate_combine.hpp:47-85).
+ *   not gated:  f = src[r][c] + bias[c] (+ old if residual_pre);
+ *               f = act(clip(f)); out = f (+ old, after the output type's
+ *               rounding of f, if add_to and not residual_pre)
+ *   gated:      src holds 2n columns, gate [0, n) and value [n, 2n):
+ *               g = T(src[r][c] + bias[c]), v = T(src[r][n + c] + bias[n + c])
+ *               (T the output type: the reference's GEMM tile is of X's
+ *               type), both clamped to +-gate_limit when finite;
+ *               y = act(clip(gate_act(g) * (v + gate_beta))), out = y (+ old
+ *               if add_to, after y's rounding to the output type); gate_act:
+ *               Silu g / (1 + exp(-gate_alpha g)), Gelu
+ *               (tanh form), Relu, Sigmoid, Tanh, None.
+ * bias is in the output's type (f32 or f16), or NULL. Stream-ordered, no
+ * allocation. */
+typedef struct NnopsFpOutArgs {
+    const float* src;           /* [rows][ld_src] f32 */
+    int64_t ld_src;             /* elements */
+    void* out;                  /* [rows][ld_out] f32 or f16 (out_f16) */
+    int64_t ld_out;             /* elements */
+    int64_t rows, n;            /* output columns n (gated: src has 2n) */
+    int32_t out_f16;
+    const void* bias;           /* [n], gated [2n], or NULL */
+    int32_t act;                /* NNOPS_ACT_* */
+    float act_alpha, act_beta, min_clip, max_clip;
+    int32_t add_to, residual_pre;
+    int32_t gated;
+    int32_t gate_act;           /* NNOPS_ACT_NONE/RELU/GELU/SIGMOID/TANH/SILU */
+    float gate_alpha, gate_beta, gate_limit;
+} NnopsFpOutArgs;
+
+int nnops_hip_fp_output_pass(const NnopsFpOutArgs* args, void* stream);
+
 /* QuantizeLinear / DequantizeLinear over a rows x cols view (row strides in
  * elements), and the activation quantization of the fp-activation int8 MatMul.
  * Replaces nnops' quantize_linear_impl / dequantize_linear_impl

@@ -76,6 +76,11 @@ typedef struct NnopsLinearAttrs {
     int32_t gated;
     int32_t requant_round_even;  /* extension */
     int32_t float_epilogue;      /* extension */
+    /* the gated form (LinearAttributes::gate_*, include/nnops/ops/linear.hpp:
+       71-88): gate activation (NNOPS_ACT_SILU default, GELU, RELU, SIGMOID,
+       TANH, NONE), alpha (Silu), beta, limit (+inf: no clamp) */
+    int32_t gate_activation;
+    float gate_alpha, gate_beta, gate_limit;
 } NnopsLinearAttrs;
 
 /* nnops::QuantLinearAttributes (include/nnops/ops/quant_linear.hpp:26-35) */

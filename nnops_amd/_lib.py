@@ -98,6 +98,19 @@ class LinearAttrs(C.Structure):
         ("add_to", C.c_int32), ("residual_pre_activation", C.c_int32),
         ("output_dtype", C.c_int32), ("gated", C.c_int32),
         ("requant_round_even", C.c_int32), ("float_epilogue", C.c_int32),
+        ("gate_activation", C.c_int32), ("gate_alpha", C.c_float), ("gate_beta", C.c_float),
+        ("gate_limit", C.c_float),
+    ]
+
+
+class FpOutArgs(C.Structure):
+    _fields_ = [
+        ("src", C.c_void_p), ("ld_src", C.c_int64), ("out", C.c_void_p), ("ld_out", C.c_int64),
+        ("rows", C.c_int64), ("n", C.c_int64), ("out_f16", C.c_int32), ("bias", C.c_void_p),
+        ("act", C.c_int32), ("act_alpha", C.c_float), ("act_beta", C.c_float),
+        ("min_clip", C.c_float), ("max_clip", C.c_float),
+        ("add_to", C.c_int32), ("residual_pre", C.c_int32), ("gated", C.c_int32),
+        ("gate_act", C.c_int32), ("gate_alpha", C.c_float), ("gate_beta", C.c_float), ("gate_limit", C.c_float),
     ]
 
 
@@ -108,6 +121,7 @@ SIGNATURES = {
     "nnops_hip_gemm_i8_noalloc": (C.c_int, [C.POINTER(GemmI8Args), C.c_void_p]),
     "nnops_hip_gemm_q4_1_workspace_size": (C.c_size_t, [C.POINTER(GemmQ41Args)]),
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "nnops_hip_fp_output_pass": (C.c_int, [C.POINTER(FpOutArgs), C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
     "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
     "nnops_hip_prepack_q4_1_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),

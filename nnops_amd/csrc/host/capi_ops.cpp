@@ -107,6 +107,11 @@ void nnops_linear_attrs_init(NnopsLinearAttrs* a)
     *a = NnopsLinearAttrs{};
     a->output_dtype = static_cast<int32_t>(DataType::f32);
     init_epilogue(a->epilogue);
+    const LinearAttributes d;
+    a->gate_activation = static_cast<int32_t>(d.gate_activation);
+    a->gate_alpha = d.gate_alpha;
+    a->gate_beta = d.gate_beta;
+    a->gate_limit = d.gate_limit;
 }
 
 NnopsOp* nnops_matmul_create(const NnopsMatMulAttrs* a, int32_t backend)
@@ -140,6 +145,10 @@ NnopsOp* nnops_linear_create(const NnopsLinearAttrs* a, int32_t backend)
         attrs.gated = a->gated != 0;
         attrs.requant_round_even = a->requant_round_even != 0;
         attrs.float_epilogue = a->float_epilogue != 0;
+        attrs.gate_activation = static_cast<EpilogueActivateType>(a->gate_activation);
+        attrs.gate_alpha = a->gate_alpha;
+        attrs.gate_beta = a->gate_beta;
+        attrs.gate_limit = a->gate_limit;
     }
     auto* h = new NnopsOp;
     h->op = Linear::create(attrs, static_cast<Backend>(backend));

@@ -204,6 +204,15 @@ struct QuantCall {
     Epilogue ep{};
     bool add_to = false, residual_pre = false;
     bool round_even = false, float_ep = false;
+    bool bias = false;                  // a bias input is present
+    // Linear's gated form (the weight's 2N rows: gate, then value)
+    bool gated = false;
+    EpilogueActivateType gate_act = EpilogueActivateType::Silu;
+    float gate_alpha = 1.0f, gate_beta = 0.0f, gate_limit = std::numeric_limits<float>::infinity();
+
+    /// The fp x q4_1 route writes its f32 results to the workspace and runs
+    /// nnops_hip_fp_output_pass when there is anything after the GEMM.
+    bool q4_1_pass() const { return bias || add_to || gated || epilogue_is_active(ep); }
 };
 
 int32_t out_kind_of(DataType dt)
@@ -315,6 +324,13 @@ size_t fp_quant_prefix(const Geometry& g)
     return 2 * align_up(static_cast<size_t>(rows) * 4) + align_up(static_cast<size_t>(rows * g.k));
 }
 
+/// The f32 results of one batch matrix of the fp x q4_1 route, ahead of its
+/// output pass (0 when the GEMM writes the destination directly).
+size_t q4_1_pass_bytes(const Geometry& g, const QuantCall& q)
+{
+    return q.q4_1_pass() ? align_up(static_cast<size_t>(g.m) * static_cast<size_t>(g.n) * sizeof(float)) : 0;
+}
+
 size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDesc* out,
                        const QuantCall& q, DataType out_dtype)
 {
@@ -333,9 +349,9 @@ size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDes
     }
     if (is_q4_1_matmul(a.dtype, b.dtype)) {
         const DataType odt = out != nullptr ? out->dtype : a.dtype;
-        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, out_kind_of(odt));
+        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, q.q4_1_pass() ? NNOPS_OUT_F32 : out_kind_of(odt));
         x.a_f16 = a.dtype == DataType::f16;
-        return align_up(nnops_hip_gemm_q4_1_workspace_size(&x));
+        return q4_1_pass_bytes(g, q) + align_up(nnops_hip_gemm_q4_1_workspace_size(&x));
     }
     return 0;
 }
@@ -592,9 +608,11 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
     if (Status s = matmul_geometry(a.desc(), b.desc(), q.trans_a, q.trans_b, g); !is_ok(s)) {
         return s;
     }
-    // The destination must be [..., M, N] with the broadcast batch.
-    if (out.rank() < 2 || out.shape(out.rank() - 2) != g.m || out.shape(out.rank() - 1) != g.n ||
-        out.numel() != g.batch * g.m * g.n) {
+    // The destination must be [..., M, N] with the broadcast batch (the
+    // gated form: [..., M, N / 2]).
+    const int64_t n_dst = q.gated ? g.n / 2 : g.n;
+    if (out.rank() < 2 || out.shape(out.rank() - 2) != g.m || out.shape(out.rank() - 1) != n_dst ||
+        out.numel() != g.batch * g.m * n_dst) {
         return Status::invalid_argument;
     }
     if (g.m == 0 || g.n == 0 || g.batch == 0) {
@@ -612,27 +630,61 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
     }
 
     if (is_q4_1_matmul(a.data_type(), b.data_type())) {
-        if (g.trans_a || bias != nullptr || q.add_to || q.ep.type != EpilogueActivateType::None ||
-            epilogue_is_active(q.ep)) {
+        if (g.trans_a) {
             return Status::unsupported;
         }
         const int32_t ok = out_kind_of(out.data_type());
         if (ok != NNOPS_OUT_F32 && !(ok == NNOPS_OUT_F16 && a.data_type() == DataType::f16)) {
             return Status::unsupported;
         }
-        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, ok);
+        const bool pass = q.q4_1_pass();
+        const int64_t n_out = q.gated ? g.n / 2 : g.n;
+        if (pass) {
+            // the output pass reads the bias in the destination's type
+            if (bias != nullptr && (bias->data_type() != out.data_type() || bias->numel() < g.n)) {
+                return Status::invalid_argument;
+            }
+            if (q.gated && ((g.n % 2) != 0 || out.data_type() != a.data_type())) {
+                return Status::invalid_argument;
+            }
+        }
+        NnopsGemmQ41Args x = q41_args_from_geometry(g, q, pass ? NNOPS_OUT_F32 : ok);
         x.a_f16 = a.data_type() == DataType::f16;
         x.lda = a.row_stride_elems();
-        x.ldc = out.row_stride_elems();
+        x.ldc = pass ? g.n : out.row_stride_elems();
         if (g.b_packed) {
             x.b_dm = reinterpret_cast<const uint32_t*>(
                 b.ptr<const char>() + align_up(static_cast<size_t>((g.k + 7) / 8 * 8 * x.ldb_bytes)));
         } else {
             x.ldb_bytes = b.pitch();
         }
+        const size_t tmp = q4_1_pass_bytes(g, q);
         const size_t need = nnops_hip_gemm_q4_1_workspace_size(&x);
-        if (need > 0 && (workspace == nullptr || ws_bytes < need)) {
+        if ((need > 0 || tmp > 0) && (workspace == nullptr || ws_bytes < tmp + align_up(need))) {
             return Status::not_initialized;
+        }
+        char* gemm_ws = static_cast<char*>(workspace) + tmp;
+        NnopsFpOutArgs fo{};
+        if (pass) {
+            fo.src = static_cast<const float*>(workspace);
+            fo.ld_src = g.n;
+            fo.ld_out = out.row_stride_elems();
+            fo.rows = g.m;
+            fo.n = n_out;
+            fo.out_f16 = out.data_type() == DataType::f16;
+            fo.bias = bias != nullptr ? bias->ptr<const void>() : nullptr;
+            fo.act = static_cast<int32_t>(q.ep.type);
+            fo.act_alpha = q.ep.alpha;
+            fo.act_beta = q.ep.beta;
+            fo.min_clip = q.ep.min_clip;
+            fo.max_clip = q.ep.max_clip;
+            fo.add_to = q.add_to;
+            fo.residual_pre = q.residual_pre;
+            fo.gated = q.gated;
+            fo.gate_act = static_cast<int32_t>(q.gate_act);
+            fo.gate_alpha = q.gate_alpha;
+            fo.gate_beta = q.gate_beta;
+            fo.gate_limit = q.gate_limit;
         }
         const int64_t a_mat = a_rows_per * a.pitch();
         const int64_t b_mat = b_rows_per * b.pitch();
@@ -641,10 +693,17 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             NnopsGemmQ41Args xb = x;
             xb.a = a.ptr<const char>() + batch_offset(bi, g, g.a_batch, a_mat);
             xb.b = reinterpret_cast<const uint8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
-            xb.c = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
-            const int rc = nnops_hip_gemm_q4_1(&xb, workspace, need, stream);
+            char* cb = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
+            xb.c = pass ? workspace : static_cast<void*>(cb);
+            const int rc = nnops_hip_gemm_q4_1(&xb, gemm_ws, need, stream);
             if (rc != NNOPS_OK) {
                 return from_code(rc);
+            }
+            if (pass) {
+                fo.out = cb;
+                if (const int rp = nnops_hip_fp_output_pass(&fo, stream); rp != NNOPS_OK) {
+                    return from_code(rp);
+                }
             }
         }
         return Status::ok;
@@ -716,15 +775,31 @@ Status MatMul::validate(std::span<const TensorDesc> inputs, std::span<const Tens
     return matmul_geometry(inputs[0], inputs[1], attrs_.transpose_a, attrs_.transpose_b, g);
 }
 
+namespace {
+
+QuantCall matmul_call(const MatMulAttributes& attrs, bool bias)
+{
+    QuantCall q;
+    q.trans_a = attrs.transpose_a;
+    q.trans_b = attrs.transpose_b;
+    q.ep = attrs.epilogue;
+    q.residual_pre = attrs.residual_pre_activation;
+    q.add_to = attrs.residual_pre_activation;  // MatMul's residual is the pre-activation fold
+    q.round_even = attrs.requant_round_even;
+    q.float_ep = attrs.float_epilogue;
+    q.bias = bias;
+    return q;
+}
+
+}  // namespace
+
 size_t MatMul::getWorkspaceSize(std::span<const TensorDesc> inputs,
                                 std::span<const TensorDesc> outputs) const
 {
     if (inputs.size() < 2) {
         return 0;
     }
-    QuantCall q;
-    q.trans_a = attrs_.transpose_a;
-    q.trans_b = attrs_.transpose_b;
+    const QuantCall q = matmul_call(attrs_, inputs.size() > 2);
     const DataType odt = !outputs.empty() ? outputs[0].dtype : attrs_.output_dtype;
     return quant_workspace(inputs[0], inputs[1], outputs.empty() ? nullptr : &outputs[0], q, odt);
 }
@@ -750,14 +825,7 @@ Status MatMul::compute(std::span<TensorView> outputs, std::span<const TensorView
         outputs[0].data_type() != attrs_.output_dtype) {
         return Status::invalid_argument;
     }
-    QuantCall q;
-    q.trans_a = attrs_.transpose_a;
-    q.trans_b = attrs_.transpose_b;
-    q.ep = attrs_.epilogue;
-    q.residual_pre = attrs_.residual_pre_activation;
-    q.add_to = attrs_.residual_pre_activation;  // MatMul's residual is the pre-activation fold
-    q.round_even = attrs_.requant_round_even;
-    q.float_ep = attrs_.float_epilogue;
+    const QuantCall q = matmul_call(attrs_, inputs.size() > 2);
     const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),
                                        std::span<const TensorDesc>(&desc_out, 1));
     return run_quant(q, outputs[0], inputs, ctx, workspace, workspace != nullptr ? ws : 0,
@@ -802,6 +870,29 @@ DataType linear_out_dtype(const LinearAttributes& attrs, DataType x, DataType w)
     return x;
 }
 
+/// Linear's call: the residual folds into the GEMM in the pre-activation
+/// order, and an identity epilogue folds either way
+/// (src/backend/cpu/matmul/linear.cpp:276-282); the gated form's combine adds
+/// it after its own epilogue.
+QuantCall linear_call(const LinearAttributes& attrs, bool bias)
+{
+    QuantCall q;
+    q.trans_b = true;
+    q.ep = attrs.epilogue;
+    q.add_to = attrs.add_to;
+    q.residual_pre = attrs.add_to && !attrs.gated &&
+                     (attrs.residual_pre_activation || !epilogue_is_active(attrs.epilogue));
+    q.round_even = attrs.requant_round_even;
+    q.float_ep = attrs.float_epilogue;
+    q.bias = bias;
+    q.gated = attrs.gated;
+    q.gate_act = attrs.gate_activation;
+    q.gate_alpha = attrs.gate_alpha;
+    q.gate_beta = attrs.gate_beta;
+    q.gate_limit = attrs.gate_limit;
+    return q;
+}
+
 }  // namespace
 
 std::vector<TensorDesc> Linear::getOutputTensorDesc(std::span<const TensorDesc> inputs) const
@@ -811,7 +902,7 @@ std::vector<TensorDesc> Linear::getOutputTensorDesc(std::span<const TensorDesc> 
         return {};
     }
     TensorDesc d = inputs[0];
-    d.dims[static_cast<size_t>(d.rank - 1)] = w.dims[0];
+    d.dims[static_cast<size_t>(d.rank - 1)] = attrs_.gated ? w.dims[0] / 2 : w.dims[0];
     d.dtype = linear_out_dtype(attrs_, inputs[0].dtype, w.dtype);
     d.row_stride_elems = 0;
     return {d};
@@ -822,12 +913,45 @@ Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const Tens
     if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
         return Status::invalid_argument;
     }
-    if (attrs_.gated) {
-        return Status::unsupported;
-    }
     TensorDesc x2, w;
     if (!linear_descs(inputs, x2, w)) {
         return Status::invalid_argument;
+    }
+    if (attrs_.gated) {
+        // nnops' gated form (src/ops/linear.cpp:63-107): Silu / Gelu / Relu /
+        // Sigmoid / Tanh / None, no pre-activation residual, W [2N, K], bias
+        // [2N] of X's type, output [..., N]. Here over a q4_1 weight (blocks
+        // along K, the Linear form): nnops runs the gated form for fp
+        // weights of X's type only, which this library has no GEMM for.
+        if (attrs_.add_to && attrs_.residual_pre_activation) {
+            return Status::unsupported;
+        }
+        switch (attrs_.gate_activation) {
+        case EpilogueActivateType::Silu:
+        case EpilogueActivateType::Gelu:
+        case EpilogueActivateType::Relu:
+        case EpilogueActivateType::Sigmoid:
+        case EpilogueActivateType::Tanh:
+        case EpilogueActivateType::None:
+            break;
+        default:
+            return Status::unsupported;
+        }
+        if ((x2.dtype != DataType::f32 && x2.dtype != DataType::f16) || w.dtype != DataType::q4_1 ||
+            w.layout != TensorLayout::Dense) {
+            return Status::unsupported;
+        }
+        if (w.dims[0] <= 0 || (w.dims[0] % 2) != 0) {
+            return Status::invalid_argument;
+        }
+        if (inputs.size() > 2 && (inputs[2].dtype != x2.dtype || inputs[2].numel() != w.dims[0])) {
+            return Status::invalid_argument;
+        }
+        if (!outputs.empty() && outputs[0].rank >= 1 &&
+            (outputs[0].dims[static_cast<size_t>(outputs[0].rank - 1)] != w.dims[0] / 2 ||
+             outputs[0].dtype != x2.dtype)) {
+            return Status::invalid_argument;
+        }
     }
     if (w.layout == TensorLayout::PackedBHip) {
         // [N, K] with a pitch covering the blob (prepack_s8)
@@ -852,14 +976,13 @@ size_t Linear::getWorkspaceSize(std::span<const TensorDesc> inputs,
     if (!linear_descs(inputs, x2, w)) {
         return 0;
     }
-    QuantCall q;
-    q.trans_b = true;
+    const QuantCall q = linear_call(attrs_, inputs.size() > 2);
     const DataType odt = !outputs.empty() ? outputs[0].dtype
                                           : linear_out_dtype(attrs_, x2.dtype, w.dtype);
     TensorDesc o;
     o.rank = 2;
     o.dims[0] = x2.dims[0];
-    o.dims[1] = w.dims[0];
+    o.dims[1] = attrs_.gated ? w.dims[0] / 2 : w.dims[0];
     o.dtype = odt;
     return quant_workspace(x2, w, &o, q, odt);
 }
@@ -893,11 +1016,12 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
     }
     // Flatten the leading dims: [..., K] -> [rows, K], [..., N] -> [rows, N].
     const int64_t rows = x.total_rows();
-    if (y.total_rows() != rows || y.shape(y.rank() - 1) != wv.shape(0)) {
+    const int64_t n_out = attrs_.gated ? wv.shape(0) / 2 : wv.shape(0);
+    if (y.total_rows() != rows || y.shape(y.rank() - 1) != n_out) {
         return Status::invalid_argument;
     }
     const int64_t xs[2] = {rows, x.shape(x.rank() - 1)};
-    const int64_t ys[2] = {rows, wv.shape(0)};
+    const int64_t ys[2] = {rows, n_out};
     const int64_t x_pitch = x.rank() >= 2 ? x.pitch()
                                           : static_cast<int64_t>(data_type_row_bytes(x.data_type(), xs[1]));
     const int64_t y_pitch = y.rank() >= 2 ? y.pitch()
@@ -906,15 +1030,7 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
     TensorView y2(ys, y.data_type(), y.ptr<void>(), y_pitch, TensorLayout::Dense, y.quant_params());
     TensorView ins[3] = {x2, wv, inputs.size() > 2 ? inputs[2] : TensorView{}};
 
-    QuantCall q;
-    q.trans_b = true;
-    q.ep = attrs_.epilogue;
-    q.add_to = attrs_.add_to;
-    // the pre-activation order folds into the GEMM, and an identity epilogue
-    // folds either way (src/backend/cpu/matmul/linear.cpp:276-282)
-    q.residual_pre = attrs_.add_to && (attrs_.residual_pre_activation || !epilogue_is_active(attrs_.epilogue));
-    q.round_even = attrs_.requant_round_even;
-    q.float_ep = attrs_.float_epilogue;
+    const QuantCall q = linear_call(attrs_, inputs.size() > 2);
     const size_t ws = getWorkspaceSize(std::span<const TensorDesc>(descs_in, inputs.size()),
                                        std::span<const TensorDesc>(&desc_out, 1));
     return run_quant(q, y2, std::span<const TensorView>(ins, inputs.size()), ctx, workspace,

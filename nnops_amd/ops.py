@@ -212,9 +212,13 @@ class Linear(_Op):
     def __init__(self, *, output_dtype=L.DT_F32, act=None, min_clip=-math.inf, max_clip=math.inf,
                  add_to=False, residual_pre_activation=False, quant=L.EQ_NONE, quant_scales=None,
                  quant_zero_points=None, quant_param_count=0, requant_round_even=False,
-                 float_epilogue=False, gated=False, act_alpha=0.0, act_beta=1.0, backend=L.BACKEND_HIP):
+                 float_epilogue=False, gated=False, gate_activation=None, gate_alpha=1.0, gate_beta=0.0,
+                 gate_limit=math.inf, act_alpha=0.0, act_beta=1.0, backend=L.BACKEND_HIP):
         a = L.LinearAttrs()
         L.lib().nnops_linear_attrs_init(C.byref(a))
+        if gate_activation is not None:
+            a.gate_activation = gate_activation
+        a.gate_alpha, a.gate_beta, a.gate_limit = gate_alpha, gate_beta, gate_limit
         a.output_dtype = output_dtype
         a.add_to = int(add_to)
         a.residual_pre_activation = int(residual_pre_activation)

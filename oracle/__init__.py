@@ -49,6 +49,17 @@ class GemmQ41(C.Structure):
     ]
 
 
+class FpOut(C.Structure):
+    _fields_ = [
+        ("src", C.c_void_p), ("ld_src", C.c_int64), ("out", C.c_void_p), ("ld_out", C.c_int64),
+        ("rows", C.c_int64), ("n", C.c_int64), ("out_f16", C.c_int32), ("bias", C.c_void_p),
+        ("act", C.c_int32), ("act_alpha", C.c_float), ("act_beta", C.c_float),
+        ("min_clip", C.c_float), ("max_clip", C.c_float),
+        ("add_to", C.c_int32), ("residual_pre", C.c_int32), ("gated", C.c_int32), ("gate_act", C.c_int32),
+        ("gate_alpha", C.c_float), ("gate_beta", C.c_float), ("gate_limit", C.c_float),
+    ]
+
+
 _lib = None
 _ref = None
 
@@ -74,6 +85,7 @@ def lib():
         _lib.orc_f32_to_f16.restype = C.c_uint16
         _lib.orc_f16_to_f32.argtypes = [C.c_uint16]
         _lib.orc_f16_to_f32.restype = C.c_float
+        _lib.orc_fp_out_pass.argtypes = [C.POINTER(FpOut)]
         _lib.orc_q4_1_decode.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
         _lib.orc_q4_1_quantize.argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
         _lib.orc_quantize_linear.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64,
@@ -146,6 +158,11 @@ def cpu_lib():
         _cpu.ref_cpu_matmul_q4_1.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
                                              C.c_int, C.c_int]
         _cpu.ref_cpu_matmul_q4_1.restype = C.c_int
+        _cpu.ref_cpu_linear_q4_1.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                             C.c_int64, C.c_int64, C.c_int, C.c_float, C.c_float, C.c_float,
+                                             C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+                                             C.c_float, C.c_int]
+        _cpu.ref_cpu_linear_q4_1.restype = C.c_int
     return _cpu
 
 
@@ -244,6 +261,43 @@ def gemm_q4_1(a, blocks, n, *, trans_b=True, ldb_bytes=None, c_f16=False,
     p.m_begin, p.m_end = (rows if rows is not None else (0, 0))
     lib().orc_gemm_q4_1(C.byref(p))
     return c
+
+
+def fp_out_pass(src, n, *, out=None, out_f16=False, bias=None, act=ACT_NONE, act_alpha=0.0, act_beta=1.0,
+                min_clip=-np.inf, max_clip=np.inf, add_to=False, residual_pre=False, gated=False,
+                gate_act=ACT_SILU, gate_alpha=1.0, gate_beta=0.0, gate_limit=np.inf):
+    """The fp output pass over f32 GEMM results ``src`` [rows, n] (gated:
+    [rows, 2n]); ``out`` holds the residual when add_to (f32 or f16, as
+    out_f16); ``bias`` in the output's type. Returns the output."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    rows = src.shape[0]
+    odt = np.float16 if out_f16 else np.float32
+    o = np.zeros((rows, n), dtype=odt) if out is None else np.ascontiguousarray(out, dtype=odt).copy()
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=odt)
+    p = FpOut()
+    p.src, p.ld_src, p.out, p.ld_out = src.ctypes.data, src.shape[1], o.ctypes.data, n
+    p.rows, p.n, p.out_f16 = rows, n, int(out_f16)
+    p.bias = None if b is None else b.ctypes.data
+    p.act, p.act_alpha, p.act_beta, p.min_clip, p.max_clip = act, act_alpha, act_beta, min_clip, max_clip
+    p.add_to, p.residual_pre, p.gated, p.gate_act = int(add_to), int(residual_pre), int(gated), gate_act
+    p.gate_alpha, p.gate_beta, p.gate_limit = gate_alpha, gate_beta, gate_limit
+    lib().orc_fp_out_pass(C.byref(p))
+    return o
+
+
+def q4_1_linear(a, blocks, n_w, rows=None, w_round_f16=False, **pass_kw):
+    """Linear over a Q4_1 weight [n_w, K] (blocks along K): the f32 dequant
+    GEMM (f64 accumulation) and then the fp output pass (``pass_kw`` as
+    fp_out_pass; gated: n_w = 2n). ``rows`` = (begin, end): only those rows
+    of X (the result has end - begin rows). ``w_round_f16``: the weight decoded
+    to f16 first (nnops' packed route for an f16 X past the small-M route)."""
+    acc = gemm_q4_1(a, blocks, n_w, trans_b=True, rows=rows, w_round_f16=w_round_f16)
+    if rows is not None:
+        acc = acc[rows[0]:rows[1]]
+        if pass_kw.get("out") is not None:
+            pass_kw["out"] = pass_kw["out"][rows[0]:rows[1]]
+    n = n_w // 2 if pass_kw.get("gated") else n_w
+    return fp_out_pass(acc, n, **pass_kw)
 
 
 def q4_1_decode(blocks, count):

@@ -449,6 +449,75 @@ void orc_gemm_q4_1(const orc_gemm_q4_1_t* p)
 }
 
 /* ---------------------------------------------------------------------------
+ * The fp output pass of the fp x q4_1 routes.
+ *  - not gated: Linear / MatMul's fp epilogue order: bias, the pre-activation
+ *    residual, clamp and activation (apply_epilogue, simd_epilogue.hpp:56-90),
+ *    then the post-activation residual added to the destination-typed result
+ *    (src/backend/cpu/matmul/linear.cpp:276-301: a compact temporary, then
+ *    residual_add at :181-196);
+ *  - gated: linear_gated_impl (linear.cpp:116-170): the GEMM with bias into a
+ *    [rows, 2n] tile of the destination's type, then gated_combine_act
+ *    (linear.cpp:84-114): act(gate) * (value + beta) with both halves clamped
+ *    to +-limit when finite, Linear's epilogue, add_to accumulating onto the
+ *    destination (tiled_map_simd's s_store_add, simd_kernel/tiled_map.hpp:
+ *    40-66); the gate activation is gate_act_scalar (common/gate_combine.hpp:
+ *    70-85).
+ * ------------------------------------------------------------------------- */
+static float gate_act_scalar(int32_t act, float g, float alpha)
+{
+    switch (act) {
+    case ORC_ACT_SILU: return g / (1.0f + expf(-alpha * g));
+    case ORC_ACT_GELU: return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+    case ORC_ACT_RELU: return g > 0.0f ? g : 0.0f;
+    case ORC_ACT_SIGMOID: return 1.0f / (1.0f + expf(-g));
+    case ORC_ACT_TANH: return tanhf(g);
+    default: return g;
+    }
+}
+
+static float fp_round(int32_t f16, float x)
+{
+    return f16 ? orc_f16_to_f32(orc_f32_to_f16(x)) : x;
+}
+
+static float fp_load(int32_t f16, const void* base, int64_t i)
+{
+    return f16 ? orc_f16_to_f32(((const uint16_t*)base)[i]) : ((const float*)base)[i];
+}
+
+void orc_fp_out_pass(const orc_fp_out_t* p)
+{
+    for (int64_t r = 0; r < p->rows; ++r) {
+        for (int64_t c = 0; c < p->n; ++c) {
+            const int64_t oi = r * p->ld_out + c;
+            const float old = p->add_to ? fp_load(p->out_f16, p->out, oi) : 0.0f;
+            const float bg = p->bias ? fp_load(p->out_f16, p->bias, c) : 0.0f;
+            float y;
+            if (p->gated) {
+                const float bv = p->bias ? fp_load(p->out_f16, p->bias, p->n + c) : 0.0f;
+                float g = fp_round(p->out_f16, p->src[r * p->ld_src + c] + bg);
+                float v = fp_round(p->out_f16, p->src[r * p->ld_src + p->n + c] + bv);
+                if (isfinite(p->gate_limit)) {
+                    g = fmaxf(fminf(g, p->gate_limit), -p->gate_limit);
+                    v = fmaxf(fminf(v, p->gate_limit), -p->gate_limit);
+                }
+                y = apply_act_fp(p->act, gate_act_scalar(p->gate_act, g, p->gate_alpha) * (v + p->gate_beta),
+                                 p->min_clip, p->max_clip, p->act_alpha, p->act_beta);
+                /* the combined value is of the destination's type before it accumulates */
+                if (p->add_to) y = old + fp_round(p->out_f16, y);
+            } else {
+                y = p->src[r * p->ld_src + c] + bg;
+                if (p->add_to && p->residual_pre) y = y + old;
+                y = apply_act_fp(p->act, y, p->min_clip, p->max_clip, p->act_alpha, p->act_beta);
+                if (p->add_to && !p->residual_pre) y = fp_round(p->out_f16, y) + old;
+            }
+            if (p->out_f16) ((uint16_t*)p->out)[oi] = orc_f32_to_f16(y);
+            else ((float*)p->out)[oi] = y;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------
  * Seeded inputs: the xorshift128+ generator seeded through splitmix64 that the
  * reference's tests use (tests/common/random_tensor.hpp:18-57), so a seed names
  * the same data here as there.

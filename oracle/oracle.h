@@ -104,6 +104,24 @@ typedef struct {
 
 void orc_gemm_q4_1(const orc_gemm_q4_1_t* p);
 
+/* The fp output pass after a Q4_1 GEMM (f32 results src [rows][ld_src]):
+ * bias, residual and epilogue, or Linear's gated combine. See orc_fp_out_pass
+ * in oracle.c for the references it follows. */
+typedef struct {
+    const float* src;
+    int64_t ld_src;
+    void* out;            /* f32 or f16 (out_f16) [rows][ld_out] */
+    int64_t ld_out, rows, n;
+    int32_t out_f16;
+    const void* bias;     /* out's type, [n] or gated [2n], or NULL */
+    int32_t act;
+    float act_alpha, act_beta, min_clip, max_clip;
+    int32_t add_to, residual_pre, gated, gate_act;
+    float gate_alpha, gate_beta, gate_limit;
+} orc_fp_out_t;
+
+void orc_fp_out_pass(const orc_fp_out_t* p);
+
 /* QuantizeLinear / DequantizeLinear over `count` flat elements; element i
  * uses parameter (i / inner) % dim; `segment` is the reference kernel's row
  * length (numel per tensor, cols per token, inner per channel). */

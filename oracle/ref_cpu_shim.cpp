@@ -7,6 +7,7 @@
 //   nnops::MatMul::create / compute   include/nnops/ops/matmul.hpp:88-135
 // with a ComputeContext whose CpuBackend hooks (include/nnops/core/
 // parallel_for.hpp:60-110) run on a small std::thread pool defined below.
+#include "nnops/ops/linear.hpp"
 #include "nnops/ops/matmul.hpp"
 
 #include <atomic>
@@ -19,6 +20,12 @@
 #include <vector>
 
 using namespace nnops;
+
+namespace nnops::backend::cpu {
+// the CPU backend's Linear (src/backend/cpu/matmul/linear.cpp:199)
+Status linear_cpu(const LinearAttributes& attrs, TensorView& output, std::span<const TensorView> inputs,
+                  const ComputeContext& ctx, void* workspace);
+}  // namespace nnops::backend::cpu
 
 namespace {
 
@@ -202,6 +209,46 @@ int ref_cpu_matmul_q4_1(const uint16_t* a, const uint8_t* w, uint16_t* c, int64_
     const TensorView ins[] = {av, wv};
     TensorView outs[] = {cv};
     const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 2), ctx);
+    return static_cast<int>(st);
+}
+
+// nnops' Linear over a q4_1 weight [N2, K] (blocks along K): f32 / f16 X
+// [M, K] (x_f16), bias of X's type [N2] or NULL, output C of X's type [M, N]
+// (N = N2 / 2 when gated, else N2; its current contents are the residual when
+// add_to). Calls the CPU backend's linear_cpu (src/backend/cpu/matmul/
+// linear.cpp:199-309) directly: the operator's validate admits the gated form
+// for fp weights of X's type only (src/ops/linear.cpp:92), and this is the
+// reference's own combine over the q4_1 GEMM for the HIP extension's parity.
+int ref_cpu_linear_q4_1(const void* x, int x_f16, const uint8_t* w, const void* bias, void* c, int64_t M,
+                        int64_t N2, int64_t K, int act, float act_alpha, float act_beta, float min_clip,
+                        float max_clip, int add_to, int residual_pre, int gated, int gate_act, float gate_alpha,
+                        float gate_beta, float gate_limit, int threads)
+{
+    Pool* p = pool_of(threads);
+    const DataType dt = x_f16 ? DataType::f16 : DataType::f32;
+    const int64_t N = gated ? N2 / 2 : N2;
+    const int64_t xshape[] = {M, K}, wshape[] = {N2, K}, bshape[] = {N2}, cshape[] = {M, N};
+    TensorView xv(xshape, dt, const_cast<void*>(x));
+    TensorView wv(wshape, DataType::q4_1, const_cast<uint8_t*>(w));
+    TensorView bv(bshape, dt, const_cast<void*>(bias));
+    TensorView cv(cshape, dt, c);
+    LinearAttributes attrs{};
+    attrs.epilogue.type = static_cast<EpilogueActivateType>(act);
+    attrs.epilogue.alpha = act_alpha;
+    attrs.epilogue.beta = act_beta;
+    attrs.epilogue.min_clip = min_clip;
+    attrs.epilogue.max_clip = max_clip;
+    attrs.add_to = add_to != 0;
+    attrs.residual_pre_activation = residual_pre != 0;
+    attrs.gated = gated != 0;
+    attrs.gate_activation = static_cast<EpilogueActivateType>(gate_act);
+    attrs.gate_alpha = gate_alpha;
+    attrs.gate_beta = gate_beta;
+    attrs.gate_limit = gate_limit;
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {xv, wv, bv};
+    const Status st = backend::cpu::linear_cpu(attrs, cv, std::span<const TensorView>(ins, bias ? 3 : 2), ctx,
+                                               nullptr);
     return static_cast<int>(st);
 }
 

@@ -410,3 +410,99 @@ def test_oracle_q4_1_close_to_nnops_cpu_matmul(M, trans_b):
     rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
     err = np.abs(c.astype(np.float64) - want) / np.maximum(np.abs(want), rms)
     assert err.max() < 2e-3
+
+
+# ---------------------------------------------------------------------------
+# The fp x q4_1 output pass and Linear's gated combine, against nnops' own CPU
+# Linear (linear_cpu, built from the reference sources into oracle/_ref).
+# f32: the same operations in the same order, so only the GEMM's f32
+# summation and the vector exp / tanh differ (<= 2e-5 of the rms). f16 with
+# identity / Relu / clip: bit for bit (the vector body), except a non-gated
+# residual, whose f16 rounding sequence in nnops' fused small-M route is its
+# own (within 2 ulp). f16 with exp or tanh activations:
+# nnops evaluates them in f16 arithmetic, every operation rounded to f16
+# (the Silu gate below is reproduced bit for bit that way); the oracle and
+# the device evaluate in f32 and round once, within 4e-3 of the rms.
+# ---------------------------------------------------------------------------
+def _ref_linear_q4_1(a, blk, n2, bias=None, old=None, **kw):
+    M, K = a.shape
+    gated = kw.get("gated", False)
+    n = n2 // 2 if gated else n2
+    c = np.zeros((M, n), dtype=a.dtype) if old is None else old.astype(a.dtype).copy()
+    b = None if bias is None else np.ascontiguousarray(bias.astype(a.dtype))
+    rc = oracle.cpu_lib().ref_cpu_linear_q4_1(
+        a.ctypes.data, int(a.dtype == np.float16), blk.ctypes.data, None if b is None else b.ctypes.data,
+        c.ctypes.data, M, n2, K, kw.get("act", 0), kw.get("act_alpha", 0.0), kw.get("act_beta", 1.0),
+        kw.get("min_clip", -np.inf), kw.get("max_clip", np.inf), int(kw.get("add_to", False)),
+        int(kw.get("residual_pre", False)), int(gated), kw.get("gate_act", oracle.ACT_SILU),
+        kw.get("gate_alpha", 1.0), kw.get("gate_beta", 0.0), kw.get("gate_limit", np.inf), 4)
+    assert rc == 0, rc
+    return c
+
+
+GATED_CASES = [
+    dict(gated=True, gate_act=oracle.ACT_SILU),
+    dict(gated=True, gate_act=oracle.ACT_SILU, gate_alpha=1.702, gate_beta=1.0, gate_limit=7.0),
+    dict(gated=True, gate_act=oracle.ACT_GELU, gate_beta=0.5, gate_limit=1.5, act=oracle.ACT_RELU),
+    dict(gated=True, gate_act=oracle.ACT_SIGMOID, act=oracle.ACT_TANH),
+    dict(gated=True, gate_act=oracle.ACT_TANH, add_to=True),
+    dict(gated=True, gate_act=oracle.ACT_RELU, min_clip=-0.3, max_clip=0.4, add_to=True),
+    dict(gated=True, gate_act=oracle.ACT_NONE),
+]
+PASS_CASES = [
+    dict(act=oracle.ACT_GELU), dict(act=oracle.ACT_SILU, add_to=True), dict(act=oracle.ACT_RELU, min_clip=-0.5,
+                                                                            max_clip=0.7),
+    dict(act=oracle.ACT_SIGMOID, add_to=True, residual_pre=True), dict(act=oracle.ACT_NONE, add_to=True),
+    dict(act=oracle.ACT_TANH, add_to=True),
+]
+_EXACT_F16 = (oracle.ACT_NONE, oracle.ACT_RELU)
+
+
+@cpu_only
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("kw", GATED_CASES + PASS_CASES)
+def test_oracle_fp_out_pass_matches_nnops_linear(f16, kw):
+    dt = np.float16 if f16 else np.float32
+    M, K, N2 = 3, 256, 104          # 104 columns: vector body and scalar tail of the combine
+    gated = kw.get("gated", False)
+    n = N2 // 2 if gated else N2
+    a = dg.normal(11, (M, K)).astype(dt)
+    blk = dg.q4_1_blocks(12, N2, K)
+    bias = dg.normal(13, (N2,)).astype(dt)
+    old = dg.normal(14, (M, n)).astype(dt) if kw.get("add_to") else None
+    want = _ref_linear_q4_1(a, blk, N2, bias=bias, old=old, **kw).astype(np.float64)
+    okw = {k: v for k, v in kw.items() if k != "gated"}
+    if kw.get("add_to") and not gated:
+        # Linear folds the residual into the GEMM's pre-activation sum when the
+        # epilogue is the identity (src/backend/cpu/matmul/linear.cpp:276-282)
+        active = kw.get("act", 0) != 0 or np.isfinite(kw.get("min_clip", -np.inf)) or \
+            np.isfinite(kw.get("max_clip", np.inf))
+        okw["residual_pre"] = kw.get("residual_pre", False) or not active
+    got = oracle.q4_1_linear(a, blk, N2, gated=gated, out_f16=f16, bias=bias, out=old, **okw).astype(np.float64)
+    err = np.max(np.abs(want - got)) / np.sqrt(np.mean(want ** 2))
+    acts = {kw.get("act", oracle.ACT_NONE), kw.get("gate_act", oracle.ACT_NONE) if gated else oracle.ACT_NONE}
+    if not f16:
+        assert err <= 2e-5, err
+    elif acts <= set(_EXACT_F16) and (gated or not kw.get("add_to")):
+        # bit for bit over the combine's vector body; its scalar tail (the last
+        # n % 8 columns) adds the residual to the unrounded f32 value instead
+        n8 = n // 8 * 8
+        assert np.array_equal(want[:, :n8], got[:, :n8]), err
+        assert err <= 4e-3, err
+    else:
+        assert err <= 4e-3, err
+
+
+@cpu_only
+def test_nnops_gated_silu_f16_is_per_operation_f16():
+    """Why the f16 bar above is a tolerance: nnops' half combine rounds every
+    operation to f16 -- reproduced here bit for bit from the f32 GEMM."""
+    M, K, N2 = 3, 256, 96
+    a = dg.normal(1, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(2, N2, K)
+    want = _ref_linear_q4_1(a, blk, N2, gated=True, gate_act=oracle.ACT_SILU)
+    acc = oracle.gemm_q4_1(a, blk, N2, trans_b=True)
+    h = lambda x: np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+    g, v = h(acc[:, :48]), h(acc[:, 48:])
+    y = h(h(g * h(1.0 / h(1.0 + h(np.exp(-g))))) * v)
+    assert np.array_equal(want.astype(np.float32), y)
