@@ -37,8 +37,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg5", "copy", "ceilings",
-                                                           "vendor"])
+    p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg4_gemm", "cfg5",
+                                                           "gated_ffn", "copy", "ceilings", "vendor"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline of the headline config")
@@ -345,6 +345,39 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
         out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, 0, cpu_seconds,
                                        f"config 4 M={M} (weight {out['weight_layout']})")
     return out
+
+
+def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=4):
+    """Linear's gated form (SwiGLU) over a q4_1 [2N, K] weight (blocks along
+    K, the GGUF form) with bias, f16 X [M, K] -> f16 [M, N], through the
+    operator API: the Q4_1 GEMM / GEMV into the workspace and the combine.
+    M=1 rotates over nbuf weights (more than the MALL) so HBM is measured."""
+    x = torch.from_numpy(dg.normal(420 + M, (M, K)).astype("float16")).cuda()
+    nb = nbuf if M <= 2 else 1
+    ws_ = [torch.from_numpy(dg.q4_1_blocks(421 + i, 2 * N, K)).cuda() for i in range(nb)]
+    bias = torch.from_numpy((0.1 * dg.normal(425, (2 * N,))).astype("float16")).cuda()
+    y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    op = na.Linear(gated=True, gate_activation=na.EP_SILU)
+    ins = [[na.tensor(x), na.tensor(w, dtype=na.DT_Q4_1, shape=[2 * N, K]), na.tensor(bias)] for w in ws_]
+    outs = [na.tensor(y)]
+    wsn = op.workspace_size(ins[0], outs)
+    wsb = torch.empty(max(wsn, 1), dtype=torch.uint8, device="cuda")
+    s = stream.cuda_stream
+    it = [0]
+
+    def step():
+        rc = op.compute(outs, ins[it[0] % nb], stream=s, workspace=wsb)
+        it[0] += 1
+        if rc != 0:
+            raise RuntimeError(f"gated Linear failed: {rc}")
+    t = Timer(stream).time(step, steps, warmup)
+    wbytes = 2 * N * (K // 32) * 20
+    by = wbytes + M * K * 2 + M * N * 2 + 2 * N * 2
+    return {"us": t["mean_ms"] * 1e3, "gbs": by / (t["mean_ms"] * 1e-3) / 1e9,
+            "frac_hbm": by / (t["mean_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": by,
+            "tflops": 2.0 * M * 2 * N * K / (t["mean_ms"] * 1e-3) / 1e12,
+            "M": M, "K": K, "N": N, "weight_layout": "[2N][K/32 blocks] (gate rows, then value rows)",
+            "op": "Linear gated (SwiGLU) + bias, f16", "timing": t["timing"]}
 
 
 def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8):
@@ -699,6 +732,12 @@ def main():
         res = {"cfg1": lambda: cfg1_case(torch, dg, na, stream, args.steps, args.warmup, cs),
                "cfg3": lambda: gemv_i8_case(torch, dg, na, stream, args.steps, args.warmup, cpu_seconds=cs),
                "cfg4": lambda: gemv_q41_case(torch, dg, na, stream, args.steps, args.warmup, cpu_seconds=cs),
+               "cfg4_gemm": lambda: {"blocks_along_k": q41_gemm_case(torch, dg, na, stream, args.steps, args.warmup),
+                                     "blocks_along_n": q41_gemm_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                                     trans_b=False)},
+               "gated_ffn": lambda: {"m1": gated_ffn_case(torch, dg, na, stream, args.steps, args.warmup),
+                                     "m512": gated_ffn_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                            M=512)},
                "cfg5": lambda: cfg5_case(torch, dg, na, stream, args.steps, args.warmup)}[args.workload]()
         print(json.dumps({"workload": args.workload, **res}))
         return
@@ -725,6 +764,8 @@ def main():
                                                             cpu_seconds=cs)
         secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
         secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
+        secondary["gated_ffn_swiglu_m1"] = gated_ffn_case(torch, dg, na, stream, st, wu)
+        secondary["gated_ffn_swiglu_m512"] = gated_ffn_case(torch, dg, na, stream, few, wu, M=512)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, few, wu)
         secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, few, wu, dq_only=True)
         secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, few, wu)
