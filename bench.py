@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOPS
 PEAK_F16_TFLOPS = 2500.0     # dense f16
+PEAK_F32_TFLOPS = 157.3      # dense f32 MFMA
 PEAK_HBM_GBS = 8000.0        # HBM3E
 METRIC = "s8 GEMM TOPS @4096³; int8/Q4_1 GEMV GB/s @M=1; % of roofline"
 
@@ -346,10 +347,12 @@ def gemv_q41_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nb
     return out
 
 
-def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, trans_b=True, cpu_seconds=0.0):
+def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, trans_b=True, cpu_seconds=0.0,
+                  a_f32=False):
     """Config 4's GEMM; trans_b=False times the literal [K][N/32] layout
-    (blocks along N) instead of the GGUF/Linear [N][K/32] one."""
-    a_h = dg.normal(403, (M, K)).astype("float16")
+    (blocks along N) instead of the GGUF/Linear [N][K/32] one; a_f32 an f32
+    A (nnops computes that product in f32: the f32 MFMA GEMM)."""
+    a_h = dg.normal(403, (M, K)).astype("float32" if a_f32 else "float16")
     b_h = dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)
     a = torch.from_numpy(a_h).cuda()
     b = torch.from_numpy(b_h).cuda()
@@ -358,9 +361,14 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
     t = Timer(stream).time(lambda: na.gemm_q4_1(a, b, c, n=N, trans_b=trans_b, stream=s), steps, warmup)
     fl = 2.0 * M * N * K
     tf = fl / (t["mean_ms"] * 1e-3) / 1e12
-    out = {"tflops": tf, "frac_f16_mfma": tf / PEAK_F16_TFLOPS, "us": t["mean_ms"] * 1e3,
+    out = {"tflops": tf, "us": t["mean_ms"] * 1e3,
            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
            "timing": t["timing"]}
+    if a_f32:
+        out["a"] = "f32"
+        out["frac_f32_mfma"] = tf / PEAK_F32_TFLOPS
+    else:
+        out["frac_f16_mfma"] = tf / PEAK_F16_TFLOPS
     if cpu_seconds > 0:
         out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, 0, cpu_seconds,
                                        f"config 4 M={M} (weight {out['weight_layout']})")
@@ -782,6 +790,7 @@ def main():
                                                           cpu_seconds=cs)
         secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, few, wu, trans_b=False,
                                                             cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemm_m512_f32a"] = q41_gemm_case(torch, dg, na, stream, few, wu, a_f32=True)
         secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
         secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
         secondary["gated_ffn_swiglu_m1"] = gated_ffn_case(torch, dg, na, stream, st, wu)

@@ -1295,7 +1295,7 @@ __device__ __forceinline__ void decode_block_f16(const uint32_t raw[5], _Float16
     }
 }
 
-template <int BM, int BN, int WM, int WN, bool TRANS_B>
+template <int BM, int BN, int WM, int WN, bool TRANS_B, bool SOA = false>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
 {
     constexpr int T = WM * WN * 64;
@@ -1354,6 +1354,19 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
             } else {
                 const int kr = idx / (BN / 32), bn = (n0 >> 5) + idx % (BN / 32);
                 live = (k0 + kr) < p.k;
+                if constexpr (SOA) {
+                    // the prepacked planes: d|m from its plane, nibble dword d
+                    // of row r at (r / 8) * 8 ldb + 128 block + 32 d + 4 (r % 8)
+                    const int64_t r = min(k0 + kr, p.k - 1);
+                    const int64_t j = min(bn, nbn - 1);
+                    const uint8_t* q = p.b + (r >> 3) * 8 * p.ldb + j * 128 + 4 * (r & 7);
+                    rb[i][0] = live ? p.bdm[r * p.ldbdm + j] : 0u;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        rb[i][1 + d] = *reinterpret_cast<const uint32_t*>(q + 32 * d);
+                    }
+                    continue;
+                }
                 src = p.b + (int64_t)min(k0 + kr, p.k - 1) * p.ldb + (int64_t)min(bn, nbn - 1) * 20;
             }
             const v4i_a4 x = *reinterpret_cast<const v4i_a4*>(src);
@@ -1454,6 +1467,174 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.m) {
+                    store_out(p, m, n, acc[i][j][r]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM for f32 A (nnops' f32 x q4_1 product is an f32 one): 128 x 128
+// tiles, 4 waves of 64 x 64 (2 x 2 fragments of v_mfma_f32_32x32x2f32). Per
+// 32-k stage (one block along K) A is staged as f32 rows and B decoded to f32
+// (fmaf(d, q, m): d * q is exact, so one rounding, as d * q + m) as [n][k]
+// rows, both with a 4-float pad. Lane group g (lane >> 5) owns k = 16 g ..
+// 16 g + 15 of the stage for A and B alike (the MFMA's k index is the lane
+// group, so any such assignment sums the same products), and a lane reads its
+// 16 operands of a fragment with four 16-byte reads. FORM: 0 blocks along K
+// ([N][K/32]); 1 blocks along N ([K][N/32] raw rows); 2 the prepacked planes
+// of form 1. Bound: f32 MFMA.
+// ---------------------------------------------------------------------------
+template <int FORM>
+__global__ __launch_bounds__(256, 1) void gemm_q4_1_f32(Q41Kern p)
+{
+    constexpr int BM = 128, BN = 128, LD = 36;
+    __shared__ __attribute__((aligned(16))) float lds_a[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) float lds_b[2][BN * LD];
+
+    const int tiles_n = (p.n + BN - 1) / BN;
+    const int tm = blockIdx.x / tiles_n;
+    const int tn = blockIdx.x - tm * tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+    const int nbn = (p.n + 31) / 32;
+    const float* A = static_cast<const float*>(p.a);
+    const bool a_vec = (p.lda & 3) == 0 && ((uintptr_t)A & 15) == 0;
+    // B: thread -> block bi of the stage's 128, nibble bytes 8 bh .. 8 bh + 7
+    // (values 8 bh .. 8 bh + 7 and 16 + 8 bh .. 16 + 8 bh + 7 of the block)
+    const int bi = tid >> 1, bh = tid & 1;
+
+    v4f ra[4];
+    uint32_t rdm, rq0, rq1;
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + i * 256;
+            const int r = idx >> 3, c = idx & 7;      // 8 chunks of 4 floats per row
+            const int k = k0 + 4 * c;
+            const float* src = A + (int64_t)min(m0 + r, p.m - 1) * p.lda + k;
+            if (a_vec && k + 4 <= p.k) {
+                ra[i] = *reinterpret_cast<const v4f*>(src);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ra[i][e] = k + e < p.k ? src[e] : 0.0f;
+                }
+            }
+        }
+        if constexpr (FORM == 0) {
+            const uint8_t* src = p.b + (int64_t)min(n0 + bi, p.n - 1) * p.ldb + (int64_t)(k0 >> 5) * 20;
+            rdm = *reinterpret_cast<const uint32_t*>(src);
+            rq0 = *reinterpret_cast<const uint32_t*>(src + 4 + 8 * bh);
+            rq1 = *reinterpret_cast<const uint32_t*>(src + 8 + 8 * bh);
+        } else {
+            const int kr = bi >> 2;
+            const bool live = k0 + kr < p.k;
+            const int64_t r = min(k0 + kr, p.k - 1);
+            const int64_t j = min((n0 >> 5) + (bi & 3), nbn - 1);
+            if constexpr (FORM == 1) {
+                const uint8_t* src = p.b + r * p.ldb + j * 20;
+                rdm = *reinterpret_cast<const uint32_t*>(src);
+                rq0 = *reinterpret_cast<const uint32_t*>(src + 4 + 8 * bh);
+                rq1 = *reinterpret_cast<const uint32_t*>(src + 8 + 8 * bh);
+            } else {
+                // nibble dword d of row r at (r / 8) * 8 ldb + 128 block + 32 d + 4 (r % 8)
+                const uint8_t* q = p.b + (r >> 3) * 8 * p.ldb + j * 128 + 4 * (r & 7) + 64 * bh;
+                rdm = p.bdm[r * p.ldbdm + j];
+                rq0 = *reinterpret_cast<const uint32_t*>(q);
+                rq1 = *reinterpret_cast<const uint32_t*>(q + 32);
+            }
+            rdm = live ? rdm : 0u;      // rows past K decode to 0
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + i * 256;
+            *reinterpret_cast<v4f*>(&lds_a[buf][(idx >> 3) * LD + 4 * (idx & 7)]) = ra[i];
+        }
+        const float d = h2f(rdm & 0xffffu), mn = h2f(rdm >> 16);
+        float lo[8], hi[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint32_t byte = ((b < 4 ? rq0 : rq1) >> (8 * (b & 3))) & 0xffu;
+            lo[b] = fmaf(d, (float)(byte & 15u), mn);
+            hi[b] = fmaf(d, (float)(byte >> 4), mn);
+        }
+        if constexpr (FORM == 0) {
+            float* row = &lds_b[buf][bi * LD];
+            *reinterpret_cast<v4f*>(row + 8 * bh) = v4f{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<v4f*>(row + 8 * bh + 4) = v4f{lo[4], lo[5], lo[6], lo[7]};
+            *reinterpret_cast<v4f*>(row + 16 + 8 * bh) = v4f{hi[0], hi[1], hi[2], hi[3]};
+            *reinterpret_cast<v4f*>(row + 16 + 8 * bh + 4) = v4f{hi[4], hi[5], hi[6], hi[7]};
+        } else {
+            const int kr = bi >> 2, c0 = (bi & 3) * 32 + 8 * bh;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                lds_b[buf][(c0 + b) * LD + kr] = lo[b];
+                lds_b[buf][(c0 + 16 + b) * LD + kr] = hi[b];
+            }
+        }
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            acc[i][j] = v16f{0.0f};
+        }
+    }
+    const int kt = (p.k + 31) / 32;
+    const int fr = lane & 31, fg = 16 * (lane >> 5);
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int t = 0; t < kt; ++t) {
+        const int cur = t & 1;
+        if (t + 1 < kt) {
+            load_stage((t + 1) * 32);
+        }
+        v4f fa[2][4], fb[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                fa[i][q] = *reinterpret_cast<const v4f*>(&lds_a[cur][(wm0 + 32 * i + fr) * LD + fg + 4 * q]);
+                fb[i][q] = *reinterpret_cast<const v4f*>(&lds_b[cur][(wn0 + 32 * i + fr) * LD + fg + 4 * q]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s >> 2][s & 3], fb[j][s >> 2][s & 3],
+                                                                    acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < kt) {
+            store_stage(cur ^ 1);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn0 + 32 * j + fr;
+        if (n >= p.n) {
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < p.m) {
                     store_out(p, m, n, acc[i][j][r]);
                 }
@@ -2044,9 +2225,15 @@ inline size_t kn_dma_part_bytes(const KnDmaPlan& r)
     return (size_t)r.groups * r.splits * 2 * 4096;
 }
 
+// f32 A: the GEMV loop (one row of A per pass, each pass streaming the whole
+// weight) up to this many rows, the f32 MFMA GEMM past them. At K = 4096,
+// N = 14336 a pass takes 17-18 us and the GEMM 300 us for any M <= 128 (one
+// 128 x 128 tile per workgroup, 112 of them), 550 us at M = 512.
+constexpr int64_t kF32GemvRows = 16;
+
 inline bool use_gemv(const NnopsGemmQ41Args& g)
 {
-    return g.m <= 2 || !g.a_f16;
+    return g.m <= 2 || (!g.a_f16 && g.m <= kF32GemvRows);
 }
 
 // The blocks-along-N ring: f16 A with 16-byte rows, K % 64 == 0, 16-byte B
@@ -2058,12 +2245,6 @@ inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
            (!g.b_soa || g.k * g.ldb_dm * 4 < INT32_MAX);
 }
 
-// The GEMV loop (two rows of A per pass) serves every M of a prepacked
-// weight the ring cannot take
-inline bool gemv_route(const NnopsGemmQ41Args& g)
-{
-    return use_gemv(g) || (g.b_soa && !kn_ring_ok(g));
-}
 
 inline int64_t prepack_q41_dmp(int64_t n) { return ((n + 31) / 32 + 3) / 4 * 4; }
 
@@ -2074,16 +2255,17 @@ using namespace nnops_amd;
 
 extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
 {
-    // a prepacked weight may take the GEMV loop whatever M is (pointer
-    // alignment, which a size query does not see, decides)
-    if (g == nullptr || g->trans_b || !(use_gemv(*g) || g->b_soa)) {
+    if (g == nullptr || g->trans_b || !use_gemv(*g)) {
         return 0;
     }
+    // pointer alignment, which a size query may not see, picks between the
+    // two blocks-along-N GEMVs: room for either
+    const size_t split_bytes = align_up((size_t)kn_splits(*g) * (size_t)g->m * (size_t)g->n * sizeof(float));
     const KnDmaPlan kd = plan_kn_dma(*g);
     if (kd.groups > 0) {
-        return align_up(kn_dma_part_bytes(kd)) + align_up((size_t)kd.groups * kd.splits * 8);
+        return std::max(split_bytes, align_up(kn_dma_part_bytes(kd)) + align_up((size_t)kd.groups * kd.splits * 8));
     }
-    return align_up((size_t)kn_splits(*g) * (size_t)g->m * (size_t)g->n * sizeof(float));
+    return split_bytes;
 }
 
 extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, size_t ws_bytes, void* stream)
@@ -2133,7 +2315,7 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
     k.ldbdm = g->b_soa ? g->ldb_dm : 0;
     const bool soa = g->b_soa != 0;
 
-    if (gemv_route(*g)) {
+    if (use_gemv(*g)) {
         // rows of A handled per pass: 2 (f16 pairs), 1 for f32 A
         const int mt = g->a_f16 ? 2 : 1;
         for (int m0 = 0; m0 < k.m; m0 += mt) {
@@ -2220,6 +2402,15 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 }
             }
         }
+    } else if (!g->a_f16) {
+        const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
+        if (g->trans_b) {
+            hipLaunchKernelGGL(gemm_q4_1_f32<0>, dim3(tiles), dim3(256), 0, s, k);
+        } else if (soa) {
+            hipLaunchKernelGGL(gemm_q4_1_f32<2>, dim3(tiles), dim3(256), 0, s, k);
+        } else {
+            hipLaunchKernelGGL(gemm_q4_1_f32<1>, dim3(tiles), dim3(256), 0, s, k);
+        }
     } else if (g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0) {
         // blocks along K: the ring kernel (A by DMA, B decoded in registers)
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
@@ -2248,6 +2439,8 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
         if (g->trans_b) {
             hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, true>), dim3(tiles), dim3(256), 0, s, k);
+        } else if (soa) {
+            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false, true>), dim3(tiles), dim3(256), 0, s, k);
         } else {
             hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
         }

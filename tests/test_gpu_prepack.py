@@ -104,7 +104,8 @@ def test_prepack_rejects_mismatched_buffer_and_k():
 
 
 @pytest.mark.parametrize("M,K,N,a_f16", [(1, 4096, 1000, True), (2, 1024, 300, True), (40, 4096, 2048, True),
-                                         (300, 1024, 1000, True), (129, 192, 384, True), (3, 512, 256, False)])
+                                         (300, 1024, 1000, True), (129, 192, 384, True), (3, 512, 256, False),
+                                         (130, 1000, 200, False), (17, 512, 256, False)])
 def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     import torch
     announce(f"prepack q4_1 {M}x{K}x{N} f16={a_f16}")
@@ -118,8 +119,9 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     at = na.tensor(dev(a))
     got_p = run(op, at, packed, torch.float32, (M, N))
     got_r = run(op, at, wt, torch.float32, (M, N))
-    if M > 2 and a_f16:
-        np.testing.assert_array_equal(got_p, got_r)    # the ring: same decode, same order
+    if (M > 2 and a_f16) or M > 16:
+        # the f16 ring or the f32 MFMA GEMM: same decode, same order
+        np.testing.assert_array_equal(got_p, got_r)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
     scale = max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2)))
     err = float(np.max(np.abs(got_p - want)) / scale)
@@ -133,10 +135,10 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
 @pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200), (3, 37, 72),
                                    (1, 97, 40)])
 def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
-    """Ragged shapes. K % 64 != 0 with M > 2: the packed weight takes the GEMV
-    loop (two rows of A per pass). N = 200 (7 blocks per row, d|m rows padded
-    to 8): the packed weight takes the ring. The raw one takes the generic
-    MFMA kernel in both cases; all within the Q4_1 tolerance of the oracle."""
+    """Ragged shapes. K % 64 != 0 with M > 2: the packed weight and the raw
+    one both take the generic MFMA kernel (the same decode and order, so the
+    same bits). N = 200 (7 blocks per row, d|m rows padded to 8): the packed
+    weight takes the ring. All within the Q4_1 tolerance of the oracle."""
     import torch
     announce(f"prepack q4_1 ragged {M}x{K}x{N}")
     a = dg.normal(M + K, (M, K)).astype(np.float16)
@@ -145,6 +147,8 @@ def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
     wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
     _, packed = op.prepack(wt)
     got = run(op, na.tensor(dev(a)), packed, torch.float32, (M, N))
+    if M > 2 and K % 64:
+        np.testing.assert_array_equal(got, run(op, na.tensor(dev(a)), wt, torch.float32, (M, N)))
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
     err = float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
     assert err <= 2e-3, err

@@ -64,6 +64,22 @@ def test_q4_1_f32_a(trans_b):
     assert norm_err(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40)])
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_q4_1_f32_a_gemm(M, K, N, trans_b):
+    """f32 A past the GEMV rows: the f32 MFMA GEMM (ragged M, N and K tiles)
+    against the f64-accumulated oracle within 1e-4 (normalized; an f32 sum of
+    K = 4096 products carries ~1e-5); M = 16 is the GEMV loop's last row
+    count."""
+    announce(f"q4_1 f32 A GEMM {M}x{K}x{N} trans_b={trans_b}")
+    seed = 3 * M + K + N + int(trans_b)
+    a = dg.normal(seed, (M, K))
+    blk = dg.q4_1_blocks(seed + 1, N, K) if trans_b else dg.q4_1_blocks(seed + 2, K, N)
+    got = run_gpu(a, blk, N, trans_b=trans_b)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
+    assert norm_err(got, want) <= 1e-4
+
+
 @pytest.mark.parametrize("M", [1, 40])
 def test_q4_1_f16_out_nnops_semantics(M):
     """f16 A -> f16 C (nnops' dtype rule): the oracle rounds each decoded
