@@ -1909,7 +1909,13 @@ template <int BM, int BN, int WM, int WN>
 void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode, bool flip, hipStream_t s)
 {
     if (bk == 128) {
-        launch_ring_bk<BM, BN, WM, WN, 128, 2>(k, sk, mode, flip, s);
+        // three slots where the LDS holds them (config 5's 192x128 tiles:
+        // 33.7 -> 32.9 us), two for the 256x256 tile
+        if constexpr ((BM + BN) * 128 * 3 <= 160 * 1024 && BM + BN < 512) {
+            launch_ring_bk<BM, BN, WM, WN, 128, 3>(k, sk, mode, flip, s);
+        } else {
+            launch_ring_bk<BM, BN, WM, WN, 128, 2>(k, sk, mode, flip, s);
+        }
     } else if constexpr (BM % (16 * WM * WN) == 0 && BN % (16 * WM * WN) == 0) {
         launch_ring_bk<BM, BN, WM, WN, 64, 4>(k, sk, mode, flip, s);
     }
