@@ -237,6 +237,13 @@ int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* args, void* workspace, size_t wo
  *   not gated:  f = src[r][c] + bias[c] (+ old if residual_pre);
  *               f = act(clip(f)); out = f (+ old, after the output type's
  *               rounding of f, if add_to and not residual_pre)
+ *   matmul_order (MatMul's C = act(clip(alpha P + bias + beta C_old)),
+ *               include/nnops/ops/matmul.hpp:5-11, with the accumulator
+ *               init of matmul_qblock_fused.cpp:106-142): b = residual_pre
+ *               ? 1 : beta; init = T(b old + bias) with a bias, else
+ *               T(b old) (old itself when b = 1, 0 when b = 0), T the
+ *               output type; out = act(clip(alpha src + init)). add_to is
+ *               not read in this order.
  *   gated:      src holds 2n columns, gate [0, n) and value [n, 2n):
  *               g = T(src[r][c] + bias[c]), v = T(src[r][n + c] + bias[n + c])
  *               (T the output type: the reference's GEMM tile is of X's
@@ -261,6 +268,8 @@ typedef struct NnopsFpOutArgs {
     int32_t gated;
     int32_t gate_act;           /* NNOPS_ACT_NONE/RELU/GELU/SIGMOID/TANH/SILU */
     float gate_alpha, gate_beta, gate_limit;
+    int32_t matmul_order;       /* 0: the orders above; 1: MatMul's (alpha, beta) */
+    float alpha, beta;          /* read only when matmul_order */
 } NnopsFpOutArgs;
 
 int nnops_hip_fp_output_pass(const NnopsFpOutArgs* args, void* stream);

@@ -100,6 +100,7 @@ class LinearAttrs(C.Structure):
         ("requant_round_even", C.c_int32), ("float_epilogue", C.c_int32),
         ("gate_activation", C.c_int32), ("gate_alpha", C.c_float), ("gate_beta", C.c_float),
         ("gate_limit", C.c_float),
+        ("matmul_order", C.c_int32), ("alpha", C.c_float), ("beta", C.c_float),
     ]
 
 

@@ -209,10 +209,17 @@ struct QuantCall {
     bool gated = false;
     EpilogueActivateType gate_act = EpilogueActivateType::Silu;
     float gate_alpha = 1.0f, gate_beta = 0.0f, gate_limit = std::numeric_limits<float>::infinity();
+    // MatMul's product scale and old-C scale (the fp routes read them, the
+    // integer routes ignore them: include/nnops/ops/matmul.hpp:37-44)
+    bool matmul = false;
+    float alpha = 1.0f, beta = 0.0f;
 
     /// The fp x q4_1 route writes its f32 results to the workspace and runs
     /// nnops_hip_fp_output_pass when there is anything after the GEMM.
-    bool q4_1_pass() const { return bias || add_to || gated || epilogue_is_active(ep); }
+    bool q4_1_pass() const
+    {
+        return bias || add_to || gated || epilogue_is_active(ep) || (matmul && (alpha != 1.0f || beta != 0.0f));
+    }
 };
 
 int32_t out_kind_of(DataType dt)
@@ -685,6 +692,9 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             fo.gate_alpha = q.gate_alpha;
             fo.gate_beta = q.gate_beta;
             fo.gate_limit = q.gate_limit;
+            fo.matmul_order = q.matmul;
+            fo.alpha = q.alpha;
+            fo.beta = q.beta;
         }
         const int64_t a_mat = a_rows_per * a.pitch();
         const int64_t b_mat = b_rows_per * b.pitch();
@@ -788,6 +798,9 @@ QuantCall matmul_call(const MatMulAttributes& attrs, bool bias)
     q.round_even = attrs.requant_round_even;
     q.float_ep = attrs.float_epilogue;
     q.bias = bias;
+    q.matmul = true;
+    q.alpha = attrs.alpha;
+    q.beta = attrs.beta;
     return q;
 }
 

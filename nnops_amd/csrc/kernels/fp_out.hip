@@ -27,6 +27,8 @@ struct FpOut {
     int add_to, residual_pre;
     int gated, gate_act;
     float gate_alpha, gate_beta, gate_limit;
+    int mm;                     // MatMul's order: alpha P + T(beta old + bias)
+    float alpha, beta;
 };
 
 __device__ __forceinline__ float round_out(bool f16, float x)
@@ -102,11 +104,25 @@ __global__ __launch_bounds__(256) void fp_out_pass(FpOut p, int cblocks)
         }
         const int c = c0 + e;
         float old = 0.0f;
-        if (p.add_to) {
+        const float beta = p.residual_pre ? 1.0f : p.beta;
+        if (p.mm ? beta != 0.0f : p.add_to) {
             old = f16 ? (float)reinterpret_cast<const _Float16*>(orow)[c] : reinterpret_cast<const float*>(orow)[c];
         }
         float y;
-        if (p.gated) {
+        if (p.mm) {
+            // the accumulator init (C primed with beta old + bias, stored in
+            // the output type), then the scaled product joins it
+            float init = 0.0f;
+            if (p.bias != nullptr) {
+                init = beta == 0.0f ? bias_at(p, c) : round_out(f16, __fadd_rn(__fmul_rn(old, beta), bias_at(p, c)));
+            } else if (beta == 1.0f) {
+                init = old;
+            } else if (beta != 0.0f) {
+                init = round_out(f16, __fmul_rn(old, beta));
+            }
+            const float prod = p.alpha == 1.0f ? a[e] : __fmul_rn(a[e], p.alpha);
+            y = apply_act_fp(p.ep, __fadd_rn(prod, init));
+        } else if (p.gated) {
             // the reference's [rows, 2n] tile is of the output's type
             float g = round_out(f16, __fadd_rn(a[e], bias_at(p, c)));
             float u = round_out(f16, __fadd_rn(v[e], bias_at(p, p.n + c)));
@@ -160,7 +176,7 @@ extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
         return NNOPS_INVALID_ARGUMENT;
     }
     if (a->act < NNOPS_ACT_NONE || a->act > NNOPS_ACT_RELU6 || (a->gated && !gate_act_ok(a->gate_act)) ||
-        (a->gated && a->add_to && a->residual_pre)) {
+        (a->gated && a->add_to && a->residual_pre) || (a->gated && a->matmul_order)) {
         return NNOPS_UNSUPPORTED;
     }
     FpOut p{};
@@ -185,6 +201,9 @@ extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
     p.gate_alpha = a->gate_alpha;
     p.gate_beta = a->gate_beta;
     p.gate_limit = a->gate_limit;
+    p.mm = a->matmul_order != 0;
+    p.alpha = a->alpha;
+    p.beta = a->beta;
     const int64_t cblocks = (a->n + 1023) / 1024;
     if (cblocks * a->rows > INT32_MAX) {
         return NNOPS_UNSUPPORTED;

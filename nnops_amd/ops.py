@@ -193,10 +193,13 @@ class MatMul(_Op):
                  min_clip=-math.inf, max_clip=math.inf, quant=L.EQ_NONE, quant_scales=None,
                  quant_zero_points=None, quant_param_count=0, residual_pre_activation=False,
                  requant_round_even=False, float_epilogue=False, act_quant_dtype=L.DT_S8,
-                 act_alpha=0.0, act_beta=1.0, backend=L.BACKEND_HIP):
+                 act_alpha=0.0, act_beta=1.0, alpha=1.0, beta=0.0, backend=L.BACKEND_HIP):
         a = L.MatMulAttrs()
         L.lib().nnops_matmul_attrs_init(C.byref(a))
         a.transpose_a, a.transpose_b = int(transpose_a), int(transpose_b)
+        # the product's and old C's scales: read by the fp (q4_1) routes,
+        # ignored by the integer ones, as in nnops
+        a.alpha, a.beta = alpha, beta
         a.output_dtype = output_dtype
         a.residual_pre_activation = int(residual_pre_activation)
         a.requant_round_even = int(requant_round_even)

@@ -57,6 +57,7 @@ class FpOut(C.Structure):
         ("min_clip", C.c_float), ("max_clip", C.c_float),
         ("add_to", C.c_int32), ("residual_pre", C.c_int32), ("gated", C.c_int32), ("gate_act", C.c_int32),
         ("gate_alpha", C.c_float), ("gate_beta", C.c_float), ("gate_limit", C.c_float),
+        ("matmul_order", C.c_int32), ("alpha", C.c_float), ("beta", C.c_float),
     ]
 
 
@@ -158,6 +159,11 @@ def cpu_lib():
         _cpu.ref_cpu_matmul_q4_1.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
                                              C.c_int, C.c_int]
         _cpu.ref_cpu_matmul_q4_1.restype = C.c_int
+        _cpu.ref_cpu_matmul_q4_1_ep.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                C.c_int64, C.c_int64, C.c_int64, C.c_int, C.c_float, C.c_float,
+                                                C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,
+                                                C.c_int]
+        _cpu.ref_cpu_matmul_q4_1_ep.restype = C.c_int
         _cpu.ref_cpu_linear_q4_1.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                              C.c_int64, C.c_int64, C.c_int, C.c_float, C.c_float, C.c_float,
                                              C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
@@ -265,10 +271,13 @@ def gemm_q4_1(a, blocks, n, *, trans_b=True, ldb_bytes=None, c_f16=False,
 
 def fp_out_pass(src, n, *, out=None, out_f16=False, bias=None, act=ACT_NONE, act_alpha=0.0, act_beta=1.0,
                 min_clip=-np.inf, max_clip=np.inf, add_to=False, residual_pre=False, gated=False,
-                gate_act=ACT_SILU, gate_alpha=1.0, gate_beta=0.0, gate_limit=np.inf):
+                gate_act=ACT_SILU, gate_alpha=1.0, gate_beta=0.0, gate_limit=np.inf, matmul_order=False,
+                alpha=1.0, beta=0.0):
     """The fp output pass over f32 GEMM results ``src`` [rows, n] (gated:
     [rows, 2n]); ``out`` holds the residual when add_to (f32 or f16, as
-    out_f16); ``bias`` in the output's type. Returns the output."""
+    out_f16); ``bias`` in the output's type. ``matmul_order``: MatMul's
+    act(clip(alpha src + T(beta old + bias))) (``out`` holds old C).
+    Returns the output."""
     src = np.ascontiguousarray(src, dtype=np.float32)
     rows = src.shape[0]
     odt = np.float16 if out_f16 else np.float32
@@ -281,6 +290,7 @@ def fp_out_pass(src, n, *, out=None, out_f16=False, bias=None, act=ACT_NONE, act
     p.act, p.act_alpha, p.act_beta, p.min_clip, p.max_clip = act, act_alpha, act_beta, min_clip, max_clip
     p.add_to, p.residual_pre, p.gated, p.gate_act = int(add_to), int(residual_pre), int(gated), gate_act
     p.gate_alpha, p.gate_beta, p.gate_limit = gate_alpha, gate_beta, gate_limit
+    p.matmul_order, p.alpha, p.beta = int(matmul_order), alpha, beta
     lib().orc_fp_out_pass(C.byref(p))
     return o
 

@@ -490,10 +490,24 @@ void orc_fp_out_pass(const orc_fp_out_t* p)
     for (int64_t r = 0; r < p->rows; ++r) {
         for (int64_t c = 0; c < p->n; ++c) {
             const int64_t oi = r * p->ld_out + c;
-            const float old = p->add_to ? fp_load(p->out_f16, p->out, oi) : 0.0f;
+            const float beta = p->residual_pre ? 1.0f : p->beta;
+            const int read_old = p->matmul_order ? beta != 0.0f : p->add_to;
+            const float old = read_old ? fp_load(p->out_f16, p->out, oi) : 0.0f;
             const float bg = p->bias ? fp_load(p->out_f16, p->bias, c) : 0.0f;
             float y;
-            if (p->gated) {
+            if (p->matmul_order) {
+                /* matmul_qblock_fused.cpp:106-142: C primed with beta old +
+                 * bias in its own type (tile_scale_add_bias, separately
+                 * rounded mul and add; matmul_helper.cpp:924-943) or scaled
+                 * by beta (tile_scale), then alpha times the product joins it
+                 * (mma_qblock.hpp:255-266), clamped, and the activation. */
+                float init = 0.0f;
+                if (p->bias) init = beta == 0.0f ? bg : fp_round(p->out_f16, old * beta + bg);
+                else if (beta == 1.0f) init = old;
+                else if (beta != 0.0f) init = fp_round(p->out_f16, old * beta);
+                const float prod = p->alpha == 1.0f ? p->src[r * p->ld_src + c] : p->src[r * p->ld_src + c] * p->alpha;
+                y = apply_act_fp(p->act, prod + init, p->min_clip, p->max_clip, p->act_alpha, p->act_beta);
+            } else if (p->gated) {
                 const float bv = p->bias ? fp_load(p->out_f16, p->bias, p->n + c) : 0.0f;
                 float g = fp_round(p->out_f16, p->src[r * p->ld_src + c] + bg);
                 float v = fp_round(p->out_f16, p->src[r * p->ld_src + p->n + c] + bv);

@@ -118,6 +118,8 @@ typedef struct {
     float act_alpha, act_beta, min_clip, max_clip;
     int32_t add_to, residual_pre, gated, gate_act;
     float gate_alpha, gate_beta, gate_limit;
+    int32_t matmul_order;  /* MatMul's alpha P + T(beta old + bias) order */
+    float alpha, beta;
 } orc_fp_out_t;
 
 void orc_fp_out_pass(const orc_fp_out_t* p);

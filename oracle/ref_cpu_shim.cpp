@@ -212,6 +212,41 @@ int ref_cpu_matmul_q4_1(const uint16_t* a, const uint8_t* w, uint16_t* c, int64_
     return static_cast<int>(st);
 }
 
+// nnops' fp x q4_1 MatMul with the full fp epilogue: f32 / f16 A [M, K]
+// (a_f16), W [N][K/32] blocks (trans_b) or [K][N/32], bias of A's type [N] or
+// NULL, C of A's type [M, N] (its contents are old C when beta != 0 or
+// residual_pre): C = act(clip(alpha A W + bias + beta C_old)), through
+// MatMul::create / compute (include/nnops/ops/matmul.hpp:5-11,33-65).
+int ref_cpu_matmul_q4_1_ep(const void* a, int a_f16, const uint8_t* w, const void* bias, void* c, int64_t M,
+                           int64_t N, int64_t K, int trans_b, float alpha, float beta, int residual_pre, int act,
+                           float act_alpha, float act_beta, float min_clip, float max_clip, int threads)
+{
+    Pool* p = pool_of(threads);
+    const DataType dt = a_f16 ? DataType::f16 : DataType::f32;
+    const int64_t ashape[] = {M, K}, wshape_t[] = {N, K}, wshape[] = {K, N}, cshape[] = {M, N}, bshape[] = {N};
+    TensorView av(ashape, dt, const_cast<void*>(a));
+    TensorView wv(trans_b ? std::span<const int64_t>(wshape_t) : std::span<const int64_t>(wshape), DataType::q4_1,
+                  const_cast<uint8_t*>(w));
+    TensorView bv(bshape, dt, const_cast<void*>(bias));
+    TensorView cv(cshape, dt, c);
+    MatMulAttributes attrs{};
+    attrs.transpose_b = trans_b != 0;
+    attrs.alpha = alpha;
+    attrs.beta = beta;
+    attrs.residual_pre_activation = residual_pre != 0;
+    attrs.epilogue.type = static_cast<EpilogueActivateType>(act);
+    attrs.epilogue.alpha = act_alpha;
+    attrs.epilogue.beta = act_beta;
+    attrs.epilogue.min_clip = min_clip;
+    attrs.epilogue.max_clip = max_clip;
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {av, wv, bv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, bias ? 3 : 2), ctx);
+    return static_cast<int>(st);
+}
+
 // nnops' Linear over a q4_1 weight [N2, K] (blocks along K): f32 / f16 X
 // [M, K] (x_f16), bias of X's type [N2] or NULL, output C of X's type [M, N]
 // (N = N2 / 2 when gated, else N2; its current contents are the residual when

@@ -152,6 +152,46 @@ def test_q4_1_matmul_bias_gelu_blocks_along_n(M):
     assert norm_err(host(y), want) <= TOL
 
 
+MM_VARIANTS = [
+    dict(alpha=0.5, beta=0.75, bias=True),
+    dict(alpha=1.0, beta=1.0),
+    dict(alpha=2.0, beta=-0.5, act=na.EP_RELU),
+    dict(alpha=1.5, beta=3.0, bias=True, act=na.EP_SILU),
+    dict(alpha=0.25, beta=0.0, residual_pre=True, bias=True),
+]
+MM_ACT = {None: oracle.ACT_NONE, na.EP_RELU: oracle.ACT_RELU, na.EP_SILU: oracle.ACT_SILU}
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("M,trans_b", [(1, True), (2, False), (40, True), (300, False)])
+@pytest.mark.parametrize("kw", MM_VARIANTS)
+def test_q4_1_matmul_alpha_beta(f16, M, trans_b, kw):
+    """MatMul's fp epilogue over a q4_1 weight: C = act(alpha P + T(beta C_old
+    + bias)) (nnops' order, pinned in tests/test_oracle.py), on the GEMV
+    and GEMM routes of both layouts."""
+    import torch
+    announce(f"q4_1 matmul alpha/beta M={M} trans_b={trans_b} f16={f16} {kw}")
+    dt = np.float16 if f16 else np.float32
+    K, N = 512, 256
+    x = dg.normal(950 + M, (M, K)).astype(dt)
+    blk = dg.q4_1_blocks(951, N, K) if trans_b else dg.q4_1_blocks(952, K, N)
+    bias = dg.normal(953, (N,)).astype(dt) if kw.get("bias") else None
+    old = dg.normal(954, (M, N)).astype(dt)
+    y = dev(old)
+    op = na.MatMul(transpose_b=trans_b, act=kw.get("act"), alpha=kw["alpha"], beta=kw["beta"],
+                   residual_pre_activation=kw.get("residual_pre", False))
+    ins = [na.tensor(dev(x)), na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[N, K] if trans_b else [K, N])]
+    if bias is not None:
+        ins.append(na.tensor(dev(bias)))
+    assert op.compute([na.tensor(y)], ins) == na.OK
+    torch.cuda.synchronize()
+    acc = oracle.gemm_q4_1(x, blk, N, trans_b=trans_b, w_round_f16=f16 and M > 2)
+    want = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, act=MM_ACT[kw.get("act")],
+                              matmul_order=True, alpha=kw["alpha"], beta=kw["beta"],
+                              residual_pre=kw.get("residual_pre", False)).astype(np.float32)
+    assert norm_err(host(y).astype(np.float32), want) <= TOL
+
+
 def test_gated_validation():
     """nnops' gated-form rules (src/ops/linear.cpp:63-107), over a q4_1 weight."""
     import torch

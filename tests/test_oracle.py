@@ -506,3 +506,59 @@ def test_nnops_gated_silu_f16_is_per_operation_f16():
     g, v = h(acc[:, :48]), h(acc[:, 48:])
     y = h(h(g * h(1.0 / h(1.0 + h(np.exp(-g))))) * v)
     assert np.array_equal(want.astype(np.float32), y)
+
+
+# ---------------------------------------------------------------------------
+# MatMul's fp epilogue order over a q4_1 weight (alpha, beta, bias, residual,
+# clip, activation) against nnops' own CPU MatMul: C = act(clip(alpha P +
+# T(beta C_old + bias))). M = 3 takes nnops' fused small-M route, M = 40 its
+# packed route (f16 A: the weight decoded to f16 first). f32 within 2e-5 of
+# the rms (the GEMM's summation order), f16 within 4e-3.
+# ---------------------------------------------------------------------------
+MM_CASES = [
+    dict(alpha=0.5, beta=0.75, bias=True),
+    dict(alpha=1.0, beta=1.0),
+    dict(alpha=2.0, beta=-0.5, act=oracle.ACT_RELU),
+    dict(alpha=1.0, beta=0.0, bias=True, act=oracle.ACT_GELU),
+    dict(alpha=0.25, beta=0.0, residual_pre=True, bias=True, min_clip=-0.5, max_clip=0.5),
+    dict(alpha=1.5, beta=3.0, bias=True, act=oracle.ACT_SILU),
+]
+
+
+def _ref_matmul_q4_1_ep(a, blk, n, trans_b, bias, old, kw):
+    M, K = a.shape
+    c = old.astype(a.dtype).copy()
+    b = None if bias is None else np.ascontiguousarray(bias.astype(a.dtype))
+    rc = oracle.cpu_lib().ref_cpu_matmul_q4_1_ep(
+        a.ctypes.data, int(a.dtype == np.float16), blk.ctypes.data, None if b is None else b.ctypes.data,
+        c.ctypes.data, M, n, K, int(trans_b), kw.get("alpha", 1.0), kw.get("beta", 0.0),
+        int(kw.get("residual_pre", False)), kw.get("act", 0), 0.0, 1.0, kw.get("min_clip", -np.inf),
+        kw.get("max_clip", np.inf), 4)
+    assert rc == 0, rc
+    return c
+
+
+@cpu_only
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("M,trans_b", [(3, True), (3, False), (40, True)])
+@pytest.mark.parametrize("kw", MM_CASES)
+def test_oracle_matmul_order_matches_nnops_matmul(f16, M, trans_b, kw):
+    dt = np.float16 if f16 else np.float32
+    K, N = 256, 72
+    a = dg.normal(21 + M, (M, K)).astype(dt)
+    blk = dg.q4_1_blocks(22, N, K) if trans_b else dg.q4_1_blocks(23, K, N)
+    bias = dg.normal(24, (N,)).astype(dt) if kw.get("bias") else None
+    old = dg.normal(25, (M, N)).astype(dt)
+    want = _ref_matmul_q4_1_ep(a, blk, N, trans_b, bias, old, kw).astype(np.float64)
+    acc = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b, w_round_f16=f16 and M > 32)
+    okw = {k: v for k, v in kw.items() if k != "bias"}
+    got = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, matmul_order=True, **okw).astype(np.float64)
+    err = np.max(np.abs(want - got)) / np.sqrt(np.mean(want ** 2))
+    assert err <= (4e-3 if f16 else 2e-5), err
+    # the order is what the bar pins: beta on the product, or alpha on the
+    # bias and old C, moves the result far past it
+    if kw.get("alpha", 1.0) != 1.0 or kw.get("beta", 0.0) not in (0.0, 1.0):
+        swapped = dict(okw, alpha=kw.get("beta", 0.0) or 1.0, beta=kw.get("alpha", 1.0))
+        bad = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, matmul_order=True,
+                                 **swapped).astype(np.float64)
+        assert np.max(np.abs(want - bad)) / np.sqrt(np.mean(want ** 2)) > 1e-2
