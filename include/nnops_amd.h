@@ -226,6 +226,32 @@ size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* args);
 int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* args, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Dense fp product of nnops' float MatMul / Linear routes: C = alpha (A B)
+ * for f32 x f32 or f16 x f16 (in_f16), accumulated in f32 and rounded once
+ * to C's type (f32, or f16 with out_f16). Replaces the product of nnops'
+ * matmul_small_fp / FpRoute<T> over dense operands
+ * (src/backend/cpu/matmul/matmul_small.cpp:325-360, matmul.cpp:57-198),
+ * whose f16 form keeps its accumulator in C between 128-deep k blocks; the
+ * bias, beta, residual and epilogue are the output pass below.
+ * A [M][lda], B [N][ldb] (trans_b) or [K][ldb], C [M][ldc]; pitches in
+ * elements. The workspace holds K-split partials (small M, [K][N] B), a
+ * transposed [K][N] f16 B and the ring GEMM's split partials (large f16
+ * shapes): nnops_hip_gemm_fp_workspace_size bytes, 16-byte aligned. */
+typedef struct NnopsGemmFpArgs {
+    const void* a;
+    const void* b;
+    void* c;
+    int64_t m, n, k;
+    int64_t lda, ldb, ldc;      /* elements */
+    int32_t trans_b;
+    int32_t in_f16;             /* A and B f16 (else f32) */
+    int32_t out_f16;            /* C f16 (else f32) */
+    float alpha;
+} NnopsGemmFpArgs;
+
+size_t nnops_hip_gemm_fp_workspace_size(const NnopsGemmFpArgs* args);
+int nnops_hip_gemm_fp(const NnopsGemmFpArgs* args, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Output pass of the fp x q4_1 routes over the GEMM's f32 results:
  * bias, the residual (add_to) and the epilogue (clip, activation), and the
  * gated combine of Linear's gated form. Replaces the fp epilogue of nnops'

@@ -18,5 +18,5 @@ from ._lib import (  # noqa: F401
     EP_RELU6, EQ_NONE, EQ_REQUANTIZE,
 )
 from .ops import (  # noqa: F401
-    MatMul, Linear, QuantizeLinear, DequantizeLinear, gemm_i8, gemm_q4_1, tensor, q4_1_quantize, q4_1_dequantize,
+    MatMul, Linear, QuantizeLinear, DequantizeLinear, gemm_i8, gemm_q4_1, gemm_fp, tensor, q4_1_quantize, q4_1_dequantize,
 )

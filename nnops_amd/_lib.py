@@ -58,6 +58,15 @@ class GemmQ41Args(C.Structure):
     ]
 
 
+class GemmFpArgs(C.Structure):
+    _fields_ = [
+        ("a", C.c_void_p), ("b", C.c_void_p), ("c", C.c_void_p),
+        ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
+        ("lda", C.c_int64), ("ldb", C.c_int64), ("ldc", C.c_int64),
+        ("trans_b", C.c_int32), ("in_f16", C.c_int32), ("out_f16", C.c_int32), ("alpha", C.c_float),
+    ]
+
+
 class Tensor(C.Structure):
     _fields_ = [
         ("rank", C.c_int64), ("dims", C.c_int64 * 8), ("dtype", C.c_int32),
@@ -122,6 +131,8 @@ SIGNATURES = {
     "nnops_hip_gemm_i8_noalloc": (C.c_int, [C.POINTER(GemmI8Args), C.c_void_p]),
     "nnops_hip_gemm_q4_1_workspace_size": (C.c_size_t, [C.POINTER(GemmQ41Args)]),
     "nnops_hip_gemm_q4_1": (C.c_int, [C.POINTER(GemmQ41Args), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "nnops_hip_gemm_fp_workspace_size": (C.c_size_t, [C.POINTER(GemmFpArgs)]),
+    "nnops_hip_gemm_fp": (C.c_int, [C.POINTER(GemmFpArgs), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_fp_output_pass": (C.c_int, [C.POINTER(FpOutArgs), C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
     "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),

@@ -32,6 +32,7 @@ SOURCES = [
     "csrc/kernels/q4_1_codec.hip",
     "csrc/kernels/quant.hip",
     "csrc/kernels/fp_out.hip",
+    "csrc/kernels/fp_gemm.hip",
     "csrc/host/ops.cpp",
     "csrc/host/quant_linear.cpp",
     "csrc/host/capi_ops.cpp",

@@ -264,6 +264,28 @@ bool is_fp_quant_pair(DataType a, DataType b)
     return (a == DataType::f32 || a == DataType::f16) && b == DataType::s8;
 }
 
+/// nnops' dense float pairs: f32 x f32 and f16 x f16 (the output follows A).
+bool is_dense_fp_pair(DataType a, DataType b)
+{
+    return (a == DataType::f32 || a == DataType::f16) && b == a;
+}
+
+NnopsGemmFpArgs fp_args_from_geometry(const Geometry& g, bool f16, bool out_f16)
+{
+    NnopsGemmFpArgs x{};
+    x.m = g.m;
+    x.n = g.n;
+    x.k = g.k;
+    x.trans_b = g.trans_b;
+    x.in_f16 = f16;
+    x.out_f16 = out_f16;
+    x.lda = g.k;
+    x.ldb = g.trans_b ? g.k : g.n;
+    x.ldc = g.n;
+    x.alpha = 1.0f;
+    return x;
+}
+
 NnopsGemmI8Args i8_args_from_geometry(const Geometry& g, int32_t out_kind)
 {
     NnopsGemmI8Args x{};
@@ -359,6 +381,11 @@ size_t quant_workspace(const TensorDesc& a, const TensorDesc& b, const TensorDes
         NnopsGemmQ41Args x = q41_args_from_geometry(g, q, q.q4_1_pass() ? NNOPS_OUT_F32 : out_kind_of(odt));
         x.a_f16 = a.dtype == DataType::f16;
         return q4_1_pass_bytes(g, q) + align_up(nnops_hip_gemm_q4_1_workspace_size(&x));
+    }
+    if (is_dense_fp_pair(a.dtype, b.dtype) && !g.b_packed) {
+        const NnopsGemmFpArgs x =
+            fp_args_from_geometry(g, a.dtype == DataType::f16, !q.q4_1_pass() && a.dtype == DataType::f16);
+        return q4_1_pass_bytes(g, q) + align_up(nnops_hip_gemm_fp_workspace_size(&x));
     }
     return 0;
 }
@@ -604,6 +631,37 @@ Status run_fp_quant(const QuantCall& q, const Geometry& g, DataType act_dtype, T
     return run_i8(q, g, out, av, b, bias, stream, static_cast<char*>(workspace) + prefix, ws_bytes - prefix);
 }
 
+/// The output pass's arguments over the f32 product staged at the head of
+/// the workspace (rows x g.n, the gated form's 2N columns included).
+NnopsFpOutArgs fp_pass_args(const QuantCall& q, const Geometry& g, const TensorView& out, const TensorView* bias,
+                            const void* staged)
+{
+    NnopsFpOutArgs fo{};
+    fo.src = static_cast<const float*>(staged);
+    fo.ld_src = g.n;
+    fo.ld_out = out.row_stride_elems();
+    fo.rows = g.m;
+    fo.n = q.gated ? g.n / 2 : g.n;
+    fo.out_f16 = out.data_type() == DataType::f16;
+    fo.bias = bias != nullptr ? bias->ptr<const void>() : nullptr;
+    fo.act = static_cast<int32_t>(q.ep.type);
+    fo.act_alpha = q.ep.alpha;
+    fo.act_beta = q.ep.beta;
+    fo.min_clip = q.ep.min_clip;
+    fo.max_clip = q.ep.max_clip;
+    fo.add_to = q.add_to;
+    fo.residual_pre = q.residual_pre;
+    fo.gated = q.gated;
+    fo.gate_act = static_cast<int32_t>(q.gate_act);
+    fo.gate_alpha = q.gate_alpha;
+    fo.gate_beta = q.gate_beta;
+    fo.gate_limit = q.gate_limit;
+    fo.matmul_order = q.matmul;
+    fo.alpha = q.alpha;
+    fo.beta = q.beta;
+    return fo;
+}
+
 Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView> inputs,
                  const ComputeContext& ctx, void* workspace, size_t ws_bytes,
                  DataType act_dtype = DataType::s8)
@@ -645,7 +703,6 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             return Status::unsupported;
         }
         const bool pass = q.q4_1_pass();
-        const int64_t n_out = q.gated ? g.n / 2 : g.n;
         if (pass) {
             // the output pass reads the bias in the destination's type
             if (bias != nullptr && (bias->data_type() != out.data_type() || bias->numel() < g.n)) {
@@ -671,31 +728,7 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             return Status::not_initialized;
         }
         char* gemm_ws = static_cast<char*>(workspace) + tmp;
-        NnopsFpOutArgs fo{};
-        if (pass) {
-            fo.src = static_cast<const float*>(workspace);
-            fo.ld_src = g.n;
-            fo.ld_out = out.row_stride_elems();
-            fo.rows = g.m;
-            fo.n = n_out;
-            fo.out_f16 = out.data_type() == DataType::f16;
-            fo.bias = bias != nullptr ? bias->ptr<const void>() : nullptr;
-            fo.act = static_cast<int32_t>(q.ep.type);
-            fo.act_alpha = q.ep.alpha;
-            fo.act_beta = q.ep.beta;
-            fo.min_clip = q.ep.min_clip;
-            fo.max_clip = q.ep.max_clip;
-            fo.add_to = q.add_to;
-            fo.residual_pre = q.residual_pre;
-            fo.gated = q.gated;
-            fo.gate_act = static_cast<int32_t>(q.gate_act);
-            fo.gate_alpha = q.gate_alpha;
-            fo.gate_beta = q.gate_beta;
-            fo.gate_limit = q.gate_limit;
-            fo.matmul_order = q.matmul;
-            fo.alpha = q.alpha;
-            fo.beta = q.beta;
-        }
+        NnopsFpOutArgs fo = fp_pass_args(q, g, out, bias, workspace);
         const int64_t a_mat = a_rows_per * a.pitch();
         const int64_t b_mat = b_rows_per * b.pitch();
         const int64_t c_mat = g.m * out.pitch();
@@ -706,6 +739,56 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             char* cb = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
             xb.c = pass ? workspace : static_cast<void*>(cb);
             const int rc = nnops_hip_gemm_q4_1(&xb, gemm_ws, need, stream);
+            if (rc != NNOPS_OK) {
+                return from_code(rc);
+            }
+            if (pass) {
+                fo.out = cb;
+                if (const int rp = nnops_hip_fp_output_pass(&fo, stream); rp != NNOPS_OK) {
+                    return from_code(rp);
+                }
+            }
+        }
+        return Status::ok;
+    }
+
+    if (is_dense_fp_pair(a.data_type(), b.data_type())) {
+        // nnops' float route: the output follows A; a bias of the output's type
+        if (g.trans_a || g.b_packed) {
+            return Status::unsupported;
+        }
+        if (out.data_type() != a.data_type()) {
+            return Status::invalid_argument;
+        }
+        const bool pass = q.q4_1_pass();
+        if (bias != nullptr && (bias->data_type() != out.data_type() || bias->numel() < g.n)) {
+            return Status::invalid_argument;
+        }
+        if (q.gated && (g.n % 2) != 0) {
+            return Status::invalid_argument;
+        }
+        const bool f16 = a.data_type() == DataType::f16;
+        NnopsGemmFpArgs x = fp_args_from_geometry(g, f16, !pass && f16);
+        x.lda = a.row_stride_elems();
+        x.ldb = b.row_stride_elems();
+        x.ldc = pass ? g.n : out.row_stride_elems();
+        const size_t tmp = q4_1_pass_bytes(g, q);
+        const size_t need = nnops_hip_gemm_fp_workspace_size(&x);
+        if ((need > 0 || tmp > 0) && (workspace == nullptr || ws_bytes < tmp + align_up(need))) {
+            return Status::not_initialized;
+        }
+        char* gemm_ws = static_cast<char*>(workspace) + tmp;
+        NnopsFpOutArgs fo = fp_pass_args(q, g, out, bias, workspace);
+        const int64_t a_mat = a_rows_per * a.pitch();
+        const int64_t b_mat = b_rows_per * b.pitch();
+        const int64_t c_mat = g.m * out.pitch();
+        for (int64_t bi = 0; bi < g.batch; ++bi) {
+            NnopsGemmFpArgs xb = x;
+            xb.a = a.ptr<const char>() + batch_offset(bi, g, g.a_batch, a_mat);
+            xb.b = b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat);
+            char* cb = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
+            xb.c = pass ? workspace : static_cast<void*>(cb);
+            const int rc = nnops_hip_gemm_fp(&xb, gemm_ws, need, stream);
             if (rc != NNOPS_OK) {
                 return from_code(rc);
             }
@@ -933,9 +1016,9 @@ Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const Tens
     if (attrs_.gated) {
         // nnops' gated form (src/ops/linear.cpp:63-107): Silu / Gelu / Relu /
         // Sigmoid / Tanh / None, no pre-activation residual, W [2N, K], bias
-        // [2N] of X's type, output [..., N]. Here over a q4_1 weight (blocks
-        // along K, the Linear form): nnops runs the gated form for fp
-        // weights of X's type only, which this library has no GEMM for.
+        // [2N] of X's type, output [..., N]: over a dense weight of X's type
+        // (nnops' rule, src/ops/linear.cpp:92), and here also over a q4_1
+        // weight (blocks along K, the Linear form).
         if (attrs_.add_to && attrs_.residual_pre_activation) {
             return Status::unsupported;
         }
@@ -950,8 +1033,8 @@ Status Linear::validate(std::span<const TensorDesc> inputs, std::span<const Tens
         default:
             return Status::unsupported;
         }
-        if ((x2.dtype != DataType::f32 && x2.dtype != DataType::f16) || w.dtype != DataType::q4_1 ||
-            w.layout != TensorLayout::Dense) {
+        if ((x2.dtype != DataType::f32 && x2.dtype != DataType::f16) ||
+            (w.dtype != DataType::q4_1 && w.dtype != x2.dtype) || w.layout != TensorLayout::Dense) {
             return Status::unsupported;
         }
         if (w.dims[0] <= 0 || (w.dims[0] % 2) != 0) {
@@ -1020,7 +1103,8 @@ Status Linear::compute(std::span<TensorView> outputs, std::span<const TensorView
     const TensorView& x = inputs[0];
     const TensorView& wv = inputs[1];
     TensorView& y = outputs[0];
-    if (!is_int8_matmul(x.data_type(), wv.data_type()) && !is_q4_1_matmul(x.data_type(), wv.data_type())) {
+    if (!is_int8_matmul(x.data_type(), wv.data_type()) && !is_q4_1_matmul(x.data_type(), wv.data_type()) &&
+        !is_dense_fp_pair(x.data_type(), wv.data_type())) {
         return Status::unsupported;  // nnops' Linear has no fp-activation x s8 route
     }
     if (y.data_type() != linear_out_dtype(attrs_, x.data_type(), wv.data_type()) &&

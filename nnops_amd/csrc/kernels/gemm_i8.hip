@@ -650,11 +650,16 @@ __device__ __forceinline__ void ring_coords(int tiles_m, int tiles_n, int& tm, i
     tn = in_group / gsize;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int NS, int MODE, bool FLIP>
+// F16: the operands are f16 (the same byte staging: K, lda and ldb in bytes,
+// a 16-byte lane fragment is 8 halves of v_mfma_f32_32x32x16_f16 as it is 16
+// int8 of v_mfma_i32_32x32x32_i8), the accumulators f32; RING_FP then writes
+// acc * s_a_scalar (alpha) and RING_PART the f32 partials' bits.
+template <int BM, int BN, int WM, int WN, int BK, int NS, int MODE, bool FLIP, bool F16 = false>
 __global__ __launch_bounds__(WM * WN * 64)
 __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 {
+    static_assert(!F16 || MODE == RING_FP || MODE == RING_PART, "f16 operands: fp or partial outputs");
     constexpr int W = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
@@ -720,9 +725,16 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     };
 
     // Accumulators (transposed layout); the fused modes start from bias[n].
-    v16i acc[FM][FN];
+    std::conditional_t<F16, v16f, v16i> acc[FM][FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+    for (int j = 0; j < FN && F16; ++j) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            acc[i][j] = std::conditional_t<F16, v16f, v16i>{0};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < FN && !F16; ++j) {
         int32_t b0[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -776,7 +788,13 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         for (int j = 0; j < FN; ++j) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+                if constexpr (F16) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fb[j]),
+                                                                      __builtin_bit_cast(v8h, fa[i]), acc[i][j], 0,
+                                                                      0, 0);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+                }
             }
         }
     };
@@ -1128,7 +1146,13 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                         v4i v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            v[e] = max(acc[i][j][4 * g + e], floor_v);
+                            if constexpr (F16) {
+                                // the f32 bits (bit-cast as a whole vector: a cast of
+                                // one subscripted element read element 0 here)
+                                v[e] = __builtin_bit_cast(v16i, acc[i][j])[4 * g + e];
+                            } else {
+                                v[e] = max(acc[i][j][4 * g + e], floor_v);
+                            }
                         }
                         *reinterpret_cast<v4i*>(crow + (int64_t)n * 4) = v;
                     }
@@ -1653,6 +1677,28 @@ __global__ __launch_bounds__(256) void transpose_i8(const int8_t* src, int64_t l
     }
 }
 
+// The same for 2-byte elements (an f16 [K][N] B staged as [N][Kp]).
+__global__ __launch_bounds__(256) void transpose_b16(const uint16_t* src, int64_t lds_, int R, int C,
+                                                    uint16_t* dst, int64_t ldd, int Rp)
+{
+    __shared__ uint16_t tile[64][65];
+    const int r0 = blockIdx.y * 64;
+    const int c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63;
+    const int ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        tile[i][tx] = (r < R && c < C) ? src[(int64_t)r * lds_ + c] : (uint16_t)0;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < C && r < Rp) {
+            dst[(int64_t)c * ldd + r] = tile[tx][i];
+        }
+    }
+}
+
 // out[r] = sum_k row r (u8 reads unsigned). One wave per row.
 __global__ __launch_bounds__(256) void rowsum_i8(const int8_t* src, int64_t ld, int R, int K, int u8,
                                                 int32_t* out)
@@ -1884,11 +1930,22 @@ void launch_gemm(const GemmI8Kern& k, bool aligned, bool fullk, int epi, hipStre
     }
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int NS>
+template <int BM, int BN, int WM, int WN, int BK, int NS, bool F16 = false>
 void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, hipStream_t s)
 {
     const unsigned blocks = (unsigned)(((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN) * sk.splits);
     const dim3 block(WM * WN * 64);
+    if constexpr (F16) {
+        (void)flip;
+        if (mode == RING_FP) {
+            hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false, true>), dim3(blocks), block, 0,
+                               s, k, sk);
+        } else {
+            hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false, true>), dim3(blocks), block,
+                               0, s, k, sk);
+        }
+        return;
+    }
     if (flip) {
         hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S8) {
@@ -1905,19 +1962,19 @@ void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool fli
 // 128-byte staged rows (whole cache lines: twice the bytes per L2 request of
 // 64-byte rows, which is what limits a CU's load rate) in 2 slots when K
 // allows, else 64-byte rows in 4 slots.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool F16 = false>
 void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode, bool flip, hipStream_t s)
 {
     if (bk == 128) {
-        // three slots where the LDS holds them (config 5's 192x128 tiles:
+        // three stage slots where the LDS holds them (config 5's 192x128 tiles:
         // 33.7 -> 32.9 us), two for the 256x256 tile
         if constexpr ((BM + BN) * 128 * 3 <= 160 * 1024 && BM + BN < 512) {
-            launch_ring_bk<BM, BN, WM, WN, 128, 3>(k, sk, mode, flip, s);
+            launch_ring_bk<BM, BN, WM, WN, 128, 3, F16>(k, sk, mode, flip, s);
         } else {
-            launch_ring_bk<BM, BN, WM, WN, 128, 2>(k, sk, mode, flip, s);
+            launch_ring_bk<BM, BN, WM, WN, 128, 2, F16>(k, sk, mode, flip, s);
         }
     } else if constexpr (BM % (16 * WM * WN) == 0 && BN % (16 * WM * WN) == 0) {
-        launch_ring_bk<BM, BN, WM, WN, 64, 4>(k, sk, mode, flip, s);
+        launch_ring_bk<BM, BN, WM, WN, 64, 4, F16>(k, sk, mode, flip, s);
     }
 }
 
@@ -1965,6 +2022,30 @@ void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t 
     launch_reduce(k, sk, s);
 }
 
+// C = alpha * (the f16 ring's f32 partials summed in split order)
+__global__ __launch_bounds__(256) void ring_f16_reduce(GemmI8Kern p, RingSplit sk)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)p.m * p.n) {
+        return;
+    }
+    const int64_t slab = (int64_t)p.m * p.n;
+    float v = 0.0f;
+    for (int sp = 0; sp < sk.splits; ++sp) {
+        v += __builtin_bit_cast(float, sk.part[sp * slab + i]);
+    }
+    v = __fmul_rn(v, p.ep.s_a_scalar);
+    const int m = (int)(i / p.n);
+    const int n = (int)(i - (int64_t)m * p.n);
+    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+    if (p.ep.out_kind == NNOPS_OUT_F16) {
+        reinterpret_cast<_Float16*>(crow)[n] = (_Float16)v;
+    } else {
+        reinterpret_cast<float*>(crow)[n] = v;
+    }
+}
+
+template <bool F16 = false>
 void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStream_t s)
 {
     RingSplit sk;
@@ -1973,18 +2054,23 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
     sk.part = part;
     const bool flip = k.a_xor != 0u;
     if (r.bm == 384) {
-        launch_ring_cfg<384, 128, 4, 2>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<384, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bm == 192) {
-        launch_ring_cfg<192, 128, 2, 4>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<192, 128, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bm == 128) {
-        launch_ring_cfg<128, 256, 2, 4>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<128, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
     } else if (r.bn == 128) {
-        launch_ring_cfg<256, 128, 4, 2>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<256, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, s);
     } else {
-        launch_ring_cfg<256, 256, 2, 4>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<256, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
     }
     if (r.mode == RING_PART) {
-        launch_reduce(k, sk, s);
+        if constexpr (F16) {
+            hipLaunchKernelGGL(ring_f16_reduce, dim3((unsigned)(((int64_t)k.m * k.n + 255) / 256)), dim3(256), 0, s,
+                               k, sk);
+        } else {
+            launch_reduce(k, sk, s);
+        }
     }
 }
 
@@ -2236,3 +2322,120 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     }
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
+
+// ---------------------------------------------------------------------------
+// The ring over f16 operands (nnops_hip_gemm_fp's large shapes): the same
+// byte staging, K and the row pitches in bytes; B [N][K] rows in place, or a
+// [K][N] B transposed into the workspace first. RING_FP writes alpha * acc
+// straight to C; K splits write f32 partials that ring_f16_reduce sums.
+// ---------------------------------------------------------------------------
+namespace nnops_amd {
+namespace {
+
+struct F16Plan {
+    RingPlan ring;          // mode < 0: the ring does not take the call
+    bool stage_b = false;
+    int64_t kp = 0;         // staged B row bytes
+    size_t part_off = 0, total = 0;
+};
+
+F16Plan plan_f16(const NnopsGemmFpArgs& g)
+{
+    F16Plan f;
+    if (!g.in_f16 || g.m < 64 || 2 * g.k > INT32_MAX || g.m > INT32_MAX || g.n > INT32_MAX) {
+        return f;
+    }
+    NnopsGemmI8Args x{};
+    x.m = g.m;
+    x.n = g.n;
+    x.k = 2 * g.k;
+    x.trans_b = 1;
+    x.a = g.a;
+    x.lda = 2 * g.lda;
+    x.c = g.c;
+    x.ldc = g.ldc;
+    x.out_kind = g.out_f16 ? NNOPS_OUT_F16 : NNOPS_OUT_F32;
+    x.act = NNOPS_ACT_NONE;
+    x.s_a_scalar = g.alpha;
+    x.s_b_scalar = 1.0f;
+    const int8_t* b = static_cast<const int8_t*>(g.b);
+    int64_t ldb = 2 * g.ldb;
+    size_t off = 0;
+    if (!g.trans_b) {
+        f.stage_b = true;
+        f.kp = (2 * g.k + 127) / 128 * 128;
+        off += align_up((size_t)g.n * (size_t)f.kp);
+        b = nullptr;          // the staged copy: 256-byte aligned, 128-byte rows
+        ldb = f.kp;
+    }
+    f.ring = plan_ring(x, static_cast<const int8_t*>(g.a), x.lda, b, ldb);
+    if (f.ring.mode != RING_FP && f.ring.mode != RING_PART) {
+        f.ring = RingPlan{};
+        return f;
+    }
+    if (f.ring.mode == RING_PART) {
+        f.part_off = off;
+        off += align_up((size_t)f.ring.splits * (size_t)g.m * (size_t)g.n * 4);
+    }
+    f.total = off;
+    return f;
+}
+
+}  // namespace
+
+bool ring_gemm_f16_ok(const NnopsGemmFpArgs& g)
+{
+    return plan_f16(g).ring.mode >= 0;
+}
+
+size_t ring_gemm_f16_workspace(const NnopsGemmFpArgs& g)
+{
+    // the destination's alignment (which a size query may not see) picks
+    // between the fused output and the split partials: room for either
+    NnopsGemmFpArgs x = g;
+    const size_t a = plan_f16(x).total;
+    x.c = reinterpret_cast<void*>(uintptr_t{2});
+    return std::max(a, plan_f16(x).total);
+}
+
+int ring_gemm_f16(const NnopsGemmFpArgs& g, void* workspace, size_t ws_bytes, hipStream_t s)
+{
+    const F16Plan f = plan_f16(g);
+    if (f.ring.mode < 0) {
+        return NNOPS_UNSUPPORTED;
+    }
+    if (f.total > 0 && (workspace == nullptr || ws_bytes < f.total || (uintptr_t)workspace % 16 != 0)) {
+        return NNOPS_NOT_INITIALIZED;
+    }
+    char* ws = static_cast<char*>(workspace);
+    GemmI8Kern k{};
+    k.m = (int)g.m;
+    k.n = (int)g.n;
+    k.k = (int)(2 * g.k);
+    k.a = static_cast<const int8_t*>(g.a);
+    k.lda = 2 * g.lda;
+    k.c = g.c;
+    k.ldc_bytes = g.ldc * (g.out_f16 ? 2 : 4);
+    if (f.stage_b) {
+        uint16_t* bt = reinterpret_cast<uint16_t*>(ws);
+        const dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((f.kp / 2 + 63) / 64));
+        hipLaunchKernelGGL(transpose_b16, grid, dim3(256), 0, s, static_cast<const uint16_t*>(g.b), g.ldb,
+                           (int)g.k, (int)g.n, bt, f.kp / 2, (int)(f.kp / 2));
+        k.b = reinterpret_cast<const int8_t*>(bt);
+        k.ldb = f.kp;
+    } else {
+        k.b = static_cast<const int8_t*>(g.b);
+        k.ldb = 2 * g.ldb;
+    }
+    EpiParams& e = k.ep;
+    e.s_a_scalar = g.alpha;
+    e.s_b_scalar = 1.0f;
+    e.out_kind = g.out_f16 ? NNOPS_OUT_F16 : NNOPS_OUT_F32;
+    e.act = NNOPS_ACT_NONE;
+    e.min_clip = -INFINITY;
+    e.max_clip = INFINITY;
+    launch_ring<true>(k, f.ring, reinterpret_cast<int32_t*>(ws + f.part_off), s);
+    return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+}
+
+}  // namespace nnops_amd

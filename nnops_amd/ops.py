@@ -305,6 +305,27 @@ def gemm_i8(a, b, c, *, trans_a=False, trans_b=False, bias=None, out_kind=L.OUT_
     return rc
 
 
+def gemm_fp(a, b, c, *, trans_b=True, alpha=1.0, workspace=None, stream=None, check=True):
+    """Direct call of nnops_hip_gemm_fp: ``a`` f32/f16 [M,K], ``b`` the same
+    type [N,K] (trans_b) or [K,N], ``c`` f32/f16 [M,N]: C = alpha A B."""
+    import torch
+    g = L.GemmFpArgs()
+    g.a, g.b, g.c = a.data_ptr(), b.data_ptr(), c.data_ptr()
+    g.m, g.k = a.shape
+    g.n = b.shape[0] if trans_b else b.shape[1]
+    g.lda, g.ldb, g.ldc = a.stride(0), b.stride(0), c.stride(0)
+    g.trans_b, g.in_f16 = int(trans_b), int(a.dtype == torch.float16)
+    g.out_f16, g.alpha = int(c.dtype == torch.float16), alpha
+    lib = L.lib()
+    need = lib.nnops_hip_gemm_fp_workspace_size(C.byref(g))
+    if workspace is None:
+        workspace = _workspace(need, a.device)
+    rc = lib.nnops_hip_gemm_fp(C.byref(g), _ptr(workspace), need, _stream_ptr(stream))
+    if check and rc != 0:
+        raise RuntimeError(f"nnops_hip_gemm_fp failed: status {rc}")
+    return rc
+
+
 def gemm_q4_1(a, b, c, *, n, trans_b=True, ldb_bytes=None, workspace=None, stream=None,
               check=True):
     """Direct call of nnops_hip_gemm_q4_1: ``a`` f16/f32 [M,K], ``b`` uint8 block

@@ -164,6 +164,14 @@ def cpu_lib():
                                                 C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,
                                                 C.c_int]
         _cpu.ref_cpu_matmul_q4_1_ep.restype = C.c_int
+        _cpu.ref_cpu_matmul_fp.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
+                                           C.c_int, C.c_int, C.c_int]
+        _cpu.ref_cpu_matmul_fp.restype = C.c_int
+        _cpu.ref_cpu_linear_fp.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                           C.c_int64, C.c_int64, C.c_int, C.c_float, C.c_float, C.c_float,
+                                           C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+                                           C.c_float, C.c_int]
+        _cpu.ref_cpu_linear_fp.restype = C.c_int
         _cpu.ref_cpu_linear_q4_1.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                              C.c_int64, C.c_int64, C.c_int, C.c_float, C.c_float, C.c_float,
                                              C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
@@ -267,6 +275,25 @@ def gemm_q4_1(a, blocks, n, *, trans_b=True, ldb_bytes=None, c_f16=False,
     p.m_begin, p.m_end = (rows if rows is not None else (0, 0))
     lib().orc_gemm_q4_1(C.byref(p))
     return c
+
+
+def gemm_fp(a, b, *, trans_b=True):
+    """Dense fp product of nnops' float routes (f32 x f32 or f16 x f16): the
+    exact products of the operands' values summed in float64, rounded once to
+    f32 (src/backend/cpu/matmul/matmul_small.cpp, matmul.cpp:57-198 compute
+    the same sum in f32; their f16 route also rounds to f16 every 128 k).
+    ``b``: [N, K] with trans_b, else [K, N]. Returns f32 [M, N]."""
+    a64 = np.asarray(a, dtype=np.float64)
+    b64 = np.asarray(b, dtype=np.float64)
+    return (a64 @ (b64.T if trans_b else b64)).astype(np.float32)
+
+
+def fp_linear(a, w, **pass_kw):
+    """Linear over a dense weight [n_w, K] of X's type: gemm_fp, then the fp
+    output pass (``pass_kw`` as fp_out_pass; gated: the weight's 2n rows)."""
+    acc = gemm_fp(a, w, trans_b=True)
+    n = w.shape[0] // 2 if pass_kw.get("gated") else w.shape[0]
+    return fp_out_pass(acc, n, **pass_kw)
 
 
 def fp_out_pass(src, n, *, out=None, out_f16=False, bias=None, act=ACT_NONE, act_alpha=0.0, act_beta=1.0,

@@ -254,17 +254,17 @@ int ref_cpu_matmul_q4_1_ep(const void* a, int a_f16, const uint8_t* w, const voi
 // linear.cpp:199-309) directly: the operator's validate admits the gated form
 // for fp weights of X's type only (src/ops/linear.cpp:92), and this is the
 // reference's own combine over the q4_1 GEMM for the HIP extension's parity.
-int ref_cpu_linear_q4_1(const void* x, int x_f16, const uint8_t* w, const void* bias, void* c, int64_t M,
-                        int64_t N2, int64_t K, int act, float act_alpha, float act_beta, float min_clip,
-                        float max_clip, int add_to, int residual_pre, int gated, int gate_act, float gate_alpha,
-                        float gate_beta, float gate_limit, int threads)
+static int linear_any(const void* x, int x_f16, const void* w, bool w_q4_1, const void* bias, void* c, int64_t M,
+                      int64_t N2, int64_t K, int act, float act_alpha, float act_beta, float min_clip,
+                      float max_clip, int add_to, int residual_pre, int gated, int gate_act, float gate_alpha,
+                      float gate_beta, float gate_limit, int threads)
 {
     Pool* p = pool_of(threads);
     const DataType dt = x_f16 ? DataType::f16 : DataType::f32;
     const int64_t N = gated ? N2 / 2 : N2;
     const int64_t xshape[] = {M, K}, wshape[] = {N2, K}, bshape[] = {N2}, cshape[] = {M, N};
     TensorView xv(xshape, dt, const_cast<void*>(x));
-    TensorView wv(wshape, DataType::q4_1, const_cast<uint8_t*>(w));
+    TensorView wv(wshape, w_q4_1 ? DataType::q4_1 : dt, const_cast<void*>(w));
     TensorView bv(bshape, dt, const_cast<void*>(bias));
     TensorView cv(cshape, dt, c);
     LinearAttributes attrs{};
@@ -284,6 +284,49 @@ int ref_cpu_linear_q4_1(const void* x, int x_f16, const uint8_t* w, const void* 
     const TensorView ins[] = {xv, wv, bv};
     const Status st = backend::cpu::linear_cpu(attrs, cv, std::span<const TensorView>(ins, bias ? 3 : 2), ctx,
                                                nullptr);
+    return static_cast<int>(st);
+}
+
+int ref_cpu_linear_q4_1(const void* x, int x_f16, const uint8_t* w, const void* bias, void* c, int64_t M,
+                        int64_t N2, int64_t K, int act, float act_alpha, float act_beta, float min_clip,
+                        float max_clip, int add_to, int residual_pre, int gated, int gate_act, float gate_alpha,
+                        float gate_beta, float gate_limit, int threads)
+{
+    return linear_any(x, x_f16, w, true, bias, c, M, N2, K, act, act_alpha, act_beta, min_clip, max_clip, add_to,
+                      residual_pre, gated, gate_act, gate_alpha, gate_beta, gate_limit, threads);
+}
+
+// The same Linear over a dense weight of X's type [N2, K] (nnops' own gated
+// route: src/ops/linear.cpp:92, linear_cpu's fp GEMM plus the combine).
+int ref_cpu_linear_fp(const void* x, int x_f16, const void* w, const void* bias, void* c, int64_t M, int64_t N2,
+                      int64_t K, int act, float act_alpha, float act_beta, float min_clip, float max_clip, int add_to,
+                      int residual_pre, int gated, int gate_act, float gate_alpha, float gate_beta, float gate_limit,
+                      int threads)
+{
+    return linear_any(x, x_f16, w, false, bias, c, M, N2, K, act, act_alpha, act_beta, min_clip, max_clip, add_to,
+                      residual_pre, gated, gate_act, gate_alpha, gate_beta, gate_limit, threads);
+}
+
+// nnops' dense float MatMul: f32 x f32 or f16 x f16 (f16), A [M, K], B
+// [N, K] (trans_b) or [K, N], C [M, N] of A's type (MatMul::create /
+// compute; matmul_small_fp or FpRoute<T> by shape).
+int ref_cpu_matmul_fp(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K, int trans_b, int f16,
+                      int threads)
+{
+    Pool* p = pool_of(threads);
+    const DataType dt = f16 ? DataType::f16 : DataType::f32;
+    const int64_t ashape[] = {M, K}, bshape_t[] = {N, K}, bshape[] = {K, N}, cshape[] = {M, N};
+    TensorView av(ashape, dt, const_cast<void*>(a));
+    TensorView bv(trans_b ? std::span<const int64_t>(bshape_t) : std::span<const int64_t>(bshape), dt,
+                  const_cast<void*>(b));
+    TensorView cv(cshape, dt, c);
+    MatMulAttributes attrs{};
+    attrs.transpose_b = trans_b != 0;
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {av, bv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 2), ctx);
     return static_cast<int>(st);
 }
 

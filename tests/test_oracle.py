@@ -562,3 +562,74 @@ def test_oracle_matmul_order_matches_nnops_matmul(f16, M, trans_b, kw):
         bad = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, matmul_order=True,
                                  **swapped).astype(np.float64)
         assert np.max(np.abs(want - bad)) / np.sqrt(np.mean(want ** 2)) > 1e-2
+
+
+# ---------------------------------------------------------------------------
+# The dense fp product (f32 x f32, f16 x f16) against nnops' own CPU MatMul:
+# the oracle sums exact products in float64. f32: within 2e-5 of the rms
+# (nnops' f32 summation order). f16: nnops keeps its accumulator in f16
+# between 128-deep k blocks and rounds the output to f16, so K = 256 carries
+# two f16 roundings of partial sums: within 4e-3. M = 3 takes nnops' GEMV
+# route, M = 40 its packed FpRoute.
+# ---------------------------------------------------------------------------
+@cpu_only
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("M,trans_b", [(3, True), (3, False), (40, True), (40, False)])
+def test_oracle_dense_fp_matches_nnops_matmul(f16, M, trans_b):
+    dt = np.float16 if f16 else np.float32
+    K, N = 256, 72
+    a = dg.normal(31 + M, (M, K)).astype(dt)
+    b = dg.normal(32, (N, K) if trans_b else (K, N)).astype(dt)
+    c = np.zeros((M, N), dtype=dt)
+    rc = oracle.cpu_lib().ref_cpu_matmul_fp(a.ctypes.data, b.ctypes.data, c.ctypes.data, M, N, K, int(trans_b),
+                                            int(f16), 4)
+    assert rc == 0, rc
+    want = c.astype(np.float64)
+    got = oracle.gemm_fp(a, b, trans_b=trans_b).astype(np.float64)
+    err = np.max(np.abs(want - got)) / np.sqrt(np.mean(want ** 2))
+    assert err <= (4e-3 if f16 else 2e-5), err
+    # a transposed operand or a dropped k block moves the result far past it
+    bad = oracle.gemm_fp(a[:, :128], b[:, :128] if trans_b else b[:128], trans_b=trans_b).astype(np.float64)
+    assert np.max(np.abs(want - bad)) / np.sqrt(np.mean(want ** 2)) > 0.1
+
+
+@cpu_only
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("kw", GATED_CASES + PASS_CASES[:3])
+def test_oracle_fp_linear_matches_nnops_linear(f16, kw):
+    """Linear over a dense weight of X's type (nnops' own gated route), the
+    oracle's gemm_fp + fp_out_pass against nnops' linear_cpu. f32 within
+    2e-5 of the rms; f16 within 6e-3: nnops' f16 product and its per-operation
+    f16 combine (the q4_1 test's 4e-3) plus the f16 rounding of its [rows, 2N]
+    product tile. Swapping the gate and value halves fails by far."""
+    dt = np.float16 if f16 else np.float32
+    M, K, N2 = 3, 256, 104
+    gated = kw.get("gated", False)
+    n = N2 // 2 if gated else N2
+    x = dg.normal(41, (M, K)).astype(dt)
+    w = (0.1 * dg.normal(42, (N2, K))).astype(dt)
+    bias = dg.normal(43, (N2,)).astype(dt)
+    old = dg.normal(44, (M, n)).astype(dt) if kw.get("add_to") else None
+    c = np.zeros((M, n), dtype=dt) if old is None else old.copy()
+    rc = oracle.cpu_lib().ref_cpu_linear_fp(
+        x.ctypes.data, int(f16), w.ctypes.data, bias.ctypes.data, c.ctypes.data, M, N2, K, kw.get("act", 0),
+        kw.get("act_alpha", 0.0), kw.get("act_beta", 1.0), kw.get("min_clip", -np.inf), kw.get("max_clip", np.inf),
+        int(kw.get("add_to", False)), int(kw.get("residual_pre", False)), int(gated),
+        kw.get("gate_act", oracle.ACT_SILU), kw.get("gate_alpha", 1.0), kw.get("gate_beta", 0.0),
+        kw.get("gate_limit", np.inf), 4)
+    assert rc == 0, rc
+    want = c.astype(np.float64)
+    okw = {k: v for k, v in kw.items() if k != "gated"}
+    if kw.get("add_to") and not gated:
+        active = kw.get("act", 0) != 0 or np.isfinite(kw.get("min_clip", -np.inf)) or \
+            np.isfinite(kw.get("max_clip", np.inf))
+        okw["residual_pre"] = kw.get("residual_pre", False) or not active
+    got = oracle.fp_linear(x, w, gated=gated, out_f16=f16, bias=bias, out=old, **okw).astype(np.float64)
+    err = np.max(np.abs(want - got)) / np.sqrt(np.mean(want ** 2))
+    assert err <= (6e-3 if f16 else 2e-5), err
+    if gated and not (kw.get("gate_act") == oracle.ACT_NONE and kw.get("gate_beta", 0.0) == 0.0):
+        # (an identity gate with no beta is symmetric in the halves)
+        ws = np.concatenate([w[n:], w[:n]])
+        bs = np.concatenate([bias[n:], bias[:n]])
+        bad = oracle.fp_linear(x, ws, gated=True, out_f16=f16, bias=bs, out=old, **okw).astype(np.float64)
+        assert np.max(np.abs(want - bad)) / np.sqrt(np.mean(want ** 2)) > 0.05
