@@ -9,11 +9,11 @@
 // pass of fp_out.hip over this product.
 //
 // Kernels
-//   gemv_fp_nk<AF16,MT>   M <= 4 rows of A per launch, B [N][K] rows (the
+//   gemv_fp_nk<AF16,MT>   M <= 16 rows of A in one launch, B [N][K] rows (the
 //                         Linear weight): a wave owns 4 rows of B, its lanes
 //                         stride 16-byte chunks over K, A read from L2; the
 //                         lanes' sums meet by shuffles. Bound: HBM.
-//   gemv_fp_kn<AF16,MT>   M <= 4, B [K][N]: a thread owns one 16-byte column
+//   gemv_fp_kn<AF16,MT>   M <= 16, B [K][N]: a thread owns one 16-byte column
 //                         chunk (8 f16 / 4 f32 columns) over a K range; A
 //                         through the scalar cache; K split over blockIdx.y
 //                         into f32 partials summed by fp_split_sum. Bound: HBM.
@@ -95,8 +95,10 @@ __device__ __forceinline__ void unpack16(v4i x, float (&f)[Chunk<AF16>::E])
 
 // ---------------------------------------------------------------------------
 // GEMV over B [N][K]: wave w of the block owns rows n0 .. n0 + 3; lane l takes
-// chunks l, l + 64, ... of each row (16 bytes each). VEC: 16-byte aligned
-// rows of A and B, K a whole number of chunks; otherwise element loads.
+// chunks l, l + 64, ... of each row (16 bytes each), A's MT rows kept packed
+// (one 16-byte chunk per row of A); f16 pairs are dotted with v_dot2_f32_f16
+// (exact products, f32 sums), f32 with fma. VEC: 16-byte aligned rows of A and
+// B, K a whole number of chunks; otherwise element loads.
 // ---------------------------------------------------------------------------
 template <bool AF16, int MT, bool VEC>
 __global__ __launch_bounds__(256) void gemv_fp_nk(FpKern p)
@@ -117,40 +119,53 @@ __global__ __launch_bounds__(256) void gemv_fp_nk(FpKern p)
             acc[r][m] = 0.0f;
         }
     }
-    for (int c = lane; c < chunks; c += 64) {
-        const int k0 = c * E;
-        float av[MT][E];
+    // 16 bytes of row `row` of X from element k0 (zeros past K)
+    auto chunk16 = [&](const void* x, int64_t ld, int64_t row, int k0) {
+        if constexpr (VEC) {
+            return *reinterpret_cast<const v4i*>(static_cast<const char*>(x) + (row * ld + k0) * (AF16 ? 2 : 4));
+        } else {
+            uint32_t w[4];
+            if constexpr (AF16) {
+                const uint16_t* src = static_cast<const uint16_t*>(x) + row * ld + k0;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const int mm = min(m, p.m - 1);
-            if constexpr (VEC) {
-                const char* src = static_cast<const char*>(p.a) + ((int64_t)mm * p.lda + k0) * (AF16 ? 2 : 4);
-                unpack16<AF16>(*reinterpret_cast<const v4i*>(src), av[m]);
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t lo = k0 + 2 * q < p.k ? src[2 * q] : 0u;
+                    const uint32_t hi = k0 + 2 * q + 1 < p.k ? src[2 * q + 1] : 0u;
+                    w[q] = lo | (hi << 16);
+                }
             } else {
+                const uint32_t* src = static_cast<const uint32_t*>(x) + row * ld + k0;
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    av[m][e] = k0 + e < p.k ? ld1<AF16>(p.a, (int64_t)mm * p.lda + k0 + e) : 0.0f;
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = k0 + q < p.k ? src[q] : 0u;
                 }
             }
+            return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        }
+    };
+    for (int c = lane; c < chunks; c += 64) {
+        const int k0 = c * E;
+        v4i av[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            av[m] = chunk16(p.a, p.lda, min(m, p.m - 1), k0);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = min(n0 + r, p.n - 1);
-            float bv[E];
-            if constexpr (VEC) {
-                const char* src = static_cast<const char*>(p.b) + ((int64_t)n * p.ldb + k0) * (AF16 ? 2 : 4);
-                unpack16<AF16>(*reinterpret_cast<const v4i*>(src), bv);
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    bv[e] = k0 + e < p.k ? ld1<AF16>(p.b, (int64_t)n * p.ldb + k0 + e) : 0.0f;
-                }
-            }
+            const v4i bv = chunk16(p.b, p.ldb, min(n0 + r, p.n - 1), k0);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    acc[r][m] = fmaf(av[m][e], bv[e], acc[r][m]);
+                for (int q = 0; q < 4; ++q) {
+                    // the words as scalars first: a bit cast of a subscripted
+                    // vector element reads element 0 with this compiler
+                    const uint32_t aw = (uint32_t)av[m][q], bw = (uint32_t)bv[q];
+                    if constexpr (AF16) {
+                        acc[r][m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, aw), __builtin_bit_cast(v2h, bw),
+                                                           acc[r][m], false);
+                    } else {
+                        acc[r][m] = fmaf(__builtin_bit_cast(float, aw), __builtin_bit_cast(float, bw), acc[r][m]);
+                    }
                 }
             }
         }
@@ -453,7 +468,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp_tile(FpKern p)
     }
 }
 
-constexpr int kGemvRows = 4;     // rows of A per GEMV launch
+constexpr int kGemvRows = 16;    // rows of A per GEMV launch
 constexpr int64_t kGemvMaxM = 16;
 
 // K split of the [K][N] GEMV: about 512 workgroups, at least 64 rows each
@@ -469,7 +484,7 @@ template <bool AF16, int MT>
 void launch_gemv(const FpKern& k, bool tb, bool vec, hipStream_t s)
 {
     if (tb) {
-        const dim3 grid((unsigned)((k.n + 4 * kGemvRows - 1) / (4 * kGemvRows)));
+        const dim3 grid((unsigned)((k.n + 15) / 16));      // 4 waves of 4 rows of B
         if (vec) {
             hipLaunchKernelGGL((gemv_fp_nk<AF16, MT, true>), grid, dim3(256), 0, s, k);
         } else {
@@ -489,11 +504,16 @@ void launch_gemv(const FpKern& k, bool tb, bool vec, hipStream_t s)
 template <bool AF16>
 void launch_gemv_rows(const FpKern& k, bool tb, bool vec, hipStream_t s)
 {
-    switch (k.m) {
-    case 1: launch_gemv<AF16, 1>(k, tb, vec, s); break;
-    case 2: launch_gemv<AF16, 2>(k, tb, vec, s); break;
-    case 3: launch_gemv<AF16, 3>(k, tb, vec, s); break;
-    default: launch_gemv<AF16, 4>(k, tb, vec, s); break;
+    if (k.m == 1) {
+        launch_gemv<AF16, 1>(k, tb, vec, s);
+    } else if (k.m == 2) {
+        launch_gemv<AF16, 2>(k, tb, vec, s);
+    } else if (k.m <= 4) {
+        launch_gemv<AF16, 4>(k, tb, vec, s);
+    } else if (k.m <= 8) {
+        launch_gemv<AF16, 8>(k, tb, vec, s);
+    } else {
+        launch_gemv<AF16, 16>(k, tb, vec, s);
     }
 }
 

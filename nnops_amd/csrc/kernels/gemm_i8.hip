@@ -2373,6 +2373,17 @@ F16Plan plan_f16(const NnopsGemmFpArgs& g)
         f.ring = RingPlan{};
         return f;
     }
+    // f32 partials cost 8 bytes of traffic per output and split: where
+    // 128 x 256 tiles alone nearly fill the CUs, take them unsplit (512 x
+    // 14336 x 4096: 89.6 us split in two over 256 x 256 tiles)
+    const int64_t tiles128 = ((g.m + 127) / 128) * ((g.n + 255) / 256);
+    const bool c_ok = (uintptr_t)g.c % 16 == 0 && (g.ldc * (g.out_f16 ? 2 : 4)) % 16 == 0;
+    if (f.ring.splits > 1 && g.m > 128 && tiles128 >= 192 && c_ok) {
+        f.ring.bm = 128;
+        f.ring.bn = 256;
+        f.ring.splits = 1;
+        f.ring.mode = RING_FP;
+    }
     if (f.ring.mode == RING_PART) {
         f.part_off = off;
         off += align_up((size_t)f.ring.splits * (size_t)g.m * (size_t)g.n * 4);
