@@ -39,7 +39,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg4", "cfg4_gemm", "cfg5",
-                                                           "gated_ffn", "copy", "ceilings", "vendor"])
+                                                           "gated_ffn", "dense", "copy", "ceilings", "vendor"])
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline of the headline config")
@@ -534,6 +534,39 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
                                        "(src/backend/cpu/matmul/linear.cpp:226) nor a GELU on an integer one"}}
 
 
+def dense_fp_case(torch, dg, na, stream, steps, warmup, M, N=4096, K=4096, f16=True, nbuf=1):
+    """nnops' dense float route (MatMul f16 x f16 or f32 x f32, B [N, K]):
+    C = A B with f32 accumulation. M <= 16 rotates over nbuf weights (more
+    than the MALL) so HBM is measured."""
+    dt = torch.float16 if f16 else torch.float32
+    npdt = "float16" if f16 else "float32"
+    a = torch.from_numpy(dg.normal(440 + M, (M, K)).astype(npdt)).cuda()
+    base = torch.from_numpy(dg.normal(441, (N, K)).astype(npdt)).cuda()
+    bs = [base] + [torch.roll(base, shifts=i, dims=1).contiguous() for i in range(1, nbuf)]
+    c = torch.empty((M, N), dtype=dt, device="cuda")
+    s = stream.cuda_stream
+    # room for any plan's partials (split K, or an unaligned destination)
+    ws = torch.empty(4 * M * N + (1 << 20), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def step():
+        na.gemm_fp(a, bs[it[0] % nbuf], c, trans_b=True, workspace=ws, stream=s)
+        it[0] += 1
+    t = Timer(stream).time(step, steps, warmup)
+    es = 2 if f16 else 4
+    by = N * K * es + M * K * es + M * N * es
+    fl = 2.0 * M * N * K
+    out = {"us": t["mean_ms"] * 1e3, "M": M, "K": K, "N": N, "dtype": npdt, "weight_layout": "[N,K]",
+           "timing": t["timing"], "tflops": fl / (t["mean_ms"] * 1e-3) / 1e12,
+           "gbs": by / (t["mean_ms"] * 1e-3) / 1e9}
+    if M <= 16:
+        out["frac_hbm"] = out["gbs"] / PEAK_HBM_GBS
+        out["bytes"] = by
+    else:
+        out["frac_mfma"] = out["tflops"] / (PEAK_F16_TFLOPS if f16 else PEAK_F32_TFLOPS)
+    return out
+
+
 def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False):
     """QuantizeLinear f16 [R,C] -> s8 (per-token scales and zero points), or
     DequantizeLinear s8 -> f16, through the operator API. HBM-bound."""
@@ -763,6 +796,10 @@ def main():
                "cfg4_gemm": lambda: {"blocks_along_k": q41_gemm_case(torch, dg, na, stream, args.steps, args.warmup),
                                      "blocks_along_n": q41_gemm_case(torch, dg, na, stream, args.steps, args.warmup,
                                                                      trans_b=False)},
+               "dense": lambda: {"f16_gemm_4096": dense_fp_case(torch, dg, na, stream, args.steps, args.warmup,
+                                                                 M=4096),
+                                 "f16_gemv_m1": dense_fp_case(torch, dg, na, stream, args.steps, args.warmup, M=1,
+                                                              N=14336, nbuf=4)},
                "gated_ffn": lambda: {"m1": gated_ffn_case(torch, dg, na, stream, args.steps, args.warmup),
                                      "m512": gated_ffn_case(torch, dg, na, stream, args.steps, args.warmup,
                                                             M=512)},
@@ -798,6 +835,9 @@ def main():
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, few, wu)
         secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, few, wu, dq_only=True)
         secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, few, wu)
+        secondary["dense_f16_gemm_4096"] = dense_fp_case(torch, dg, na, stream, few, wu, M=4096)
+        secondary["dense_f16_gemv_m1_14336x4096"] = dense_fp_case(torch, dg, na, stream, st, wu, M=1, N=14336,
+                                                                   nbuf=4)
         secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu)
         secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu, dequant=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
