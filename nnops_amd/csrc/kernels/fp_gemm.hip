@@ -13,10 +13,11 @@
 //                         Linear weight): a wave owns 4 rows of B, its lanes
 //                         stride 16-byte chunks over K, A read from L2; the
 //                         lanes' sums meet by shuffles. Bound: HBM.
-//   gemv_fp_kn<AF16,MT>   M <= 16, B [K][N]: a thread owns one 16-byte column
-//                         chunk (8 f16 / 4 f32 columns) over a K range; A
-//                         through the scalar cache; K split over blockIdx.y
-//                         into f32 partials summed by fp_split_sum. Bound: HBM.
+//   gemv_fp_kn<AF16,MT>   M <= 16, B [K][N]: a lane owns one 16-byte column
+//                         chunk (8 f16 / 4 f32 columns), the block's 4 waves
+//                         quarters of its K range (met in LDS); A through the
+//                         scalar cache; K split over blockIdx.y into f32
+//                         partials summed by fp_split_sum. Bound: HBM.
 //   gemm_fp_tile<AF16,TB> the other shapes: 128 x 128 tiles, 4 waves of
 //                         64 x 64, v_mfma_f32_32x32x2f32 with A and B staged
 //                         in LDS as f32 (32-deep k stages). Bound: f32 MFMA.
@@ -196,10 +197,12 @@ __global__ __launch_bounds__(256) void gemv_fp_nk(FpKern p)
 }
 
 // ---------------------------------------------------------------------------
-// GEMV over B [K][N]: thread t of block (bx, split) owns the 16-byte column
-// chunk bx * 256 + t (E columns) for rows [split * kper, + kper). A's rows
-// are wave-uniform: read through the scalar cache. VEC: 16-byte aligned B
-// rows and N a whole number of chunks; otherwise element loads.
+// GEMV over B [K][N]: block (bx, split) owns the 64 16-byte column chunks
+// bx * 64 .. + 63 (one per lane, E columns each) for rows [split * kper,
+// + kper); its 4 waves take a quarter of those rows each and meet in LDS, so
+// a split writes one partial per output. A's rows are wave-uniform: read
+// through the scalar cache. VEC: 16-byte aligned B rows and N a whole number
+// of chunks; otherwise element loads.
 // ---------------------------------------------------------------------------
 template <bool AF16, int MT, bool VEC>
 __global__ __launch_bounds__(256) void gemv_fp_kn(FpKern p)
@@ -207,10 +210,15 @@ __global__ __launch_bounds__(256) void gemv_fp_kn(FpKern p)
     constexpr int E = Chunk<AF16>::E;
     typedef std::conditional_t<AF16, _Float16, float> T;
     typedef const __attribute__((address_space(4))) T* ConstT;
-    const int chunk = blockIdx.x * 256 + threadIdx.x;
-    const int c0 = chunk * E;
-    const int k0 = blockIdx.y * p.kper;
-    const int k1 = min(p.k, k0 + p.kper);
+    __shared__ float red[3][E][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c0 = (blockIdx.x * 64 + lane) * E;
+    const int ks = blockIdx.y * p.kper;
+    const int ke = min(p.k, ks + p.kper);
+    const int kq = (ke - ks + 3) / 4;
+    const int k0 = ks + wave * kq;
+    const int k1 = min(ke, k0 + kq);
     float acc[MT][E];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -225,21 +233,24 @@ __global__ __launch_bounds__(256) void gemv_fp_kn(FpKern p)
         arow[m] = (ConstT)(static_cast<const T*>(p.a) + (int64_t)min(m, p.m - 1) * p.lda);
     }
     const int cc = min(c0, (p.n - 1) / E * E);   // a chunk past N re-reads the last one (never stored)
+    auto load_row = [&](int k, float (&bv)[E]) {
+        if constexpr (VEC) {
+            const char* src = static_cast<const char*>(p.b) + ((int64_t)k * p.ldb + cc) * (AF16 ? 2 : 4);
+            unpack16<AF16>(*reinterpret_cast<const v4i*>(src), bv);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                bv[e] = cc + e < p.n ? ld1<AF16>(p.b, (int64_t)k * p.ldb + cc + e) : 0.0f;
+            }
+        }
+    };
     constexpr int U = 4;
     int k = k0;
     for (; k + U <= k1; k += U) {
         float bv[U][E];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if constexpr (VEC) {
-                const char* src = static_cast<const char*>(p.b) + ((int64_t)(k + u) * p.ldb + cc) * (AF16 ? 2 : 4);
-                unpack16<AF16>(*reinterpret_cast<const v4i*>(src), bv[u]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    bv[u][e] = cc + e < p.n ? ld1<AF16>(p.b, (int64_t)(k + u) * p.ldb + cc + e) : 0.0f;
-                }
-            }
+            load_row(k + u, bv[u]);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -255,15 +266,7 @@ __global__ __launch_bounds__(256) void gemv_fp_kn(FpKern p)
     }
     for (; k < k1; ++k) {
         float bv[E];
-        if constexpr (VEC) {
-            const char* src = static_cast<const char*>(p.b) + ((int64_t)k * p.ldb + cc) * (AF16 ? 2 : 4);
-            unpack16<AF16>(*reinterpret_cast<const v4i*>(src), bv);
-        } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                bv[e] = cc + e < p.n ? ld1<AF16>(p.b, (int64_t)k * p.ldb + cc + e) : 0.0f;
-            }
-        }
+        load_row(k, bv);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const float a = (float)arow[m][k];
@@ -273,28 +276,35 @@ __global__ __launch_bounds__(256) void gemv_fp_kn(FpKern p)
             }
         }
     }
-    if (c0 >= p.n) {
-        return;
-    }
+    // the four quarters meet in LDS (wave order), one row of A at a time
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        if (m >= p.m) {
-            continue;
-        }
+        if (wave > 0) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            if (c0 + e < p.n) {
-                if (p.part != nullptr) {
-                    p.part[((int64_t)blockIdx.y * p.m + m) * p.n + c0 + e] = acc[m][e];
-                } else {
-                    st_out(p, m, c0 + e, acc[m][e] * p.alpha);
+            for (int e = 0; e < E; ++e) {
+                red[wave - 1][e][lane] = acc[m][e];
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && m < p.m && c0 < p.n) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float v = ((acc[m][e] + red[0][e][lane]) + red[1][e][lane]) + red[2][e][lane];
+                if (c0 + e < p.n) {
+                    if (p.part != nullptr) {
+                        p.part[((int64_t)blockIdx.y * p.m + m) * p.n + c0 + e] = v;
+                    } else {
+                        st_out(p, m, c0 + e, v * p.alpha);
+                    }
                 }
             }
         }
+        __syncthreads();
     }
 }
 
-// C = alpha * sum of the splits (split order), one thread per output.
+// C = alpha * sum of the splits (split order): one thread per output, its
+// loads issued 8 splits at a time.
 __global__ __launch_bounds__(256) void fp_split_sum(FpKern p)
 {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -303,7 +313,19 @@ __global__ __launch_bounds__(256) void fp_split_sum(FpKern p)
     }
     const int64_t slab = (int64_t)p.m * p.n;
     float s = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp) {
+    int sp = 0;
+    for (; sp + 8 <= p.splits; sp += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            v[u] = p.part[(sp + u) * slab + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            s += v[u];
+        }
+    }
+    for (; sp < p.splits; ++sp) {
         s += p.part[sp * slab + i];
     }
     const int m = (int)(i / p.n);
@@ -472,11 +494,13 @@ constexpr int kGemvRows = 16;    // rows of A per GEMV launch
 constexpr int64_t kGemvMaxM = 16;
 
 // K split of the [K][N] GEMV: about 512 workgroups, at least 64 rows each
+// K split of the [K][N] GEMV: about 512 workgroups (each 1 KiB of columns),
+// at least 128 rows (32 per wave) per split
 int kn_splits_fp(int64_t n, int64_t k, bool f16)
 {
-    const int64_t blocks = (n + (f16 ? 8 : 4) * 256 - 1) / ((f16 ? 8 : 4) * 256);
+    const int64_t blocks = (n + (f16 ? 8 : 4) * 64 - 1) / ((f16 ? 8 : 4) * 64);
     int64_t s = (512 + blocks - 1) / blocks;
-    s = std::min<int64_t>(s, std::max<int64_t>(1, k / 64));
+    s = std::min<int64_t>(s, std::max<int64_t>(1, k / 128));
     return (int)std::max<int64_t>(1, std::min<int64_t>(s, 1024));
 }
 
@@ -492,7 +516,7 @@ void launch_gemv(const FpKern& k, bool tb, bool vec, hipStream_t s)
         }
     } else {
         const int e = AF16 ? 8 : 4;
-        const dim3 grid((unsigned)((k.n + 256 * e - 1) / (256 * e)), (unsigned)k.splits);
+        const dim3 grid((unsigned)((k.n + 64 * e - 1) / (64 * e)), (unsigned)k.splits);
         if (vec) {
             hipLaunchKernelGGL((gemv_fp_kn<AF16, MT, true>), grid, dim3(256), 0, s, k);
         } else {
