@@ -84,3 +84,41 @@ def test_quantize_linear_under_graph_replay():
     def fn(s):
         assert op.compute(outs, ins, stream=s) == na.OK
     graph_replays_match(fn, q)
+
+
+@pytest.mark.parametrize("M,K,N,trans_b", [(1, 4096, 2048, False), (4, 4096, 2048, True), (512, 4096, 1024, True),
+                                           (1024, 256, 2048, False), (300, 1000, 200, True)])
+def test_dense_fp_under_graph_replay(M, K, N, trans_b):
+    """The dense f16 product: the [K,N] GEMV's split partials and their sum,
+    the ring's split partials and reduce, the ring over a B transposed into
+    the workspace, and the f32-MFMA tile kernel."""
+    import torch
+    announce(f"graph dense f16 {M}x{K}x{N} trans_b={trans_b}")
+    a = dev(dg.normal(11 + M, (M, K)).astype(np.float16))
+    b = dev(dg.normal(12, (N, K) if trans_b else (K, N)).astype(np.float16))
+    c = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+
+    def fn(s):
+        na.gemm_fp(a, b, c, trans_b=trans_b, workspace=ws, stream=s.cuda_stream)
+    graph_replays_match(fn, c)
+
+
+def test_linear_gated_dense_under_graph_replay():
+    """Linear's gated form over a dense f16 weight: the product staged in the
+    workspace, then the output pass."""
+    import torch
+    announce("graph linear gated dense")
+    M, K, N = 64, 1024, 512
+    x = dev(dg.normal(13, (M, K)).astype(np.float16))
+    w = dev((0.05 * dg.normal(14, (2 * N, K))).astype(np.float16))
+    bias = dev((0.1 * dg.normal(15, (2 * N,))).astype(np.float16))
+    y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    op = na.Linear(gated=True, gate_activation=na.EP_SILU)
+    ins = [na.tensor(x), na.tensor(w), na.tensor(bias)]
+    outs = [na.tensor(y)]
+    ws = torch.empty(max(op.workspace_size(ins, outs), 1), dtype=torch.uint8, device="cuda")
+
+    def fn(s):
+        assert op.compute(outs, ins, stream=s, workspace=ws) == na.OK
+    graph_replays_match(fn, y)
