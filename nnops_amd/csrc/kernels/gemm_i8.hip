@@ -885,7 +885,13 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         const int32_t lo_i = (u8 ? 0 : -128) - ep.zp_out;
         const int32_t hi_i = (u8 ? 255 : 127) - ep.zp_out;
         const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
-        int8_t* stage8 = ring + wave * (TM * kPitch8);   // this wave's [TM][TN] byte tile
+        // the whole [BM][BN] byte tile staged at once where the ring holds it,
+        // so the stores are whole rows of the tile (BN bytes: whole 128-byte
+        // lines) rather than each wave's TN-byte segments
+        constexpr int kWholeP = BN + 16;
+        constexpr bool kWhole = BM * kWholeP <= NS * kStage && (BN % 128) == 0 && (BM * BN / 16) % (W * 64) == 0;
+        constexpr int kSP = kWhole ? kWholeP : kPitch8;
+        int8_t* stage8 = kWhole ? ring + wm0 * kSP + wn0 : ring + wave * (TM * kPitch8);
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -916,9 +922,25 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                     }
                     const uint32_t w = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
                                        __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
-                    *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kPitch8 + nl) = w;
+                    *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kSP + nl) = w;
                 }
             }
+        }
+        if constexpr (kWhole) {
+            __syncthreads();
+            // 16-byte chunks of whole tile rows, wave w taking rows w, w + W, ...
+            constexpr int CPRW = BN / 16;
+#pragma unroll
+            for (int q = 0; q < BM * CPRW / (W * 64); ++q) {
+                const int idx = (q * W + wave) * 64 + lane, r = idx / CPRW, c = idx % CPRW;
+                const int m = m0 + r, n = n0 + c * 16;
+                const v4i v = *reinterpret_cast<const v4i*>(ring + r * kSP + c * 16);
+                if (m < p.m && n < p.n) {
+                    char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + n;
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(cptr));
+                }
+            }
+            return;
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
