@@ -1274,6 +1274,133 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
 }
 
 // ---------------------------------------------------------------------------
+// Skinny GEMM, blocks along K ([N][K/32]), f16 A with 3 <= M <= 16 rows per
+// launch (more rows: one launch per 16), K % 256 == 0: the weight streams
+// once, its blocks decoded to f16 and multiplied on the matrix cores.
+//
+// A workgroup of two waves owns 32 weight rows, 16 per wave, and runs the
+// whole K in stages of 8 blocks (256 k), NS stages in flight. A stage is
+// three DMA regions in LDS:
+//   weights  per wave 16 rows x 176 bytes: the rows' 160 stage bytes (10
+//            16-byte chunks) plus a pad chunk, so the 16 rows a read serves
+//            fall on 16 distinct bank groups (176 bytes = 44 dwords per row);
+//   A        16 rows x 528 bytes, shared by the two waves: the stage's 256
+//            halves plus a pad chunk (132 dwords per row: a 16-byte read per
+//            row of 16 rows covers the 64 banks once).
+// The pads come from the DMA itself: lane i of piece q writes 16 bytes at
+// q * 1024 + 16 i, so chunk c = 64 q + i is given row c / 11, column c % 11
+// (c / 33, c % 33 for A), and a pad or surplus chunk re-reads a valid one.
+// Each wave issues its rows and half of A's pieces; a stage is read after
+// every wave has waited for its own pieces and passed the block barrier.
+// Per block, lane l decodes the 8 values of row l % 16 at k = 8 (l / 16) ..
+// + 7 (low or high nibbles of bytes 0-7 or 8-15): a byte permute and
+// v_and_or_b32 make (1024 + q) f16 pairs, v_pk_add_f16 removes 1024 exactly
+// and v_pk_fma_f16 rounds d * q + m once; the 16 x 32 weight tile and A's
+// 32 x 16 tile (lane l: row l % 16, the same 8 k) meet in one
+// v_mfma_f32_16x16x32_f16. Bound: HBM (the weight once, A once per 32 rows).
+// ---------------------------------------------------------------------------
+constexpr int kSkRows = 32;                          // per workgroup (16 per wave)
+constexpr int kSkWChunks = 11;                       // per weight row: 10 + pad
+constexpr int kSkWPieces = (16 * kSkWChunks + 63) / 64;        // 3 per wave
+constexpr int kSkAChunks = 33;                       // per row of A: 32 + pad
+constexpr int kSkAPieces = 10;                       // 16 x 33 = 528 chunks, in 2 x 5 pieces
+constexpr int kSkL = kSkWPieces + kSkAPieces / 2;    // DMA instructions per wave and stage
+constexpr int kSkAAt = 2 * kSkWPieces * 1024;
+constexpr int kSkStage = kSkAAt + kSkAPieces * 1024;
+
+template <int NS>
+__global__ __launch_bounds__(128) void gemv_q4_1_skinny(Q41Kern p)
+{
+    static_assert(NS >= 2 && (NS - 2) * kSkL < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kSkStage];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * kSkRows + 16 * wave;
+    const int rows = max(1, min(16, p.n - n0));      // a wave past N re-reads row N - 1 (never stored)
+    const int stages = p.k / 256;
+    const QBufRsrc rw = q_buffer_rsrc(p.b + (int64_t)min(n0, p.n - 1) * p.ldb, (uint32_t)((int64_t)rows * p.ldb));
+    const QBufRsrc ra = q_buffer_rsrc(p.a, 0x7fffffffu);
+    int w_off[kSkWPieces], a_off[kSkAPieces / 2];
+#pragma unroll
+    for (int q = 0; q < kSkWPieces; ++q) {
+        const int c = 64 * q + lane, r = c / kSkWChunks, cc = c % kSkWChunks;
+        w_off[q] = (r < 16 && cc < 10) ? min(r, rows - 1) * (int)p.ldb + 16 * cc : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kSkAPieces / 2; ++q) {
+        const int c = 64 * (q + wave * (kSkAPieces / 2)) + lane, m = c / kSkAChunks, cc = c % kSkAChunks;
+        a_off[q] = (m < 16 && cc < 32) ? min(m, p.m - 1) * (int)p.lda * 2 + 16 * cc : 0;
+    }
+    auto issue = [&](int s) {
+        uint8_t* dst = ring + (s % NS) * kSkStage;
+#pragma unroll
+        for (int q = 0; q < kSkWPieces; ++q) {
+            q_buffer_load_lds16(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], s * 160);
+        }
+#pragma unroll
+        for (int q = 0; q < kSkAPieces / 2; ++q) {
+            q_buffer_load_lds16(ra, dst + kSkAAt + (wave * (kSkAPieces / 2) + q) * 1024, a_off[q], s * 512);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        if (s < stages) {
+            issue(s);
+        }
+    }
+    const int r16 = lane & 15, qk = lane >> 4;
+    const int nb = 8 * (qk & 1);                     // first nibble byte of this lane's 8 values
+    const int sh = 4 * (qk >> 1);                    // low (0) or high (4) nibbles
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < stages; ++s) {
+        // this wave's pieces of stage s have landed (later stages may be in
+        // flight), every wave's reads of stage s - 1 are done, then the barrier
+        if (s + NS - 2 < stages) {
+            wait_vmcnt<(NS - 2) * kSkL>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
+        q_block_barrier();
+        if (s + NS - 1 < stages) {
+            issue(s + NS - 1);                       // into the slot of stage s - 1
+        }
+        const uint8_t* st = ring + (s % NS) * kSkStage;
+        const uint8_t* wbase = st + wave * kSkWPieces * 1024 + r16 * (16 * kSkWChunks);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const v8h bf = *reinterpret_cast<const v8h*>(st + kSkAAt + r16 * (16 * kSkAChunks) + 64 * jj + 16 * qk);
+            const uint8_t* wr = wbase + 20 * jj;
+            const uint32_t dm = *reinterpret_cast<const uint32_t*>(wr);
+            const uint32_t x0 = *reinterpret_cast<const uint32_t*>(wr + 4 + nb) >> sh;
+            const uint32_t x1 = *reinterpret_cast<const uint32_t*>(wr + 8 + nb) >> sh;
+            const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x01000100u));
+            const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm, dm, 0x03020302u));
+            uint32_t w[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                // bytes 2h and 2h + 1 of the 8 into the two halves' low bytes
+                const uint32_t src = h < 2 ? x0 : x1;
+                const uint32_t t = __builtin_amdgcn_perm(src, src, h % 2 == 0 ? 0x0c010c00u : 0x0c030c02u);
+                const v2h qv = __builtin_bit_cast(v2h, and_or_u32(t, 0x000f000fu, 0x64006400u)) - k1024;
+                w[h] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(d2, qv, m2));
+            }
+            const v8h af = __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc, 0, 0, 0);
+        }
+    }
+    // lane l: rows 4 (l / 16) .. + 3 of the wave's 16, column (row of A) l % 16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 4 * qk + r;
+        if (r16 < p.m && n < p.n) {
+            store_out(p, r16, n, acc[r]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA GEMM, f16 A.
 // ---------------------------------------------------------------------------
 constexpr int kQBK = 64;                 // k values per stage (2 Q4_1 blocks)
@@ -2238,6 +2365,19 @@ inline bool use_gemv(const NnopsGemmQ41Args& g)
 
 // The blocks-along-N ring: f16 A with 16-byte rows, K % 64 == 0, 16-byte B
 // rows, and every stage offset within a buffer resource's 31-bit range
+// The skinny MFMA GEMM (gemv_q4_1_skinny): blocks along K, f16 A with 16-byte
+// rows, 3 <= M <= 48 (launches of 16 rows), K % 256 == 0, 16-byte weight rows,
+// 32-bit offsets. At K = 4096, N = 14336 a launch takes 16 us, the ring 58-62
+// us for any M <= 128: past three launches the ring is the faster.
+constexpr int64_t kSkinnyMaxM = 48;
+
+inline bool skinny_ok(const NnopsGemmQ41Args& g)
+{
+    return g.trans_b && g.a_f16 && !g.b_soa && g.m >= 3 && g.m <= kSkinnyMaxM && g.k % 256 == 0 &&
+           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 && (g.lda % 8) == 0 &&
+           ((uintptr_t)g.a & 15) == 0 && 32 * g.ldb_bytes < INT32_MAX && g.m * g.lda * 2 < INT32_MAX;
+}
+
 inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
 {
     return !g.trans_b && g.a_f16 && g.k % 64 == 0 && (g.lda % 8) == 0 && ((uintptr_t)g.a & 15) == 0 &&
@@ -2401,6 +2541,16 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     hipLaunchKernelGGL(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
                 }
             }
+        }
+    } else if (skinny_ok(*g)) {
+        // a few rows of A: the weight streams once per 16 rows
+        for (int m0 = 0; m0 < k.m; m0 += 16) {
+            Q41Kern kk = k;
+            kk.m = std::min(16, k.m - m0);
+            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
+            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
+            hipLaunchKernelGGL(gemv_q4_1_skinny<4>, dim3((unsigned)((g->n + kSkRows - 1) / kSkRows)), dim3(128), 0,
+                               s, kk);
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

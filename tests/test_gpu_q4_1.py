@@ -64,6 +64,22 @@ def test_q4_1_f32_a(trans_b):
     assert norm_err(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,N", [(3, 4096, 1024), (4, 256, 1000), (8, 512, 64), (16, 4096, 14336), (17, 1024, 520),
+                                   (33, 4096, 96), (48, 768, 1030)])
+@pytest.mark.parametrize("out_f16", [False, True])
+def test_q4_1_skinny(M, K, N, out_f16):
+    """3 <= M <= 48 rows of f16 A over [N][K/32] blocks, K % 256 == 0: the
+    skinny MFMA kernel (weights decoded to f16, one launch per 16 rows of
+    A; ragged N: rows past it are computed and never stored)."""
+    import torch
+    announce(f"q4_1 skinny {M}x{K}x{N} f16out={out_f16}")
+    a = dg.normal(M + K, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(N + 3, N, K)
+    got = run_gpu(a, blk, N, trans_b=True, out_f16=out_f16)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=True, w_round_f16=True, c_f16=out_f16).astype(np.float32)
+    assert norm_err(got, want) <= TOL
+
+
 @pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40)])
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_q4_1_f32_a_gemm(M, K, N, trans_b):
