@@ -369,6 +369,11 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
         out["frac_f32_mfma"] = tf / PEAK_F32_TFLOPS
     else:
         out["frac_f16_mfma"] = tf / PEAK_F16_TFLOPS
+    if M <= 48:
+        # a few rows of A: bound by the weight stream, not the matrix cores
+        by = N * (K // 32) * 20 + M * K * (4 if a_f32 else 2) + M * N * 4
+        out["gbs"] = by / (t["mean_ms"] * 1e-3) / 1e9
+        out["frac_hbm"] = out["gbs"] / PEAK_HBM_GBS
     if cpu_seconds > 0:
         out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, 0, cpu_seconds,
                                        f"config 4 M={M} (weight {out['weight_layout']})")
@@ -827,6 +832,7 @@ def main():
                                                           cpu_seconds=cs)
         secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, few, wu, trans_b=False,
                                                             cpu_seconds=cs)
+        secondary["cfg4_q4_1_m8_decode_batch"] = q41_gemm_case(torch, dg, na, stream, st, wu, M=8)
         secondary["cfg4_q4_1_gemm_m512_f32a"] = q41_gemm_case(torch, dg, na, stream, few, wu, a_f32=True)
         secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
         secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
