@@ -1278,26 +1278,28 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
 // launch (more rows: one launch per 16), K % 256 == 0: the weight streams
 // once, its blocks decoded to f16 and multiplied on the matrix cores.
 //
-// A workgroup of two waves owns 32 weight rows, 16 per wave, and runs the
-// whole K in stages of 8 blocks (256 k), NS stages in flight. A stage is
-// three DMA regions in LDS:
+// A workgroup of 2 x KH waves owns 32 weight rows: wave w takes the 16 rows
+// 16 (w % 2) .. and the K part w / 2 of KH. Each part runs in stages of 8
+// blocks (256 k), NS stages in flight; a stage is, per part, DMA regions in
+// LDS:
 //   weights  per wave 16 rows x 176 bytes: the rows' 160 stage bytes (10
 //            16-byte chunks) plus a pad chunk, so the 16 rows a read serves
 //            fall on 16 distinct bank groups (176 bytes = 44 dwords per row);
-//   A        16 rows x 528 bytes, shared by the two waves: the stage's 256
-//            halves plus a pad chunk (132 dwords per row: a 16-byte read per
-//            row of 16 rows covers the 64 banks once).
+//   A        16 rows x 528 bytes, shared by the part's two waves: the stage's
+//            256 halves plus a pad chunk (132 dwords per row: a 16-byte read
+//            per row of 16 rows covers the 64 banks once).
 // The pads come from the DMA itself: lane i of piece q writes 16 bytes at
 // q * 1024 + 16 i, so chunk c = 64 q + i is given row c / 11, column c % 11
 // (c / 33, c % 33 for A), and a pad or surplus chunk re-reads a valid one.
-// Each wave issues its rows and half of A's pieces; a stage is read after
-// every wave has waited for its own pieces and passed the block barrier.
-// Per block, lane l decodes the 8 values of row l % 16 at k = 8 (l / 16) ..
-// + 7 (low or high nibbles of bytes 0-7 or 8-15): a byte permute and
+// Each wave issues its rows and half of its part's A pieces; a stage is read
+// after every wave has waited for its own pieces and passed the block
+// barrier. Per block, lane l decodes the 8 values of row l % 16 at k = 8 (l /
+// 16) .. + 7 (low or high nibbles of bytes 0-7 or 8-15): a byte permute and
 // v_and_or_b32 make (1024 + q) f16 pairs, v_pk_add_f16 removes 1024 exactly
 // and v_pk_fma_f16 rounds d * q + m once; the 16 x 32 weight tile and A's
 // 32 x 16 tile (lane l: row l % 16, the same 8 k) meet in one
-// v_mfma_f32_16x16x32_f16. Bound: HBM (the weight once, A once per 32 rows).
+// v_mfma_f32_16x16x32_f16. The K parts meet in LDS at the end, in part
+// order. Bound: the decode at a few waves per SIMD, then HBM.
 // ---------------------------------------------------------------------------
 constexpr int kSkRows = 32;                          // per workgroup (16 per wave)
 constexpr int kSkWChunks = 11;                       // per weight row: 10 + pad
@@ -1305,19 +1307,21 @@ constexpr int kSkWPieces = (16 * kSkWChunks + 63) / 64;        // 3 per wave
 constexpr int kSkAChunks = 33;                       // per row of A: 32 + pad
 constexpr int kSkAPieces = 10;                       // 16 x 33 = 528 chunks, in 2 x 5 pieces
 constexpr int kSkL = kSkWPieces + kSkAPieces / 2;    // DMA instructions per wave and stage
-constexpr int kSkAAt = 2 * kSkWPieces * 1024;
-constexpr int kSkStage = kSkAAt + kSkAPieces * 1024;
 
-template <int NS>
-__global__ __launch_bounds__(128) void gemv_q4_1_skinny(Q41Kern p)
+template <int NS, int KH>
+__global__ __launch_bounds__(128 * KH) void gemv_q4_1_skinny(Q41Kern p)
 {
     static_assert(NS >= 2 && (NS - 2) * kSkL < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kSkStage];
+    constexpr int kAAt = 2 * KH * kSkWPieces * 1024;            // A regions after every wave's rows
+    constexpr int kStage = kAAt + KH * kSkAPieces * 1024;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = blockIdx.x * kSkRows + 16 * wave;
-    const int rows = max(1, min(16, p.n - n0));      // a wave past N re-reads row N - 1 (never stored)
-    const int stages = p.k / 256;
+    const int grp = wave & 1, part = wave >> 1;
+    const int n0 = blockIdx.x * kSkRows + 16 * grp;
+    const int rows = max(1, min(16, p.n - n0));      // a group past N re-reads row N - 1 (never stored)
+    const int stages = p.k / 256 / KH;               // per part (host-checked: K % (256 KH) == 0)
+    const int s0 = part * stages;                    // the part's first stage of K
     const QBufRsrc rw = q_buffer_rsrc(p.b + (int64_t)min(n0, p.n - 1) * p.ldb, (uint32_t)((int64_t)rows * p.ldb));
     const QBufRsrc ra = q_buffer_rsrc(p.a, 0x7fffffffu);
     int w_off[kSkWPieces], a_off[kSkAPieces / 2];
@@ -1328,18 +1332,21 @@ __global__ __launch_bounds__(128) void gemv_q4_1_skinny(Q41Kern p)
     }
 #pragma unroll
     for (int q = 0; q < kSkAPieces / 2; ++q) {
-        const int c = 64 * (q + wave * (kSkAPieces / 2)) + lane, m = c / kSkAChunks, cc = c % kSkAChunks;
+        const int c = 64 * (q + grp * (kSkAPieces / 2)) + lane, m = c / kSkAChunks, cc = c % kSkAChunks;
         a_off[q] = (m < 16 && cc < 32) ? min(m, p.m - 1) * (int)p.lda * 2 + 16 * cc : 0;
     }
+    uint8_t* const a_region = ring + kAAt + part * kSkAPieces * 1024;
     auto issue = [&](int s) {
-        uint8_t* dst = ring + (s % NS) * kSkStage;
+        uint8_t* dst = ring + (s % NS) * kStage;
+        const int sg = s0 + s;
 #pragma unroll
         for (int q = 0; q < kSkWPieces; ++q) {
-            q_buffer_load_lds16(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], s * 160);
+            q_buffer_load_lds16(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], sg * 160);
         }
 #pragma unroll
         for (int q = 0; q < kSkAPieces / 2; ++q) {
-            q_buffer_load_lds16(ra, dst + kSkAAt + (wave * (kSkAPieces / 2) + q) * 1024, a_off[q], s * 512);
+            q_buffer_load_lds16(ra, a_region - ring + dst + (grp * (kSkAPieces / 2) + q) * 1024, a_off[q],
+                                sg * 512);
         }
     };
 #pragma unroll
@@ -1366,11 +1373,12 @@ __global__ __launch_bounds__(128) void gemv_q4_1_skinny(Q41Kern p)
         if (s + NS - 1 < stages) {
             issue(s + NS - 1);                       // into the slot of stage s - 1
         }
-        const uint8_t* st = ring + (s % NS) * kSkStage;
+        const uint8_t* st = ring + (s % NS) * kStage;
+        const uint8_t* abase = a_region - ring + st + r16 * (16 * kSkAChunks) + 16 * qk;
         const uint8_t* wbase = st + wave * kSkWPieces * 1024 + r16 * (16 * kSkWChunks);
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-            const v8h bf = *reinterpret_cast<const v8h*>(st + kSkAAt + r16 * (16 * kSkAChunks) + 64 * jj + 16 * qk);
+            const v8h bf = *reinterpret_cast<const v8h*>(abase + 64 * jj);
             const uint8_t* wr = wbase + 20 * jj;
             const uint32_t dm = *reinterpret_cast<const uint32_t*>(wr);
             const uint32_t x0 = *reinterpret_cast<const uint32_t*>(wr + 4 + nb) >> sh;
@@ -1390,7 +1398,24 @@ __global__ __launch_bounds__(128) void gemv_q4_1_skinny(Q41Kern p)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc, 0, 0, 0);
         }
     }
-    // lane l: rows 4 (l / 16) .. + 3 of the wave's 16, column (row of A) l % 16
+    if constexpr (KH > 1) {
+        // the later K parts hand their sums to part 0 through LDS (the ring is free)
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        q_block_barrier();
+        v4f* xs = reinterpret_cast<v4f*>(ring);      // [KH - 1][2 groups][64 lanes]
+        if (part > 0) {
+            xs[((part - 1) * 2 + grp) * 64 + lane] = acc;
+        }
+        __syncthreads();
+        if (part > 0) {
+            return;
+        }
+#pragma unroll
+        for (int h = 1; h < KH; ++h) {
+            acc += xs[((h - 1) * 2 + grp) * 64 + lane];
+        }
+    }
+    // lane l: rows 4 (l / 16) .. + 3 of the group's 16, column (row of A) l % 16
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int n = n0 + 4 * qk + r;
@@ -2549,8 +2574,13 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             kk.m = std::min(16, k.m - m0);
             kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
             kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
-            hipLaunchKernelGGL(gemv_q4_1_skinny<4>, dim3((unsigned)((g->n + kSkRows - 1) / kSkRows)), dim3(128), 0,
-                               s, kk);
+            const dim3 grid((unsigned)((g->n + kSkRows - 1) / kSkRows));
+            if (g->k % 512 == 0) {
+                // two K halves per workgroup: four waves, two stages in flight
+                hipLaunchKernelGGL((gemv_q4_1_skinny<2, 2>), grid, dim3(256), 0, s, kk);
+            } else {
+                hipLaunchKernelGGL((gemv_q4_1_skinny<4, 1>), grid, dim3(128), 0, s, kk);
+            }
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
