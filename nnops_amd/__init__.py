@@ -9,7 +9,7 @@ Python or CPU fallback: a missing library raises.
 """
 from ._lib import (  # noqa: F401
     lib, load, LIB_PATH,
-    GemmI8Args, GemmQ41Args, QdqArgs, Tensor, Epilogue, MatMulAttrs, LinearAttrs, QuantLinearAttrs,
+    GemmI8Args, GemmQ41Args, GemmFpArgs, QdqArgs, Tensor, Epilogue, MatMulAttrs, LinearAttrs, QuantLinearAttrs,
     OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_INITIALIZED, OUT_OF_MEMORY, INTERNAL,
     OUT_S32, OUT_S8, OUT_U8, OUT_F32, OUT_F16, ACT_NONE, ACT_RELU, ACT_GELU,
     ACT_SIGMOID, ACT_TANH, ACT_LEAKY_RELU, ACT_SILU, ACT_HARDSWISH, ACT_ELU, ACT_RELU6,

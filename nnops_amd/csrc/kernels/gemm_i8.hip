@@ -2437,8 +2437,11 @@ int ring_gemm_f16(const NnopsGemmFpArgs& g, void* workspace, size_t ws_bytes, hi
     if (f.ring.mode < 0) {
         return NNOPS_UNSUPPORTED;
     }
-    if (f.total > 0 && (workspace == nullptr || ws_bytes < f.total || (uintptr_t)workspace % 16 != 0)) {
+    if (f.total > 0 && (workspace == nullptr || ws_bytes < f.total)) {
         return NNOPS_NOT_INITIALIZED;
+    }
+    if ((uintptr_t)workspace % 16 != 0) {
+        return NNOPS_INVALID_ARGUMENT;   // staged operands and partials are 16-byte vectors
     }
     char* ws = static_cast<char*>(workspace);
     GemmI8Kern k{};

@@ -117,6 +117,29 @@ def test_gemm_q4_1_rejects_before_any_launch():
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
 
 
+def test_gemm_fp_rejects_before_any_launch():
+    lib = na.lib()
+    g = na.GemmFpArgs()
+    g.m, g.n, g.k = 64, 64, 64
+    g.a = g.b = g.c = 16
+    g.lda, g.ldb, g.ldc = 64, 64, 64
+    g.trans_b, g.in_f16, g.alpha = 1, 1, 1.0
+    g.lda = 63                                   # shorter than K
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.lda, g.ldc = 64, 32                        # C rows shorter than N
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.ldc, g.trans_b, g.ldb, g.n = 64, 0, 64, 96  # [K,N] B rows shorter than N
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.c = None
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.m = 0                                      # an empty problem: ok
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.OK
+    # a split [K,N] GEMV needs its partials: no workspace is not_initialized
+    g.m, g.n, g.ldb, g.ldc, g.k, g.lda, g.c = 1, 4096, 4096, 4096, 4096, 4096, 16
+    assert lib.nnops_hip_gemm_fp_workspace_size(C.byref(g)) > 0
+    assert lib.nnops_hip_gemm_fp(C.byref(g), None, 0, None) == na.NOT_INITIALIZED
+
+
 def desc(shape, dtype):
     t = na.Tensor()
     t.rank = len(shape)
