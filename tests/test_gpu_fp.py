@@ -181,3 +181,47 @@ def test_dense_validation():
     y32 = torch.zeros((4, 32), dtype=torch.float32, device="cuda")
     assert op.compute([na.tensor(y32)], [na.tensor(a), na.tensor(b32)]) == na.UNSUPPORTED
     assert op.compute([na.tensor(y32)], [na.tensor(a), na.tensor(b16)]) == na.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_matmul_dense_batched_broadcast(f16):
+    """Batched dense operands with broadcast on leading axes (nnops' batch
+    walk): A [2, 1, 70, K] x B [3, K, N] -> [2, 3, 70, N]."""
+    import torch
+    announce(f"matmul dense broadcast f16={f16}")
+    dt = np.float16 if f16 else np.float32
+    K, N = 256, 72
+    a = dg.normal(120, (2, 1, 70, K)).astype(dt)
+    b = dg.normal(121, (3, K, N)).astype(dt)
+    out_shape = (2, 3, 70, N)
+    c = torch.zeros(out_shape, dtype=torch.float16 if f16 else torch.float32, device="cuda")
+    op = na.MatMul()
+    ins = [na.tensor(dev(a)), na.tensor(dev(b))]
+    shape, _ = op.output_desc(ins)
+    assert tuple(shape) == out_shape
+    assert op.compute([na.tensor(c)], ins) == na.OK
+    torch.cuda.synchronize()
+    got = host(c).astype(np.float32)
+    for i in range(2):
+        for j in range(3):
+            want = oracle.gemm_fp(a[i, 0], b[j], trans_b=False)
+            if f16:
+                want = want.astype(np.float16).astype(np.float32)
+            assert norm_err(got[i, j], want) <= TOL[f16]
+
+
+def test_linear_dense_rank3_input():
+    """Linear flattens X's leading dims: X [2, 5, K] x W [N, K] -> [2, 5, N]."""
+    import torch
+    announce("linear dense rank3")
+    K, N = 512, 48
+    x = dg.normal(130, (2, 5, K)).astype(np.float16)
+    w = dg.normal(131, (N, K)).astype(np.float16)
+    y = torch.zeros((2, 5, N), dtype=torch.float16, device="cuda")
+    op = na.Linear()
+    ins = [na.tensor(dev(x)), na.tensor(dev(w))]
+    assert op.output_desc(ins)[0] == [2, 5, N]
+    assert op.compute([na.tensor(y)], ins) == na.OK
+    torch.cuda.synchronize()
+    want = oracle.gemm_fp(x.reshape(10, K), w, trans_b=True).astype(np.float16).astype(np.float32)
+    assert norm_err(host(y).astype(np.float32).reshape(10, N), want) <= TOL[True]
