@@ -1426,6 +1426,114 @@ __global__ __launch_bounds__(128 * KH) void gemv_q4_1_skinny(Q41Kern p)
 }
 
 // ---------------------------------------------------------------------------
+// The skinny GEMM for f32 A (nnops computes f32 x Q4_1 in f32): the same
+// workgroup of two waves over 32 weight rows and 256-k stages, the same
+// padded weight rows; A's stage is 16 rows x 1040 bytes (256 floats plus a
+// pad chunk: 260 dwords per row, so a 16-byte read per row of 16 rows covers
+// the 64 banks once). Lane l decodes the 8 values of row l % 16 at k = 8 (l
+// / 16) + t to f32 (fmaf(d, q, m), nnops' f32 decode) and runs 8
+// v_mfma_f32_16x16x4f32, t = 0 .. 7, against A's same 8 k.
+// ---------------------------------------------------------------------------
+constexpr int kSkFAChunks = 65;                      // per row of A: 64 + pad
+constexpr int kSkFAPieces = 18;                      // 16 x 65 = 1040 chunks, in 2 x 9 pieces
+constexpr int kSkFL = kSkWPieces + kSkFAPieces / 2;
+
+template <int NS>
+__global__ __launch_bounds__(128) void gemv_q4_1_skinny_f32(Q41Kern p)
+{
+    static_assert(NS >= 2 && (NS - 2) * kSkFL < 64, "vmcnt range");
+    constexpr int kAAt = 2 * kSkWPieces * 1024;
+    constexpr int kStage = kAAt + kSkFAPieces * 1024;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * kSkRows + 16 * wave;
+    const int rows = max(1, min(16, p.n - n0));      // a group past N re-reads row N - 1 (never stored)
+    const int stages = p.k / 256;
+    const QBufRsrc rw = q_buffer_rsrc(p.b + (int64_t)min(n0, p.n - 1) * p.ldb, (uint32_t)((int64_t)rows * p.ldb));
+    const QBufRsrc ra = q_buffer_rsrc(p.a, 0x7fffffffu);
+    int w_off[kSkWPieces], a_off[kSkFAPieces / 2];
+#pragma unroll
+    for (int q = 0; q < kSkWPieces; ++q) {
+        const int c = 64 * q + lane, r = c / kSkWChunks, cc = c % kSkWChunks;
+        w_off[q] = (r < 16 && cc < 10) ? min(r, rows - 1) * (int)p.ldb + 16 * cc : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kSkFAPieces / 2; ++q) {
+        const int c = 64 * (q + wave * (kSkFAPieces / 2)) + lane, m = c / kSkFAChunks, cc = c % kSkFAChunks;
+        a_off[q] = (m < 16 && cc < 64) ? min(m, p.m - 1) * (int)p.lda * 4 + 16 * cc : 0;
+    }
+    auto issue = [&](int s) {
+        uint8_t* dst = ring + (s % NS) * kStage;
+#pragma unroll
+        for (int q = 0; q < kSkWPieces; ++q) {
+            q_buffer_load_lds16(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], s * 160);
+        }
+#pragma unroll
+        for (int q = 0; q < kSkFAPieces / 2; ++q) {
+            q_buffer_load_lds16(ra, dst + kAAt + (wave * (kSkFAPieces / 2) + q) * 1024, a_off[q], s * 1024);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        if (s < stages) {
+            issue(s);
+        }
+    }
+    const int r16 = lane & 15, qk = lane >> 4;
+    const int nb = 8 * (qk & 1);                     // first nibble byte of this lane's 8 values
+    const int sh = 4 * (qk >> 1);                    // low (0) or high (4) nibbles
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < stages; ++s) {
+        if (s + NS - 2 < stages) {
+            wait_vmcnt<(NS - 2) * kSkFL>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
+        q_block_barrier();
+        if (s + NS - 1 < stages) {
+            issue(s + NS - 1);                       // into the slot of stage s - 1
+        }
+        const uint8_t* st = ring + (s % NS) * kStage;
+        const uint8_t* abase = st + kAAt + r16 * (16 * kSkFAChunks) + 32 * qk;
+        const uint8_t* wbase = st + wave * kSkWPieces * 1024 + r16 * (16 * kSkWChunks);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const v4f a0 = *reinterpret_cast<const v4f*>(abase + 128 * jj);
+            const v4f a1 = *reinterpret_cast<const v4f*>(abase + 128 * jj + 16);
+            const uint8_t* wr = wbase + 20 * jj;
+            const uint32_t dm = *reinterpret_cast<const uint32_t*>(wr);
+            const uint32_t x0 = (*reinterpret_cast<const uint32_t*>(wr + 4 + nb) >> sh) & 0x0f0f0f0fu;
+            const uint32_t x1 = (*reinterpret_cast<const uint32_t*>(wr + 8 + nb) >> sh) & 0x0f0f0f0fu;
+            const float d = h2f(dm & 0xffffu), mn = h2f(dm >> 16);
+            float w[8];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[b] = fmaf(d, (float)((x0 >> (8 * b)) & 0xffu), mn);
+                w[4 + b] = fmaf(d, (float)((x1 >> (8 * b)) & 0xffu), mn);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[t], a0[t], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 + t], a1[t], acc, 0, 0, 0);
+            }
+        }
+    }
+    // lane l: rows 4 (l / 16) .. + 3 of the group's 16, column (row of A) l % 16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 4 * qk + r;
+        if (r16 < p.m && n < p.n) {
+            store_out(p, r16, n, acc[r]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA GEMM, f16 A.
 // ---------------------------------------------------------------------------
 constexpr int kQBK = 64;                 // k values per stage (2 Q4_1 blocks)
@@ -2398,9 +2506,10 @@ constexpr int64_t kSkinnyMaxM = 48;
 
 inline bool skinny_ok(const NnopsGemmQ41Args& g)
 {
-    return g.trans_b && g.a_f16 && !g.b_soa && g.m >= 3 && g.m <= kSkinnyMaxM && g.k % 256 == 0 &&
-           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 && (g.lda % 8) == 0 &&
-           ((uintptr_t)g.a & 15) == 0 && 32 * g.ldb_bytes < INT32_MAX && g.m * g.lda * 2 < INT32_MAX;
+    const int64_t es = g.a_f16 ? 2 : 4;
+    return g.trans_b && !g.b_soa && g.m >= 3 && g.m <= kSkinnyMaxM && g.k % 256 == 0 &&
+           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 && (g.lda * es) % 16 == 0 &&
+           ((uintptr_t)g.a & 15) == 0 && 32 * g.ldb_bytes < INT32_MAX && g.m * g.lda * es < INT32_MAX;
 }
 
 inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
@@ -2480,7 +2589,24 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
     k.ldbdm = g->b_soa ? g->ldb_dm : 0;
     const bool soa = g->b_soa != 0;
 
-    if (use_gemv(*g)) {
+    if (skinny_ok(*g)) {
+        // a few rows of A: the weight streams once per 16 rows
+        for (int m0 = 0; m0 < k.m; m0 += 16) {
+            Q41Kern kk = k;
+            kk.m = std::min(16, k.m - m0);
+            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * (g->a_f16 ? 2 : 4);
+            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
+            const dim3 grid((unsigned)((g->n + kSkRows - 1) / kSkRows));
+            if (!g->a_f16) {
+                hipLaunchKernelGGL(gemv_q4_1_skinny_f32<3>, grid, dim3(128), 0, s, kk);
+            } else if (g->k % 512 == 0) {
+                // two K halves per workgroup: four waves, two stages in flight
+                hipLaunchKernelGGL((gemv_q4_1_skinny<2, 2>), grid, dim3(256), 0, s, kk);
+            } else {
+                hipLaunchKernelGGL((gemv_q4_1_skinny<4, 1>), grid, dim3(128), 0, s, kk);
+            }
+        }
+    } else if (use_gemv(*g)) {
         // rows of A handled per pass: 2 (f16 pairs), 1 for f32 A
         const int mt = g->a_f16 ? 2 : 1;
         for (int m0 = 0; m0 < k.m; m0 += mt) {
@@ -2565,21 +2691,6 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 } else {
                     hipLaunchKernelGGL(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
                 }
-            }
-        }
-    } else if (skinny_ok(*g)) {
-        // a few rows of A: the weight streams once per 16 rows
-        for (int m0 = 0; m0 < k.m; m0 += 16) {
-            Q41Kern kk = k;
-            kk.m = std::min(16, k.m - m0);
-            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
-            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
-            const dim3 grid((unsigned)((g->n + kSkRows - 1) / kSkRows));
-            if (g->k % 512 == 0) {
-                // two K halves per workgroup: four waves, two stages in flight
-                hipLaunchKernelGGL((gemv_q4_1_skinny<2, 2>), grid, dim3(256), 0, s, kk);
-            } else {
-                hipLaunchKernelGGL((gemv_q4_1_skinny<4, 1>), grid, dim3(128), 0, s, kk);
             }
         }
     } else if (!g->a_f16) {

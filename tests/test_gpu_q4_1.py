@@ -80,6 +80,18 @@ def test_q4_1_skinny(M, K, N, out_f16):
     assert norm_err(got, want) <= TOL
 
 
+@pytest.mark.parametrize("M,K,N", [(3, 4096, 1024), (16, 512, 1000), (40, 768, 96)])
+def test_q4_1_skinny_f32_a(M, K, N):
+    """f32 A, 3 <= M <= 48, K % 256 == 0: the skinny kernel's f32 form (f32
+    decode, f32 MFMA) against the f64-accumulated oracle within 1e-4."""
+    announce(f"q4_1 skinny f32 {M}x{K}x{N}")
+    a = dg.normal(M + 2 * K, (M, K))
+    blk = dg.q4_1_blocks(N + 5, N, K)
+    got = run_gpu(a, blk, N, trans_b=True)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=True)
+    assert norm_err(got, want) <= 1e-4
+
+
 @pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40)])
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_q4_1_f32_a_gemm(M, K, N, trans_b):
