@@ -160,17 +160,21 @@ int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int
  * src/ops/matmul.cpp:96-141; the CPU path packs no Q4_1 form,
  * matmul_helper.cpp:695-723, this is the gfx950 one). From B [K][ceil(N/32)]
  * blocks (trans_b = 0), row pitch ldb_bytes, it writes the same blocks as
- * two planes, structure of arrays:
- *   nibbles  k-blocked: per group of 8 rows, per block, per nibble dword
- *            d, the 8 rows' dwords: dword d of row k, block j at byte
- *            ((k / 8) * nbn + j) * 128 + 32 d + 4 (k % 8) (rows past K zero);
- *   d|m      [K][dmp] u32 (f16 d low, f16 m high), dmp = nbn rounded up to
- *            4, at byte offset align_up(ceil(K / 8) * 8 * nbn * 16, 256);
- * nbn = ceil(N / 32). A call then passes b = out, ldb_bytes = nbn * 16,
- * b_soa = 1, b_dm = out + that offset, ldb_dm = dmp: the GEMV's and GEMM's
- * lane loads become contiguous 4- and 16-byte runs instead of 20-byte
- * strides. Blocks along K (trans_b = 1) already stream as whole rows and have
- * no packed form (NNOPS_UNSUPPORTED). `out` must be 256-byte aligned and hold
+ * two planes, structure of arrays, one block column (32 columns) after
+ * another:
+ *   nibbles  k-blocked: block column j is kg * 128 bytes (kg = ceil(K/8)),
+ *            per group of 8 rows, per nibble dword d, the 8 rows' dwords:
+ *            dword d of row k, block j at byte
+ *            (j * kg + k / 8) * 128 + 32 d + 4 (k % 8) (rows past K zero);
+ *   d|m      block column j is kdm u32 (kdm = K rounded up to 64), row k's
+ *            (f16 d low, f16 m high) at j * kdm + k (rows past K zero), the
+ *            plane at byte offset align_up(nbn * kg * 128, 256);
+ * nbn = ceil(N / 32). A call then passes b = out, ldb_bytes = kg * 128,
+ * b_soa = 1, b_dm = out + that offset, ldb_dm = kdm: a block column's bytes
+ * are two contiguous runs over the whole of K, so the GEMV streams each as
+ * whole lines with no K split, and the GEMM's lane loads are contiguous 4-
+ * and 16-byte runs instead of 20-byte strides. Blocks along K (trans_b = 1)
+ * already stream as whole rows and have no packed form (NNOPS_UNSUPPORTED). `out` must be 256-byte aligned and hold
  * nnops_hip_prepack_q4_1_bytes(k, n) bytes. Stream-ordered, no allocation. */
 size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n);
 int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b, void* out,
@@ -215,8 +219,8 @@ typedef struct NnopsGemmQ41Args {
     int32_t out_kind;           /* NNOPS_OUT_F32 / NNOPS_OUT_F16 */
     /* b_soa = 1: B is the prepacked blocks-along-N form (trans_b = 0) of
      * nnops_hip_prepack_q4_1: b = the k-blocked nibble plane (ldb_bytes =
-     * nbn * 16, one group of 8 rows every 8 * ldb_bytes),
-     * b_dm = the d|m plane (row pitch ldb_dm u32 elements). */
+     * its block-column pitch, exactly ceil(K/8) * 128), b_dm = the d|m plane
+     * (ldb_dm = its block-column pitch in u32, exactly K rounded up to 64). */
     int32_t b_soa;
     const uint32_t* b_dm;
     int64_t ldb_dm;

@@ -315,12 +315,12 @@ NnopsGemmQ41Args q41_args_from_geometry(const Geometry& g, const QuantCall& q, i
     x.ldb_bytes = static_cast<int64_t>(data_type_row_bytes(DataType::q4_1, g.trans_b ? g.k : g.n));
     x.out_kind = out_kind;
     if (g.b_packed) {
-        // the planes of nnops_hip_prepack_q4_1: nibble rows of nbn * 16 bytes,
-        // d|m rows of nbn rounded up to 4 dwords (b_dm is set with the pointer)
-        const int64_t nbn = (g.n + 31) / 32;
+        // the planes of nnops_hip_prepack_q4_1, one block column after
+        // another: ceil(K/8) * 128 nibble bytes and K rounded up to 64 d|m
+        // dwords per block column (b_dm is set with the pointer)
         x.b_soa = 1;
-        x.ldb_bytes = nbn * 16;
-        x.ldb_dm = (nbn + 3) / 4 * 4;
+        x.ldb_bytes = (g.k + 7) / 8 * 128;
+        x.ldb_dm = (g.k + 63) / 64 * 64;
     }
     return x;
 }
@@ -718,7 +718,7 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
         x.ldc = pass ? g.n : out.row_stride_elems();
         if (g.b_packed) {
             x.b_dm = reinterpret_cast<const uint32_t*>(
-                b.ptr<const char>() + align_up(static_cast<size_t>((g.k + 7) / 8 * 8 * x.ldb_bytes)));
+                b.ptr<const char>() + align_up(static_cast<size_t>((g.n + 31) / 32 * x.ldb_bytes)));
         } else {
             x.ldb_bytes = b.pitch();
         }

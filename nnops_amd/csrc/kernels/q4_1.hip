@@ -18,10 +18,14 @@
 //                   f16 pairs of two rows and dotted with (a d) pairs; the K
 //                   splits of a column group summed by its last-arriving
 //                   workgroup in the same launch. Bound: HBM.
-//   gemv_q4_1_kn    the prepacked planes of blocks along N (and f32 A or odd
-//                   K): a lane owns one nibble dword (8 columns) of a block, 16
-//                   rows of loads in flight; waves and workgroups split K,
-//                   partial planes summed by reduce_q4_1. Bound: HBM.
+//   gemv_q4_1_bcm   the prepacked planes of blocks along N, f16 A, M <= 2 per
+//                   launch: a workgroup per block column (32 columns) over the
+//                   whole of K, streaming its two contiguous runs as 1 KiB
+//                   wave loads; one launch, no workspace. Bound: HBM.
+//   gemv_q4_1_kn    blocks along N with f32 A or odd K (raw rows or the
+//                   prepacked planes): a lane owns one nibble dword (8
+//                   columns) of a block, 16 rows of loads in flight; waves and
+//                   workgroups split K, partial planes summed by reduce_q4_1.
 //   gemm_q4_1_ring  larger M, f16 A, blocks along K, K % 64 == 0: a 4-stage
 //                   LDS ring filled by DMA (A and the raw Q4_1 bytes), 8 waves
 //                   of 128 x 32, B decoded per lane into MFMA operands with
@@ -54,13 +58,27 @@ struct Q41Kern {
     int64_t lda, ldc, ldb;   // lda/ldc in elements, ldb in bytes
     int out_f16;
     int splits;
-    const uint32_t* bdm; // SoA d|m plane [K][ldbdm] (prepacked blocks along N)
+    const uint32_t* bdm; // SoA d|m plane, block column j at j * ldbdm (prepacked blocks along N)
     int64_t ldbdm;       // u32 elements
 };
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
 {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// The prepacked blocks-along-N planes (nnops_hip_prepack_q4_1), one block
+// column (32 columns) after another: block column j of the nibble plane is
+// p.ldb = ceil(K/8) * 128 bytes, its group of 8 rows r / 8 the 128 bytes at
+// (r / 8) * 128, holding nibble dword d of row r at 32 d + 4 (r % 8); block
+// column j of the d|m plane is p.ldbdm dwords, row r's (f16 d, f16 m) at r.
+__device__ __forceinline__ const uint8_t* soa_group(const Q41Kern& p, int64_t j, int64_t r)
+{
+    return p.b + j * p.ldb + (r >> 3) * 128;
+}
+__device__ __forceinline__ uint32_t soa_dm(const Q41Kern& p, int64_t j, int64_t r)
+{
+    return p.bdm[j * p.ldbdm + r];
 }
 
 template <bool AF16>
@@ -827,13 +845,13 @@ __global__ __launch_bounds__(256) void gemv_q4_1_kn(Q41Kern p)
 #pragma unroll
             for (int gg = 0; gg < GB; ++gg) {
                 const int64_t grp = min(g0 + 4 * gg, (k1 - 1) / 8);
-                const v4i* xs = reinterpret_cast<const v4i*>(p.b + (grp * nblocks + bc) * 128 + jq * 32);
+                const v4i* xs = reinterpret_cast<const v4i*>(soa_group(p, bc, 8 * grp) + jq * 32);
                 xq[gg][0] = xs[0];
                 xq[gg][1] = xs[1];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int64_t r = 8 * grp + e < k1 ? 8 * grp + e : k1 - 1;
-                    dmw[gg][e] = p.bdm[r * p.ldbdm + bc];
+                    dmw[gg][e] = soa_dm(p, bc, r);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
                         ar[gg][e][m] = static_cast<const AT*>(p.a)[(int64_t)min(m, p.m - 1) * p.lda + r];
@@ -1274,6 +1292,149 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
 }
 
 // ---------------------------------------------------------------------------
+// GEMV over the prepacked blocks-along-N planes, f16 A, M <= 2 per launch, K
+// % 8 == 0: one launch, no workspace. Workgroup j owns block column j (32
+// columns) over the whole of K, which the planes hold as two contiguous runs
+// (K / 8 groups of 128 nibble bytes, K d|m dwords), so no partial sum leaves
+// it. The nibble run is read as consecutive 16-byte chunks by consecutive
+// lanes (every wave load is 1 KiB of whole lines: the access pattern that
+// streams HBM at full rate; 32-byte pieces per lane ran 40 % slower). Chunk c
+// of a group is nibble dword c / 2 (columns 4 (c/2) + i from the low
+// nibbles, 16 + 4 (c/2) + i from the high, i < 4) of the group's rows 4 (c %
+// 2) .. + 3, so lane t always owns chunk t % 8 of the groups t / 8, t / 8 +
+// T / 8, ...; with it the 4 rows' d|m dwords (16 bytes) and A's 4 halves per
+// row of A, U chunks in flight. Per row pair (k, k+1) the arithmetic of
+// gemv_q4_1_kn_dma: s = (a_k, a_k+1) * (d_k, d_k+1) as the exact f16 sum
+// sv + sl, nibble pairs of the two rows widened by v_perm / v_and_or (64 +
+// q/16 and 64 + q), dotted with s in f32, the low nibbles' sums scaled by 16
+// and the 1024 S and 64 S offsets removed per batch; plus sum a m per block.
+// The lanes of a column
+// meet in LDS in lane order (deterministic). Bound: HBM.
+// ---------------------------------------------------------------------------
+template <int MT, int W, int U>
+__global__ __launch_bounds__(W * 64) void gemv_q4_1_bcm(Q41Kern p)
+{
+    constexpr int T = W * 64, NS = T / 4;        // lanes per nibble dword
+    __shared__ float red[MT * 32][NS + 1];
+    const int t = threadIdx.x;
+    const int c = t & 7, jq = c >> 1, h = c & 1;
+    const int slot = (t >> 3) * 2 + h;           // the lane among those of its dword
+    const int64_t j = blockIdx.x;                // block column
+    const int nch = p.k;                         // 16-byte chunks: 8 per group of 8 rows
+    const v4i* nib = reinterpret_cast<const v4i*>(p.b + j * p.ldb);
+    const uint32_t* dmc = p.bdm + j * p.ldbdm;
+    const _Float16* A = static_cast<const _Float16*>(p.a);
+    const v2h ones = {(_Float16)1.0f, (_Float16)1.0f};
+    float tot_lo[MT][4], tot_hi[MT][4], tot_m[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        tot_m[m] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tot_lo[m][i] = 0.0f;
+            tot_hi[m][i] = 0.0f;
+        }
+    }
+    for (int i0 = t; i0 < nch; i0 += U * T) {
+        v4i x[U], dmv[U];
+        v2u32 av[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // chunk ci: rows r0 .. r0 + 3 (a chunk past K re-reads the last)
+            const int ci = min(i0 + u * T, nch - 8 + c);
+            const int r0 = (ci >> 3) * 8 + 4 * h;
+            x[u] = __builtin_nontemporal_load(nib + ci);
+            dmv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(dmc + r0));
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                av[u][m] = *reinterpret_cast<const v2u32*>(A + (int64_t)min(m, p.m - 1) * p.lda + r0);
+            }
+        }
+        float acc_lo[MT][4], acc_hi[MT][4], sum_s[MT], acc_m[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            sum_s[m] = 0.0f;
+            acc_m[m] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc_lo[m][i] = 0.0f;
+                acc_hi[m][i] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // a chunk past K (the clamped re-read) and rows of A past M count 0
+            const bool live = i0 + u * T < nch;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t x0 = (uint32_t)x[u][2 * e], x1 = (uint32_t)x[u][2 * e + 1];
+                const uint32_t dm0 = (uint32_t)dmv[u][2 * e], dm1 = (uint32_t)dmv[u][2 * e + 1];
+                const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x05040100u));
+                const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dm1, dm0, 0x07060302u));
+                v2h sv[MT], sl[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const uint32_t aw = (live && m < p.m) ? (uint32_t)av[u][m][e] : 0u;
+                    const v2h a2 = __builtin_bit_cast(v2h, aw);
+                    sv[m] = a2 * d2;
+                    sl[m] = __builtin_elementwise_fma(a2, d2, -sv[m]);
+                    sum_s[m] = __builtin_amdgcn_fdot2(sv[m], ones, sum_s[m], false);
+                    sum_s[m] = __builtin_amdgcn_fdot2(sl[m], ones, sum_s[m], false);
+                    acc_m[m] = __builtin_amdgcn_fdot2(a2, m2, acc_m[m], false);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // (byte i of x0, 0, byte i of x1, 0): selector 0x0c is a zero byte
+                    const uint32_t sel = 0x0c000c00u | (uint32_t)(4 + i) << 16 | (uint32_t)i;
+                    const uint32_t tt = __builtin_amdgcn_perm(x1, x0, sel);
+                    const v2h lo = __builtin_bit_cast(v2h, and_or_u32(tt, 0x000f000fu, 0x54005400u));
+                    const v2h hi = __builtin_bit_cast(v2h, and_or_u32(tt, 0x00f000f0u, 0x54005400u));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        acc_lo[m][i] = __builtin_amdgcn_fdot2(sv[m], lo, acc_lo[m][i], false);
+                        acc_lo[m][i] = __builtin_amdgcn_fdot2(sl[m], lo, acc_lo[m][i], false);
+                        acc_hi[m][i] = __builtin_amdgcn_fdot2(sv[m], hi, acc_hi[m][i], false);
+                        acc_hi[m][i] = __builtin_amdgcn_fdot2(sl[m], hi, acc_hi[m][i], false);
+                    }
+                }
+            }
+        }
+        // fold the batch: remove the 64 S offsets while they are small; the low
+        // nibbles' sums (of s (64 + q/16)) are scaled by 16 exactly first
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            tot_m[m] += acc_m[m];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                tot_lo[m][i] += fmaf(-1024.0f, sum_s[m], 16.0f * acc_lo[m][i]);
+                tot_hi[m][i] += fmaf(-64.0f, sum_s[m], acc_hi[m][i]);
+            }
+        }
+    }
+    // column col of the block, row m: word (m * 32 + col, slot)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            red[m * 32 + 4 * jq + i][slot] = tot_lo[m][i] + tot_m[m];
+            red[m * 32 + 16 + 4 * jq + i][slot] = tot_hi[m][i] + tot_m[m];
+        }
+    }
+    __syncthreads();
+    if (t < MT * 32) {
+        const int m = t / 32, n = (int)j * 32 + t % 32;
+        float v = 0.0f;
+#pragma unroll 8
+        for (int q = 0; q < NS; ++q) {
+            v += red[t][q];
+        }
+        if (m < p.m && n < p.n) {
+            store_out(p, m, n, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM, blocks along K ([N][K/32]), f16 A with 3 <= M <= 16 rows per
 // launch (more rows: one launch per 16), K % 256 == 0: the weight streams
 // once, its blocks decoded to f16 and multiplied on the matrix cores.
@@ -1616,11 +1777,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_q4_1_mfma(Q41Kern p)
                 live = (k0 + kr) < p.k;
                 if constexpr (SOA) {
                     // the prepacked planes: d|m from its plane, nibble dword d
-                    // of row r at (r / 8) * 8 ldb + 128 block + 32 d + 4 (r % 8)
+                    // of row r at 32 d + 4 (r % 8) of its group
                     const int64_t r = min(k0 + kr, p.k - 1);
                     const int64_t j = min(bn, nbn - 1);
-                    const uint8_t* q = p.b + (r >> 3) * 8 * p.ldb + j * 128 + 4 * (r & 7);
-                    rb[i][0] = live ? p.bdm[r * p.ldbdm + j] : 0u;
+                    const uint8_t* q = soa_group(p, j, r) + 4 * (r & 7);
+                    rb[i][0] = live ? soa_dm(p, j, r) : 0u;
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
                         rb[i][1 + d] = *reinterpret_cast<const uint32_t*>(q + 32 * d);
@@ -1801,9 +1962,9 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_f32(Q41Kern p)
                 rq0 = *reinterpret_cast<const uint32_t*>(src + 4 + 8 * bh);
                 rq1 = *reinterpret_cast<const uint32_t*>(src + 8 + 8 * bh);
             } else {
-                // nibble dword d of row r at (r / 8) * 8 ldb + 128 block + 32 d + 4 (r % 8)
-                const uint8_t* q = p.b + (r >> 3) * 8 * p.ldb + j * 128 + 4 * (r & 7) + 64 * bh;
-                rdm = p.bdm[r * p.ldbdm + j];
+                // nibble dword d of row r at 32 d + 4 (r % 8) of its group
+                const uint8_t* q = soa_group(p, j, r) + 4 * (r & 7) + 64 * bh;
+                rdm = soa_dm(p, j, r);
                 rq0 = *reinterpret_cast<const uint32_t*>(q);
                 rq1 = *reinterpret_cast<const uint32_t*>(q + 32);
             }
@@ -2180,12 +2341,16 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
     // this tile's blocks of row 0; a stage's rows start s * 64 * ldb further
     const int nbn = (p.n + 31) / 32;
-    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * (SOA ? 128 : 20);
-    const int64_t b_end = SOA ? (int64_t)(p.k / 8 - 1) * 8 * p.ldb + (int64_t)(nbn - n0 / 32) * 128
+    // SOA: the tile's first block column of each plane; a stage is 8 groups
+    // (1 KiB) further along every block column's nibbles, 256 bytes along its
+    // d|m dwords
+    const uint8_t* b0 = p.b + (int64_t)(n0 / 32) * (SOA ? p.ldb : 20);
+    const int64_t b_end = SOA ? (int64_t)(nbn - n0 / 32) * p.ldb
                               : (int64_t)(p.k - 1) * p.ldb + (int64_t)(nbn - n0 / 32) * 20;
-    const int64_t ldd = p.ldbdm * 4;                // SOA: d|m row pitch in bytes
-    const uint8_t* d0 = reinterpret_cast<const uint8_t*>(p.bdm) + (int64_t)(n0 / 32) * 4;
-    const int64_t d_end = (int64_t)(p.k - 1) * ldd + (int64_t)(nbn - n0 / 32) * 4;
+    const int64_t ldd = p.ldbdm * 4;                // SOA: d|m block column pitch in bytes
+    const uint8_t* d0 = reinterpret_cast<const uint8_t*>(p.bdm) + (int64_t)(n0 / 32) * ldd;
+    const int64_t d_end = (int64_t)(nbn - n0 / 32) * ldd;
+    const int last_blk = nbn - 1 - n0 / 32;         // blocks past N re-read the last one
     int a_off[QA], b_off[2];
 #pragma unroll
     for (int i = 0; i < QA; ++i) {
@@ -2197,15 +2362,14 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     for (int i = 0; i < 2; ++i) {
         const int q = (wave + W * i) * 64 + lane;     // chunk = LDS slot
         if constexpr (SOA) {
-            // nibble piece: the wave's group of 8 rows, 1 KiB contiguous;
-            // d|m pieces: 2 chunks per row, slot-row order
+            // nibble piece: the wave's group of 8 rows, 128 bytes from each
+            // of the tile's 8 block columns; d|m pieces: 16 chunks of 4 rows
+            // per block column, [block][row] in the slot
             if (i == 0) {
-                b_off[i] = wave * 8 * (int)p.ldb + lane * 16;
+                b_off[i] = min(lane >> 3, last_blk) * (int)p.ldb + wave * 128 + (lane & 7) * 16;
             } else {
                 const int qq = q - W * 64;
-                const int pr = qq / 2, c = qq - pr * 2;
-                const int k = pr ^ ((pr >> 3) & 1);
-                b_off[i] = k * (int)ldd + c * 16;
+                b_off[i] = min(qq >> 4, last_blk) * (int)ldd + (qq & 15) * 16;
             }
         } else {
             const int pr = q / 10, c = q - pr * 10;
@@ -2219,12 +2383,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
         for (int i = 0; i < QA; ++i) {
             q_buffer_load_lds16(rsa, base + (QA * wave + i) * 1024, a_off[i], s * 128);
         }
-        const int64_t row0 = (int64_t)s * 64 * p.ldb;
+        const int64_t row0 = SOA ? (int64_t)s * 1024 : (int64_t)s * 64 * p.ldb;
         const QBufRsrc rsb = q_buffer_rsrc(b0 + row0, (uint32_t)std::min<int64_t>(b_end - row0, 0x7fffffff));
         q_buffer_load_lds16(rsb, base + kA + wave * (SOA ? kGrp : 1024), b_off[0], 0);
         if (two) {
             if constexpr (SOA) {
-                const int64_t drow0 = (int64_t)s * 64 * ldd;
+                const int64_t drow0 = (int64_t)s * 256;
                 const QBufRsrc rsd =
                     q_buffer_rsrc(d0 + drow0, (uint32_t)std::min<int64_t>(d_end - drow0, 0x7fffffff));
                 q_buffer_load_lds16(rsd, base + kA + kDmAt + wave * 1024, b_off[1], 0);
@@ -2260,6 +2424,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     // immediate offsets
     const int sr0 = 9 * kh, sr1 = 7 * kh + 1;
     const int bxs = kA + kh * kGrp + 128 * wave + 32 * ((fr & 15) >> 2);   // SOA nibbles
+    const int bds = kA + kDmAt + 256 * wave + 32 * kh;                     // SOA d|m: rows 8 kh ..
     const int bd0 = kA + sr0 * kRowD + bcol, bq0 = kA + sr0 * kRowQ + qdw;
     const int bd1 = kA + sr1 * kRowD + bcol, bq1 = kA + sr1 * kRowQ + qdw;
     // Low-nibble lanes keep 0x0f under exponent byte 0x64: f16 1024 + q.
@@ -2279,9 +2444,14 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int od = (16 * ks + 2 * e) * kRowD, oq = (16 * ks + 2 * e) * kRowQ;
-            r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + od);
-            r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + od);
-            if constexpr (!SOA) {
+            if constexpr (SOA) {
+                // rows 16 ks + 8 kh + 2 e and + 1 of the wave's block column
+                const v2u32 dd = *reinterpret_cast<const v2u32*>(st + bds + (16 * ks + 2 * e) * 4);
+                r.dm0[e] = dd.x;
+                r.dm1[e] = dd.y;
+            } else {
+                r.dm0[e] = *reinterpret_cast<const uint32_t*>(st + bd0 + od);
+                r.dm1[e] = *reinterpret_cast<const uint32_t*>(st + bd1 + od);
                 r.x0[e] = *reinterpret_cast<const uint32_t*>(st + bq0 + oq);
                 r.x1[e] = *reinterpret_cast<const uint32_t*>(st + bq1 + oq);
             }
@@ -2388,12 +2558,13 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 
 // ---------------------------------------------------------------------------
 // Prepack of a blocks-along-N weight into its two planes (structure of
-// arrays): thread per block; the nibble plane is k-blocked (per 8 rows, per
-// block, per nibble dword: the 8 rows' dwords, 32 bytes), the d|m dword goes
-// into its plane; padding is zeroed.
+// arrays), one block column after another: thread per block; the nibble
+// plane is k-blocked (block column j: per 8 rows, per nibble dword, the 8
+// rows' dwords, 32 bytes), the d|m dword goes to row r of block column j of
+// its plane; padding (rows past K) is zeroed.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t ldb, int k, int nbn,
-                                                       uint8_t* nib, uint32_t* dm, int64_t dmp)
+                                                       uint8_t* nib, uint32_t* dm, int64_t kdm)
 {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)k * nbn) {
@@ -2402,26 +2573,23 @@ __global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t
     const int64_t r = idx / nbn;
     const int j = (int)(idx - r * nbn);
     const uint32_t* src = reinterpret_cast<const uint32_t*>(b + r * ldb + (int64_t)j * 20);
-    // nibble dword d of row r at ((r / 8) * nbn + j) * 128 + 32 d + 4 (r % 8):
-    // a block's 8 consecutive rows of one dword are 32 contiguous bytes
-    uint32_t* g = reinterpret_cast<uint32_t*>(nib + (((r >> 3) * nbn + j) * 128));
+    const int64_t kg = (k + 7) / 8;
+    uint32_t* g = reinterpret_cast<uint32_t*>(nib + ((int64_t)j * kg + (r >> 3)) * 128);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
         g[8 * d + (r & 7)] = src[1 + d];
     }
+    dm[(int64_t)j * kdm + r] = src[0];
     if (r == k - 1) {
-        // the last group's rows past K
+        // the last group's rows past K, and the block column's d|m rows past K
         for (int rr = (int)(r & 7) + 1; rr < 8; ++rr) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 g[8 * d + rr] = 0u;
             }
         }
-    }
-    dm[r * dmp + j] = src[0];
-    if (j == nbn - 1) {
-        for (int64_t t = nbn; t < dmp; ++t) {
-            dm[r * dmp + t] = 0u;
+        for (int64_t t = k; t < kdm; ++t) {
+            dm[(int64_t)j * kdm + t] = 0u;
         }
     }
 }
@@ -2512,15 +2680,24 @@ inline bool skinny_ok(const NnopsGemmQ41Args& g)
            ((uintptr_t)g.a & 15) == 0 && 32 * g.ldb_bytes < INT32_MAX && g.m * g.lda * es < INT32_MAX;
 }
 
+// The one-launch GEMV over the prepacked planes (gemv_q4_1_bcm): f16 A with
+// 16-byte-aligned rows, K % 8 == 0.
+inline bool bcm_ok(const NnopsGemmQ41Args& g)
+{
+    return g.b_soa && !g.trans_b && g.a_f16 && g.k % 8 == 0 && (g.lda % 8) == 0 && ((uintptr_t)g.a & 15) == 0;
+}
+
 inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
 {
     return !g.trans_b && g.a_f16 && g.k % 64 == 0 && (g.lda % 8) == 0 && ((uintptr_t)g.a & 15) == 0 &&
-           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 && g.k * g.ldb_bytes < INT32_MAX &&
-           (!g.b_soa || g.k * g.ldb_dm * 4 < INT32_MAX);
+           (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 &&
+           (g.b_soa ? 8 * g.ldb_bytes < INT32_MAX && 8 * g.ldb_dm * 4 < INT32_MAX : g.k * g.ldb_bytes < INT32_MAX);
 }
 
 
-inline int64_t prepack_q41_dmp(int64_t n) { return ((n + 31) / 32 + 3) / 4 * 4; }
+// the prepacked planes' block-column pitches: nibbles in bytes, d|m in dwords
+inline int64_t prepack_q41_nib_pitch(int64_t k) { return (k + 7) / 8 * 128; }
+inline int64_t prepack_q41_dm_pitch(int64_t k) { return (k + 63) / 64 * 64; }
 
 }  // namespace
 }  // namespace nnops_amd
@@ -2529,7 +2706,7 @@ using namespace nnops_amd;
 
 extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
 {
-    if (g == nullptr || g->trans_b || !use_gemv(*g)) {
+    if (g == nullptr || g->trans_b || !use_gemv(*g) || bcm_ok(*g)) {
         return 0;
     }
     // pointer alignment, which a size query may not see, picks between the
@@ -2560,13 +2737,15 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         return NNOPS_UNSUPPORTED;
     }
     const int64_t nbn = (g->n + 31) / 32;
-    const int64_t row_bytes = g->trans_b ? (g->k + 31) / 32 * 20 : nbn * (g->b_soa ? 16 : 20);
+    // the prepacked planes' pitches are fixed by K (exact, checked below)
+    const int64_t row_bytes = g->b_soa ? 0 : g->trans_b ? (g->k + 31) / 32 * 20 : nbn * 20;
     if (g->lda < g->k || g->ldc < g->n || g->ldb_bytes < row_bytes || (g->ldb_bytes & 3) ||
         ((uintptr_t)g->b & 3)) {
         return NNOPS_INVALID_ARGUMENT;
     }
-    if (g->b_soa && (g->trans_b || g->b_dm == nullptr || g->ldb_bytes != nbn * 16 || ((uintptr_t)g->b & 15) ||
-                     ((uintptr_t)g->b_dm & 15) || (g->ldb_dm & 3) || g->ldb_dm < nbn)) {
+    if (g->b_soa && (g->trans_b || g->b_dm == nullptr || g->ldb_bytes != prepack_q41_nib_pitch(g->k) ||
+                     ((uintptr_t)g->b & 15) || ((uintptr_t)g->b_dm & 15) ||
+                     g->ldb_dm != prepack_q41_dm_pitch(g->k))) {
         return NNOPS_INVALID_ARGUMENT;
     }
     const size_t need = nnops_hip_gemm_q4_1_workspace_size(g);
@@ -2647,6 +2826,15 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     }
                 } else {
                     hipLaunchKernelGGL((gemv_q4_1_nk<1, false>), dim3(blocks), dim3(256), 0, s, kk);
+                }
+            } else if (bcm_ok(*g)) {
+                // the prepacked planes: one workgroup per block column, whole K
+                // 8 waves, 4 chunks in flight per lane: 10.6 us at config 4
+                // (4 waves x 2 chunks 12.0, 8 x 2 11.2, 4 x 8 10.8)
+                if (kk.m == 1) {
+                    hipLaunchKernelGGL((gemv_q4_1_bcm<1, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                } else {
+                    hipLaunchKernelGGL((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
                 }
             } else if (const KnDmaPlan pl = plan_kn_dma(*g); pl.groups > 0) {
                 KnDma kd;
@@ -2744,8 +2932,8 @@ extern "C" size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n)
     if (k <= 0 || n <= 0) {
         return 0;
     }
-    return align_up((size_t)((k + 7) / 8 * 8) * (size_t)((n + 31) / 32) * 16) +
-           (size_t)k * (size_t)prepack_q41_dmp(n) * 4;
+    const size_t nbn = (size_t)((n + 31) / 32);
+    return align_up(nbn * (size_t)prepack_q41_nib_pitch(k)) + nbn * (size_t)prepack_q41_dm_pitch(k) * 4;
 }
 
 extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b,
@@ -2762,11 +2950,11 @@ extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, in
         return NNOPS_INVALID_ARGUMENT;
     }
     uint8_t* nib = static_cast<uint8_t*>(out);
-    uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)((k + 7) / 8 * 8) * (size_t)nbn * 16));
+    uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)nbn * (size_t)prepack_q41_nib_pitch(k)));
     const int64_t blocks = k * nbn;
     hipLaunchKernelGGL(prepack_q4_1_kn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), b, ldb_bytes, (int)k, (int)nbn, nib, dm,
-                       prepack_q41_dmp(n));
+                       prepack_q41_dm_pitch(k));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
 

@@ -105,15 +105,19 @@ def test_gemm_q4_1_rejects_before_any_launch():
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
     g.ldb_bytes = 42  # not a multiple of 4
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
-    # the prepacked planes (b_soa) have one nibble-row pitch, nbn * 16: the
-    # GEMV and the ring place the 8-row groups by it, so a padded pitch is
-    # rejected rather than read two different ways
-    g.trans_b, g.b_soa, g.b_dm, g.ldb_dm = 0, 1, 4096, 4
-    g.ldb_bytes = 32
+    # the prepacked planes (b_soa) have fixed block-column pitches, ceil(K/8)
+    # * 128 nibble bytes and K rounded up to 64 d|m dwords: every kernel
+    # places the block columns by them, so a padded pitch is rejected rather
+    # than read two different ways (K = 64: 1024 bytes, 64 dwords)
+    g.trans_b, g.b_soa, g.b_dm = 0, 1, 4096
+    g.ldb_bytes, g.ldb_dm = 1024 + 128, 64
     g.m = 0  # an empty problem returns before the argument checks: ok
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.OK
     g.m = 2
-    g.ldb_bytes = 48
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.ldb_bytes, g.ldb_dm = 1024, 128
+    assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
+    g.ldb_bytes, g.ldb_dm = 32, 64   # the old nbn * 16 row pitch
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
 
 
@@ -293,7 +297,7 @@ def test_prepack_query_descriptor():
     # [N, K], pitched at whole blocks so that N rows cover the two planes
     q_bytes = lib.nnops_hip_prepack_q4_1_bytes(256, 100)
     nbn = 4
-    assert q_bytes == ((256 * nbn * 16 + 255) // 256) * 256 + 256 * 4 * 4
+    assert q_bytes == ((nbn * 32 * 128 + 255) // 256) * 256 + nbn * 256 * 4
     qop = na.MatMul(transpose_b=False)
     ins = (L.Tensor * 1)(desc([256, 100], na.DT_Q4_1))
     out = (L.Tensor * 1)()

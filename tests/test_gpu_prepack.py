@@ -211,11 +211,11 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
 
 @pytest.mark.parametrize("K,N", [(64, 200), (96, 1024), (37, 72)])
 def test_q4_1_packed_blob_layout(K, N):
-    """The packed q4_1 blob byte for byte: the k-blocked nibble plane (per 8
-    rows, per block, per nibble dword the 8 rows' dwords; rows past K zero),
-    then at align_up(ceil(K/8)*8*nbn*16, 256) the d|m plane [K][nbn rounded
-    up to 4] (padding zeroed), restated here with numpy from the raw [K][nbn]
-    20-byte blocks."""
+    """The packed q4_1 blob byte for byte, one block column after another:
+    the k-blocked nibble plane (block column j: per 8 rows, per nibble dword
+    the 8 rows' dwords; rows past K zero), then at align_up(nbn*ceil(K/8)*128,
+    256) the d|m plane [nbn][K rounded up to 64] (padding zeroed), restated
+    here with numpy from the raw [K][nbn] 20-byte blocks."""
     announce(f"prepack q4_1 blob layout {K}x{N}")
     blk = dg.q4_1_blocks(K * 7 + N, K, N)                # uint8 [K, nbn*20]
     nbn = (N + 31) // 32
@@ -228,11 +228,12 @@ def test_q4_1_packed_blob_layout(K, N):
     kg = (K + 7) // 8
     q32 = np.zeros((kg * 8, nbn, 4), np.uint32)
     q32[:K] = np.ascontiguousarray(b3[:, :, 4:]).view(np.uint32).reshape(K, nbn, 4)
-    nib = q32.reshape(kg, 8, nbn, 4).transpose(0, 2, 3, 1).reshape(-1).view(np.uint8)
-    dmp = (nbn + 3) // 4 * 4
-    dm = np.zeros((K, dmp, 4), np.uint8)
-    dm[:, :nbn, :] = b3[:, :, :4]
-    off = (kg * 8 * nbn * 16 + 255) // 256 * 256
-    assert na.lib().nnops_hip_prepack_q4_1_bytes(K, N) == off + K * dmp * 4
+    # [kg][8 rows][nbn][4 dwords] -> [nbn][kg][4 dwords][8 rows]
+    nib = q32.reshape(kg, 8, nbn, 4).transpose(2, 0, 3, 1).reshape(-1).view(np.uint8)
+    kdm = (K + 63) // 64 * 64
+    dm = np.zeros((nbn, kdm, 4), np.uint8)
+    dm[:, :K, :] = b3[:, :, :4].transpose(1, 0, 2)
+    off = (nbn * kg * 128 + 255) // 256 * 256
+    assert na.lib().nnops_hip_prepack_q4_1_bytes(K, N) == off + nbn * kdm * 4
     np.testing.assert_array_equal(got[:nib.size], nib)
     np.testing.assert_array_equal(got[off:off + dm.size], dm.reshape(-1))
