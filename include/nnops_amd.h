@@ -304,6 +304,20 @@ typedef struct NnopsFpOutArgs {
 
 int nnops_hip_fp_output_pass(const NnopsFpOutArgs* args, void* stream);
 
+/* The Q4_1 GEMM with its output pass fused into the write-back: the product
+ * of `g` (its c, ldc and out_kind unused) goes through `pass` (src and
+ * ld_src unused; rows = g->m, n = g->n, or g->n / 2 for the gated form, whose
+ * weight holds the gate rows and then the value rows) straight to pass->out,
+ * with the same operations and rounding as nnops_hip_gemm_q4_1 into f32
+ * followed by nnops_hip_fp_output_pass (nnops' Linear write-back,
+ * src/backend/cpu/matmul/linear.cpp:74-170,233-282). Taken by the gated
+ * form on the blocks-along-K ring route (trans_b, f16 A, K % 64 == 0,
+ * 16-byte A rows, M past the GEMV and skinny shapes), where it saves the
+ * f32 staging of both halves; NNOPS_UNSUPPORTED otherwise (the plain pass
+ * included: in the write-back it costs more than its staging), with nothing
+ * launched, and the caller runs the two-step form. No workspace. */
+int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsFpOutArgs* pass, void* stream);
+
 /* QuantizeLinear / DequantizeLinear over a rows x cols view (row strides in
  * elements), and the activation quantization of the fp-activation int8 MatMul.
  * Replaces nnops' quantize_linear_impl / dequantize_linear_impl

@@ -121,6 +121,7 @@ class FpOutArgs(C.Structure):
         ("min_clip", C.c_float), ("max_clip", C.c_float),
         ("add_to", C.c_int32), ("residual_pre", C.c_int32), ("gated", C.c_int32),
         ("gate_act", C.c_int32), ("gate_alpha", C.c_float), ("gate_beta", C.c_float), ("gate_limit", C.c_float),
+        ("matmul_order", C.c_int32), ("alpha", C.c_float), ("beta", C.c_float),
     ]
 
 
@@ -134,6 +135,7 @@ SIGNATURES = {
     "nnops_hip_gemm_fp_workspace_size": (C.c_size_t, [C.POINTER(GemmFpArgs)]),
     "nnops_hip_gemm_fp": (C.c_int, [C.POINTER(GemmFpArgs), C.c_void_p, C.c_size_t, C.c_void_p]),
     "nnops_hip_fp_output_pass": (C.c_int, [C.POINTER(FpOutArgs), C.c_void_p]),
+    "nnops_hip_gemm_q4_1_fused": (C.c_int, [C.POINTER(GemmQ41Args), C.POINTER(FpOutArgs), C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
     "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
     "nnops_hip_prepack_q4_1_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),

@@ -738,12 +738,23 @@ Status run_quant(const QuantCall& q, TensorView& out, std::span<const TensorView
             xb.b = reinterpret_cast<const uint8_t*>(b.ptr<const char>() + batch_offset(bi, g, g.b_batch, b_mat));
             char* cb = out.ptr<char>() + batch_offset(bi, g, g.out_batch, c_mat);
             xb.c = pass ? workspace : static_cast<void*>(cb);
+            if (pass) {
+                // the output pass in the GEMM's write-back where its route
+                // takes it, else the GEMM into the workspace and the pass
+                fo.out = cb;
+                const int rf = nnops_hip_gemm_q4_1_fused(&xb, &fo, stream);
+                if (rf == NNOPS_OK) {
+                    continue;
+                }
+                if (rf != NNOPS_UNSUPPORTED) {
+                    return from_code(rf);
+                }
+            }
             const int rc = nnops_hip_gemm_q4_1(&xb, gemm_ws, need, stream);
             if (rc != NNOPS_OK) {
                 return from_code(rc);
             }
             if (pass) {
-                fo.out = cb;
                 if (const int rp = nnops_hip_fp_output_pass(&fo, stream); rp != NNOPS_OK) {
                     return from_code(rp);
                 }

@@ -9,62 +9,10 @@
 //                 every float operation a separately rounded one, in the
 //                 reference's order. Bound: HBM (rows x n x (4 + 4 or 2)
 //                 bytes, twice the source columns when gated).
-#include "common.hpp"
+#include "fp_out.hpp"
 
 namespace nnops_amd {
 namespace {
-
-struct FpOut {
-    const float* src;
-    int64_t ld_src;
-    void* out;
-    int64_t ld_out;
-    int64_t rows;
-    int n;
-    int out_f16;
-    const void* bias;
-    EpiParams ep;               // act, act_alpha, act_beta, min_clip, max_clip, out_kind
-    int add_to, residual_pre;
-    int gated, gate_act;
-    float gate_alpha, gate_beta, gate_limit;
-    int mm;                     // MatMul's order: alpha P + T(beta old + bias)
-    float alpha, beta;
-};
-
-__device__ __forceinline__ float round_out(bool f16, float x)
-{
-    return f16 ? (float)(_Float16)x : x;
-}
-
-__device__ __forceinline__ float bias_at(const FpOut& p, int c)
-{
-    if (p.bias == nullptr) {
-        return 0.0f;
-    }
-    return p.out_f16 ? (float)static_cast<const _Float16*>(p.bias)[c] : static_cast<const float*>(p.bias)[c];
-}
-
-// The gate activations of gate_act_scalar (gate_combine.hpp:70-85), with the
-// device library's expf / tanhf.
-__device__ __forceinline__ float gate_act(const FpOut& p, float g)
-{
-    switch (p.gate_act) {
-    case NNOPS_ACT_SILU:
-        return __fdiv_rn(g, __fadd_rn(1.0f, expf(__fmul_rn(-p.gate_alpha, g))));
-    case NNOPS_ACT_GELU: {
-        const float inner = __fadd_rn(g, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, g), g), g));
-        return __fmul_rn(__fmul_rn(0.5f, g), __fadd_rn(1.0f, tanhf(__fmul_rn(0.7978845608028654f, inner))));
-    }
-    case NNOPS_ACT_RELU:
-        return g > 0.0f ? g : 0.0f;
-    case NNOPS_ACT_SIGMOID:
-        return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
-    case NNOPS_ACT_TANH:
-        return tanhf(g);
-    default:
-        return g;
-    }
-}
 
 __global__ __launch_bounds__(256) void fp_out_pass(FpOut p, int cblocks)
 {
@@ -103,53 +51,9 @@ __global__ __launch_bounds__(256) void fp_out_pass(FpOut p, int cblocks)
             break;
         }
         const int c = c0 + e;
-        float old = 0.0f;
-        const float beta = p.residual_pre ? 1.0f : p.beta;
-        if (p.mm ? beta != 0.0f : p.add_to) {
-            old = f16 ? (float)reinterpret_cast<const _Float16*>(orow)[c] : reinterpret_cast<const float*>(orow)[c];
-        }
-        float y;
-        if (p.mm) {
-            // the accumulator init (C primed with beta old + bias, stored in
-            // the output type), then the scaled product joins it
-            float init = 0.0f;
-            if (p.bias != nullptr) {
-                init = beta == 0.0f ? bias_at(p, c) : round_out(f16, __fadd_rn(__fmul_rn(old, beta), bias_at(p, c)));
-            } else if (beta == 1.0f) {
-                init = old;
-            } else if (beta != 0.0f) {
-                init = round_out(f16, __fmul_rn(old, beta));
-            }
-            const float prod = p.alpha == 1.0f ? a[e] : __fmul_rn(a[e], p.alpha);
-            y = apply_act_fp(p.ep, __fadd_rn(prod, init));
-        } else if (p.gated) {
-            // the reference's [rows, 2n] tile is of the output's type
-            float g = round_out(f16, __fadd_rn(a[e], bias_at(p, c)));
-            float u = round_out(f16, __fadd_rn(v[e], bias_at(p, p.n + c)));
-            if (__builtin_isfinite(p.gate_limit)) {
-                g = fmaxf(fminf(g, p.gate_limit), -p.gate_limit);
-                u = fmaxf(fminf(u, p.gate_limit), -p.gate_limit);
-            }
-            y = apply_act_fp(p.ep, __fmul_rn(gate_act(p, g), __fadd_rn(u, p.gate_beta)));
-            if (p.add_to) {
-                // the combined value is of the destination's type before it accumulates
-                y = __fadd_rn(old, round_out(f16, y));
-            }
-        } else {
-            y = __fadd_rn(a[e], bias_at(p, c));
-            if (p.add_to && p.residual_pre) {
-                y = __fadd_rn(y, old);
-            }
-            y = apply_act_fp(p.ep, y);
-            if (p.add_to && !p.residual_pre) {
-                y = __fadd_rn(round_out(f16, y), old);
-            }
-        }
-        if (f16) {
-            reinterpret_cast<_Float16*>(orow)[c] = (_Float16)y;
-        } else {
-            reinterpret_cast<float*>(orow)[c] = y;
-        }
+        const float y = fp_out_value(p, a[e], v[e], fp_out_old(p, orow, c), bias_at(p, c),
+                                     p.gated ? bias_at(p, p.n + c) : 0.0f);
+        fp_out_store(p, orow, c, y);
     }
 }
 
@@ -160,26 +64,20 @@ bool gate_act_ok(int a)
 }
 
 }  // namespace
-}  // namespace nnops_amd
 
-using namespace nnops_amd;
-
-extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
+int make_fp_out(const NnopsFpOutArgs* a, FpOut& p)
 {
     if (a == nullptr || a->rows < 0 || a->n < 0 || a->n > INT32_MAX) {
         return NNOPS_INVALID_ARGUMENT;
     }
-    if (a->rows == 0 || a->n == 0) {
-        return NNOPS_OK;
-    }
-    if (a->src == nullptr || a->out == nullptr || a->ld_src < (a->gated ? 2 : 1) * a->n || a->ld_out < a->n) {
+    if (a->out == nullptr || a->ld_out < a->n) {
         return NNOPS_INVALID_ARGUMENT;
     }
     if (a->act < NNOPS_ACT_NONE || a->act > NNOPS_ACT_RELU6 || (a->gated && !gate_act_ok(a->gate_act)) ||
         (a->gated && a->add_to && a->residual_pre) || (a->gated && a->matmul_order)) {
         return NNOPS_UNSUPPORTED;
     }
-    FpOut p{};
+    p = FpOut{};
     p.src = a->src;
     p.ld_src = a->ld_src;
     p.out = a->out;
@@ -204,6 +102,28 @@ extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
     p.mm = a->matmul_order != 0;
     p.alpha = a->alpha;
     p.beta = a->beta;
+    return NNOPS_OK;
+}
+
+}  // namespace nnops_amd
+
+using namespace nnops_amd;
+
+extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
+{
+    if (a == nullptr || a->rows < 0 || a->n < 0 || a->n > INT32_MAX) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    if (a->rows == 0 || a->n == 0) {
+        return NNOPS_OK;
+    }
+    if (a->src == nullptr || a->ld_src < (a->gated ? 2 : 1) * a->n) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    FpOut p;
+    if (const int rc = make_fp_out(a, p); rc != NNOPS_OK) {
+        return rc;
+    }
     const int64_t cblocks = (a->n + 1023) / 1024;
     if (cblocks * a->rows > INT32_MAX) {
         return NNOPS_UNSUPPORTED;

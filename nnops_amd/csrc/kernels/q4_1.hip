@@ -37,7 +37,7 @@
 //                   f32, rounded once) into LDS, A tiles staged k-contiguous.
 //   prepack_q4_1_kn prepackWeights of a blocks-along-N weight: its nibble
 //                   plane and its d|m plane.
-#include "common.hpp"
+#include "fp_out.hpp"
 
 
 #include <atomic>
@@ -60,6 +60,7 @@ struct Q41Kern {
     int splits;
     const uint32_t* bdm; // SoA d|m plane, block column j at j * ldbdm (prepacked blocks along N)
     int64_t ldbdm;       // u32 elements
+    FpOut fo;            // the fused gated combine (gemm_q4_1_ring with GATED)
 };
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
@@ -2099,9 +2100,18 @@ __device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v
     return __builtin_bit_cast(v8h, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
 }
 
-template <bool OUT16, int NS, int WM, int WN = 4>
+// GATED: Linear's gated form with its output pass p.fo fused: the tile covers
+// output columns 128 tn .. + 127 and stages the weight's gate rows there and
+// its value rows (N / 2 further) in its second half, so waves 0-3 hold the
+// gate products and waves 4-7 the value products of the same columns, which
+// meet through LDS for the combine. (Fusing the plain pass -- bias, residual,
+// activation -- measured slower than the separate pass: 108 against 98 us at
+// 512 x 14336 x 4096, the pass's arithmetic then running with the matrix
+// cores idle; the gated form saves the larger staging: 196 -> 184 us.)
+template <bool OUT16, int NS, int WM, int WN = 4, bool GATED = false>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 {
+    static_assert(!GATED || (WM == 1 && WN == 8), "gated: one wave per 32 columns, halves 4 waves apart");
     constexpr int W = WM * WN;                      // waves: WM along M x WN along N
     constexpr int QA = 16 / W, QB = 16 / W;         // 1 KiB pieces per wave per stage
     constexpr int L = QA + QB;
@@ -2118,7 +2128,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
         bid = (bid & 7) * (nb >> 3) + (bid >> 3);     // consecutive logical tiles on one XCD
     }
     const int tm = bid % tiles_m, tn = bid / tiles_m; // the M tiles of a column band share B in L2
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM;
+    const int n0 = GATED ? tn * (BN / 2) : tn * BN;   // gated: output columns; the weight has 2 p.fo.n rows
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wn0 = (wave % WN) * TN;
@@ -2127,8 +2138,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 
     // A: rows 8 * (4 * wave + i) + lane / 8; B raw: rows 16 * (4 * wave + i) + lane / 4
     const QBufRsrc rsa = q_buffer_rsrc(static_cast<const _Float16*>(p.a) + (int64_t)m0 * p.lda, 0x7fffffffu);
-    const int64_t b_bytes = (int64_t)(p.n - n0) * p.ldb;
-    const QBufRsrc rsb = q_buffer_rsrc(p.b + (int64_t)n0 * p.ldb,
+    const int64_t b_bytes = (int64_t)(p.n - (GATED ? 0 : n0)) * p.ldb;
+    const QBufRsrc rsb = q_buffer_rsrc(p.b + (GATED ? 0 : (int64_t)n0 * p.ldb),
                                        (uint32_t)std::min<int64_t>(b_bytes, 0x7fffffff));
     int a_off[QA], b_off[QB];
 #pragma unroll
@@ -2141,7 +2152,14 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
     for (int i = 0; i < QB; ++i) {
         const int rb = 16 * (QB * wave + i) + (lane >> 2);
         const int cb = (lane & 3) ^ ((rb >> 2) & 3);
-        b_off[i] = min(rb, p.n - 1 - n0) * (int)p.ldb + cb * 16;
+        if constexpr (GATED) {
+            // tile rows 0..127: gate rows n0 + rb; 128..255: value rows
+            // p.fo.n + n0 + rb - 128 (each half clamped to its own rows)
+            const int half = rb >> 7, r = min(n0 + (rb & 127), p.fo.n - 1);
+            b_off[i] = (half * p.fo.n + r) * (int)p.ldb + cb * 16;
+        } else {
+            b_off[i] = min(rb, p.n - 1 - n0) * (int)p.ldb + cb * 16;
+        }
     }
     auto issue = [&](int s) {
         uint8_t* base = ring + (s % NS) * kStage;
@@ -2262,6 +2280,46 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
     }
 
     // C[m][n]: lane holds column n = (lane & 31) of fragment j, rows 8 (r / 4) + 4 (lane >> 5) + r % 4
+    // The gated combine. The pass is too large to inline once per register
+    // (a call would put its parameters on the stack), so the products go
+    // through the ring (free once every wave is past it) and a loop of a few
+    // rows per step applies it: xs[wave][i * 16 + r][lane] is product row
+    // 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 of the wave's column lane % 32.
+    // Gate wave w (0-3) and value wave w + 4 hold the two products of the
+    // same outputs; the gate wave combines rows 0-63, the value wave 64-127.
+    if constexpr (GATED) {
+        static_assert(W * FM * 16 * 64 * 4 <= NS * kStage, "the products fit the ring");
+        const FpOut fo = p.fo;
+        __syncthreads();
+        float* xs = reinterpret_cast<float*>(ring);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                xs[((wave * FM + i) * 16 + r) * 64 + lane] = acc[i][0][r];
+            }
+        }
+        __syncthreads();
+        const int gw = wave & 3;
+        const int n = n0 + gw * 32 + (lane & 31);
+        if (n >= fo.n) {
+            return;
+        }
+        const float bg = bias_at(fo, n), bu = bias_at(fo, fo.n + n);
+        const int first = wave >= 4 ? FM * 8 : 0;
+#pragma unroll 4
+        for (int q = 0; q < FM * 8; ++q) {
+            const int ir = first + q, i = ir >> 4, r = ir & 15;
+            const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < p.m) {
+                char* orow = static_cast<char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
+                const float g = xs[((gw * FM) * 16 + ir) * 64 + lane];
+                const float v = xs[(((gw + 4) * FM) * 16 + ir) * 64 + lane];
+                fp_out_store(fo, orow, n, fp_out_value(fo, g, v, fp_out_old(fo, orow, n), bg, bu));
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int n = n0 + wn0 + j * 32 + (lane & 31);
@@ -2924,6 +2982,51 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
         }
     }
+    return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+}
+
+extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsFpOutArgs* pass, void* stream)
+{
+    if (g == nullptr || pass == nullptr) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    // the blocks-along-K ring route only (f16 A past the GEMV and skinny
+    // shapes); anything else is the caller's two-step form
+    if (!g->trans_b || g->b_soa || !g->a_f16 || g->m <= 0 || g->n <= 0 || g->k <= 0 || g->m > INT32_MAX ||
+        g->n > INT32_MAX || g->k > INT32_MAX || g->a == nullptr || g->b == nullptr || use_gemv(*g) ||
+        skinny_ok(*g) || g->k % 64 != 0 || (g->lda % 8) != 0 || ((uintptr_t)g->a & 15) != 0 || g->lda < g->k ||
+        g->ldb_bytes < (g->k + 31) / 32 * 20 || (g->ldb_bytes & 3) || ((uintptr_t)g->b & 3)) {
+        return NNOPS_UNSUPPORTED;
+    }
+    FpOut fo;
+    if (const int rc = make_fp_out(pass, fo); rc != NNOPS_OK) {
+        return rc;
+    }
+    if (pass->rows != g->m || pass->n * (pass->gated ? 2 : 1) != g->n) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    // only the gated form gains: the plain pass's arithmetic in the GEMM's
+    // write-back costs more than the staging it saves
+    if (!pass->gated) {
+        return NNOPS_UNSUPPORTED;
+    }
+    // the gated tile addresses both halves of the weight from its start
+    if (pass->gated && g->n * g->ldb_bytes >= INT32_MAX) {
+        return NNOPS_UNSUPPORTED;
+    }
+    Q41Kern k{};
+    k.a = g->a;
+    k.b = g->b;
+    k.m = (int)g->m;
+    k.n = (int)g->n;
+    k.k = (int)g->k;
+    k.lda = g->lda;
+    k.ldb = g->ldb_bytes;
+    k.fo = fo;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t tiles_m = (g->m + 127) / 128;
+    const unsigned tiles = (unsigned)(tiles_m * ((pass->n + 127) / 128));
+    hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8, true>), dim3(tiles), dim3(512), 0, s, k);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
 

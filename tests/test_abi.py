@@ -121,6 +121,32 @@ def test_gemm_q4_1_rejects_before_any_launch():
     assert lib.nnops_hip_gemm_q4_1(C.byref(g), None, 0, None) == na.INVALID_ARGUMENT
 
 
+def test_gemm_q4_1_fused_declines_before_any_launch():
+    """nnops_hip_gemm_q4_1_fused takes only the blocks-along-K ring route and
+    answers NNOPS_UNSUPPORTED, launching nothing, for the others (the caller
+    then runs the two-step form); missing arguments are invalid."""
+    from nnops_amd._lib import FpOutArgs
+    lib = na.lib()
+    g = na.GemmQ41Args()
+    fo = FpOutArgs()
+    assert lib.nnops_hip_gemm_q4_1_fused(None, C.byref(fo), None) == na.INVALID_ARGUMENT
+    assert lib.nnops_hip_gemm_q4_1_fused(C.byref(g), None, None) == na.INVALID_ARGUMENT
+    g.m, g.n, g.k = 256, 512, 256
+    g.a = g.b = 256
+    g.lda, g.ldb_bytes, g.a_f16, g.trans_b = 256, 160, 1, 1
+    fo.out, fo.ld_out, fo.rows, fo.n = 256, 512, 256, 512
+    for field, value in (("trans_b", 0), ("a_f16", 0), ("m", 2), ("m", 16), ("k", 96), ("lda", 260)):
+        old = getattr(g, field)
+        setattr(g, field, value)
+        assert lib.nnops_hip_gemm_q4_1_fused(C.byref(g), C.byref(fo), None) == na.UNSUPPORTED, field
+        setattr(g, field, old)
+    # the pass's own checks: an unknown gate activation, a row count other than M
+    fo.gated, fo.gate_act, fo.n = 1, na.ACT_HARDSWISH, 256
+    assert lib.nnops_hip_gemm_q4_1_fused(C.byref(g), C.byref(fo), None) == na.UNSUPPORTED
+    fo.gate_act, fo.rows = na.ACT_SILU, 255
+    assert lib.nnops_hip_gemm_q4_1_fused(C.byref(g), C.byref(fo), None) == na.INVALID_ARGUMENT
+
+
 def test_gemm_fp_rejects_before_any_launch():
     lib = na.lib()
     g = na.GemmFpArgs()
