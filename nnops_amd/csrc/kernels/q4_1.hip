@@ -2738,6 +2738,10 @@ inline bool skinny_ok(const NnopsGemmQ41Args& g)
            ((uintptr_t)g.a & 15) == 0 && 32 * g.ldb_bytes < INT32_MAX && g.m * g.lda * es < INT32_MAX;
 }
 
+// rows of A up to which the prepacked planes take the GEMV passes rather than
+// the ring (M = 12: 65 us against 77)
+constexpr int64_t kBcmMaxM = 12;
+
 // The one-launch GEMV over the prepacked planes (gemv_q4_1_bcm): f16 A with
 // 16-byte-aligned rows, K % 8 == 0.
 inline bool bcm_ok(const NnopsGemmQ41Args& g)
@@ -2938,6 +2942,27 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     hipLaunchKernelGGL(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
                 }
             }
+        }
+    } else if (bcm_ok(*g) && g->m <= kBcmMaxM) {
+        // a few rows of A over the prepacked planes: the one-launch GEMV, up
+        // to 8 rows per pass (its arithmetic grows with the rows: config 4's
+        // shape 10.6 / 13.7 / 22.7 / 42.9 us for 1 / 2 / 4 / 8 rows, the ring
+        // 77-85 us for any M up to 128)
+        for (int m0 = 0; m0 < k.m;) {
+            const int rem = k.m - m0;
+            const int mt = rem > 4 ? 8 : rem > 2 ? 4 : 2;
+            Q41Kern kk = k;
+            kk.m = std::min(mt, rem);
+            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
+            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
+            if (mt == 2) {
+                hipLaunchKernelGGL((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+            } else if (mt == 4) {
+                hipLaunchKernelGGL((gemv_q4_1_bcm<4, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+            } else {
+                hipLaunchKernelGGL((gemv_q4_1_bcm<8, 8, 2>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+            }
+            m0 += mt;
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

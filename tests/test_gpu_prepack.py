@@ -135,10 +135,11 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
 @pytest.mark.parametrize("M,K,N", [(5, 1000, 77), (64, 96, 40), (64, 256, 200), (3, 64, 200), (3, 37, 72),
                                    (1, 97, 40)])
 def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
-    """Ragged shapes. K % 64 != 0 with M > 2: the packed weight and the raw
-    one both take the generic MFMA kernel (the same decode and order, so the
-    same bits). N = 200 (7 blocks per row, d|m rows padded to 8): the packed
-    weight takes the ring. All within the Q4_1 tolerance of the oracle."""
+    """Ragged shapes. K % 64 != 0 with M > 2 and no GEMV pass (K % 8 != 0 or
+    M > 12): the packed weight and the raw one both take the generic MFMA
+    kernel (the same decode and order, so the same bits). N = 200 (7 blocks
+    per row): the packed weight takes the GEMV passes (M <= 12) or the ring.
+    All within the Q4_1 tolerance of the oracle."""
     import torch
     announce(f"prepack q4_1 ragged {M}x{K}x{N}")
     a = dg.normal(M + K, (M, K)).astype(np.float16)
@@ -147,7 +148,7 @@ def test_matmul_q4_1_prepacked_ragged_k(M, K, N):
     wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
     _, packed = op.prepack(wt)
     got = run(op, na.tensor(dev(a)), packed, torch.float32, (M, N))
-    if M > 2 and K % 64:
+    if M > 2 and K % 64 and (M > 12 or K % 8):
         np.testing.assert_array_equal(got, run(op, na.tensor(dev(a)), wt, torch.float32, (M, N)))
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
     err = float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2))))
@@ -207,6 +208,31 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
         for got in (got_p, got_r):
             err = float(np.max(np.abs(got[bi].astype(np.float32) - want)) / scale)
             assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("f16_out", [False, True])
+@pytest.mark.parametrize("M", [3, 5, 8, 12])
+def test_matmul_q4_1_prepacked_few_rows(M, f16_out):
+    """3 <= M <= 12 rows of f16 A over the packed planes take the one-launch
+    GEMV in passes of up to 8 rows (products a * d split exactly, like the M
+    <= 2 passes): within the Q4_1 bar of the f32 dequant oracle, rows of
+    every pass checked, f32 and f16 destinations, N ragged (not a multiple of
+    the 32-column block)."""
+    import torch
+    announce(f"prepack q4_1 few rows M={M} f16_out={f16_out}")
+    K, N = 2048, 1000
+    a = dg.normal(950 + M, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(951 + M, K, N)
+    op = na.MatMul(transpose_b=False)
+    wt = na.tensor(dev(blk), dtype=na.DT_Q4_1, shape=[K, N])
+    _, packed = op.prepack(wt)
+    got = run(op, na.tensor(dev(a)), packed, torch.float16 if f16_out else torch.float32, (M, N))
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
+    if f16_out:
+        want = want.astype(np.float16).astype(np.float32)
+    scale = max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2)))
+    err = float(np.max(np.abs(got.astype(np.float32) - want)) / scale)
+    assert err <= 2e-3, err
 
 
 @pytest.mark.parametrize("K,N", [(64, 200), (96, 1024), (37, 72)])
