@@ -396,7 +396,7 @@ def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, n
     operator API: the Q4_1 GEMM / GEMV into the workspace and the combine.
     M=1 rotates over nbuf weights (more than the MALL) so HBM is measured."""
     x = torch.from_numpy(dg.normal(420 + M, (M, K)).astype("float16")).cuda()
-    nb = nbuf if M <= 2 else 1
+    nb = nbuf if M <= 48 else 1
     ws_ = [torch.from_numpy(dg.q4_1_blocks(421 + i, 2 * N, K)).cuda() for i in range(nb)]
     bias = torch.from_numpy((0.1 * dg.normal(425, (2 * N,))).astype("float16")).cuda()
     y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
@@ -425,12 +425,12 @@ def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, n
 
 def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8):
     """Config 4 with the [K][N/32] weight prepacked (MatMul.prepackWeights:
-    the nibble and d|m planes), through the operator API. M=1 rotates over
-    nbuf packed weights (more than the MALL) so HBM is measured."""
+    the nibble and d|m planes), through the operator API. Up to 48 rows of A
+    rotate over nbuf packed weights (more than the MALL) so HBM is measured."""
     a = torch.from_numpy(dg.normal(405, (M, K)).astype("float16")).cuda()
     base = torch.from_numpy(dg.q4_1_blocks(406, K, N)).cuda()
     op = na.MatMul(transpose_b=False)
-    nb = nbuf if M <= 2 else 1
+    nb = nbuf if M <= 48 else 1
     packed = []
     for i in range(nb):
         raw = base if i == 0 else torch.roll(base, shifts=20 * i, dims=1).contiguous()
@@ -451,7 +451,7 @@ def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nb
 
     t = Timer(stream).time(step, steps, warmup)
     out = {"us": t["mean_ms"] * 1e3, "M": M, "K": K, "N": N, "weight_layout": "[K][N/32 blocks], prepacked planes"}
-    if M <= 2:
+    if M <= 16:
         nbytes = N * (K // 32) * 20 + K * M * 2 + N * M * 4
         out.update(gbs=nbytes / (t["mean_ms"] * 1e-3) / 1e9, bytes=nbytes)
         out["frac_hbm"] = out["gbs"] / PEAK_HBM_GBS
@@ -846,6 +846,7 @@ def main():
         secondary["cfg4_q4_1_gemm_m512_f32a"] = q41_gemm_case(torch, dg, na, stream, few, wu, a_f32=True)
         secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
         secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
+        secondary["cfg4_q4_1_m8_decode_batch_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=8)
         secondary["gated_ffn_swiglu_m1"] = gated_ffn_case(torch, dg, na, stream, st, wu)
         secondary["gated_ffn_swiglu_m512"] = gated_ffn_case(torch, dg, na, stream, few, wu, M=512)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, few, wu)
