@@ -603,10 +603,12 @@ __device__ __forceinline__ BufRsrc buffer_rsrc(const void* base)
 }
 
 // 16 bytes per lane from base + voff + soff into LDS at lds + 16 * lane.
+// AUX: the cache policy bits (2: non-temporal, for data read once).
+template <int AUX = 0>
 __device__ __forceinline__ void buffer_load_lds16(BufRsrc r, int8_t* lds, int voff, int soff)
 {
 #if __HIP_DEVICE_COMPILE__
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, AUX);
 #else
     (void)r, (void)lds, (void)voff, (void)soff;
 #endif
@@ -1387,7 +1389,7 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_lds(GemmI8Kern p)
     for (int kb = wave * KW; kb < p.k; kb += W * KW) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            buffer_load_lds16(rs, st + r * PITCH, (int)((int64_t)r * p.ldb) + kb + lane * 16, 0);
+            buffer_load_lds16<2>(rs, st + r * PITCH, (int)((int64_t)r * p.ldb) + kb + lane * 16, 0);
         }
         v4i fa[T];
 #pragma unroll

@@ -179,10 +179,12 @@ __device__ __forceinline__ v4i q_buffer_load16_sc1(QBufRsrc r, int voff)
 #endif
 }
 
+// AUX: the cache policy bits (2: non-temporal, for weights read once)
+template <int AUX = 0>
 __device__ __forceinline__ void q_buffer_load_lds16(QBufRsrc r, uint8_t* lds, int voff, int soff)
 {
 #if __HIP_DEVICE_COMPILE__
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, NNOPS_LPTR(lds), 16, voff, soff, 0, AUX);
 #else
     (void)r, (void)lds, (void)voff, (void)soff;
 #endif
@@ -1059,7 +1061,7 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             if (q < nq) {
-                q_buffer_load_lds16(rs, dst + (wave + W * q) * 1024, min(prow[q], rmax) * (int)p.ldb + pcol[q],
+                q_buffer_load_lds16<2>(rs, dst + (wave + W * q) * 1024, min(prow[q], rmax) * (int)p.ldb + pcol[q],
                                     st * kKnRS * (int)p.ldb);
             }
         }
@@ -1503,7 +1505,7 @@ __global__ __launch_bounds__(128 * KH) void gemv_q4_1_skinny(Q41Kern p)
         const int sg = s0 + s;
 #pragma unroll
         for (int q = 0; q < kSkWPieces; ++q) {
-            q_buffer_load_lds16(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], sg * 160);
+            q_buffer_load_lds16<2>(rw, dst + (wave * kSkWPieces + q) * 1024, w_off[q], sg * 160);
         }
 #pragma unroll
         for (int q = 0; q < kSkAPieces / 2; ++q) {
