@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "nnops_amd.h"
 
 namespace nnops_amd {
@@ -30,6 +32,21 @@ __device__ __forceinline__ void wait_vmcnt()
 {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Launch epochs for the split-completion flags of the one-launch split
+// kernels: unique in the process and never 0. Consecutive counter values are
+// spread over 64 bits (splitmix64's finalizer), so a flag word that a caller's
+// workspace happens to hold from other work (small integers, float partials)
+// does not pass for this launch's epoch.
+inline uint64_t next_launch_epoch()
+{
+    static std::atomic<uint64_t> counter{0};
+    uint64_t z = counter.fetch_add(1, std::memory_order_relaxed) + 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    return z != 0 ? z : 1;
 }
 
 // ---------------------------------------------------------------------------

@@ -1192,6 +1192,74 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 // summing every TPG-th split with its loads in flight together, then combine
 // with lane shuffles; the first of them runs the output pass. TPG = 4 suits
 // many splits of a small output, TPG = 1 a few splits of a large one.
+// The output pass of 4 consecutive columns nb..nb+3 of row m: its row and
+// column constants and the residual word, loaded before the raw sums arrive
+// (out4_prepare), then the pass itself (out4_store).
+struct Out4 {
+    EpiRow row;
+    EpiCol cols[4];
+    uint32_t oldw;
+    char* crow;
+    int8_t* c8;
+    bool word8;
+};
+
+__device__ __forceinline__ Out4 out4_prepare(const GemmI8Kern& p, int m, int nb)
+{
+    const EpiParams& ep = p.ep;
+    Out4 o{};
+    o.crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+    o.c8 = reinterpret_cast<int8_t*>(o.crow) + nb;
+    o.word8 = !epi_is_fp(ep) && ep.out_kind != NNOPS_OUT_S32 && ((uintptr_t)o.c8 & 3) == 0;
+    o.row = epi_row(ep, m);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        o.cols[e] = epi_col(ep, nb + e);
+    }
+    if (o.word8 && ep.add_to) {
+        o.oldw = *reinterpret_cast<const uint32_t*>(o.c8);
+    }
+    return o;
+}
+
+__device__ __forceinline__ void out4_store(const GemmI8Kern& p, const Out4& o, int nb, v4i raw)
+{
+    const EpiParams& ep = p.ep;
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    if (epi_is_fp(ep)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            epi_store(ep, o.row, o.cols[e], raw[e], o.crow, nb + e);
+        }
+        return;
+    }
+    if (ep.out_kind == NNOPS_OUT_S32) {
+        int32_t* c32 = reinterpret_cast<int32_t*>(o.crow) + nb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            c32[e] = epi_value(ep, o.row, o.cols[e], raw[e], 0);
+        }
+        return;
+    }
+    if (o.word8) {
+        // one 4-byte read of the residual (in out4_prepare) and one 4-byte store
+        uint32_t outw = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t ob = (o.oldw >> (8 * e)) & 0xffu;
+            const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
+            outw |= ((uint32_t)epi_value(ep, o.row, o.cols[e], raw[e], old) & 0xffu) << (8 * e);
+        }
+        *reinterpret_cast<uint32_t*>(o.c8) = outw;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int32_t old = ep.add_to ? (u8 ? (int32_t)((const uint8_t*)o.c8)[e] : (int32_t)o.c8[e]) : 0;
+        o.c8[e] = (int8_t)epi_value(ep, o.row, o.cols[e], raw[e], old);
+    }
+}
+
 template <int TPG>
 __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk)
 {
@@ -1203,26 +1271,11 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     const int nb = in ? (int)(gid - (int64_t)m * groups) * 4 : 0;
     const int64_t slab = (int64_t)p.m * p.n;
     const int32_t* src = sk.part + (int64_t)m * p.n + nb;
-    // the output pass's row / column constants and the residual word, loaded
-    // with the partials rather than after them
-    const EpiParams& ep = p.ep;
-    const bool s32 = ep.out_kind == NNOPS_OUT_S32;
-    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
-    char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
-    int8_t* c8 = reinterpret_cast<int8_t*>(crow) + nb;
-    const bool word8 = !epi_is_fp(ep) && !s32 && ((uintptr_t)c8 & 3) == 0;
-    EpiRow row{};
-    EpiCol cols[4]{};
-    uint32_t oldw = 0u;
+    // the output pass's constants and the residual word, loaded with the
+    // partials rather than after them
+    Out4 o{};
     if (in && j == 0) {
-        row = epi_row(ep, m);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            cols[e] = epi_col(ep, nb + e);
-        }
-        if (word8 && ep.add_to) {
-            oldw = *reinterpret_cast<const uint32_t*>(c8);
-        }
+        o = out4_prepare(p, m, nb);
     }
     v4i raw = v4i{0, 0, 0, 0};
     if (in) {
@@ -1248,38 +1301,7 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     if (!in || j != 0) {
         return;
     }
-    if (epi_is_fp(ep)) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            epi_store(ep, row, cols[e], raw[e], crow, nb + e);
-        }
-        return;
-    }
-    if (s32) {
-        int32_t* c32 = reinterpret_cast<int32_t*>(crow) + nb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            c32[e] = epi_value(ep, row, cols[e], raw[e], 0);
-        }
-        return;
-    }
-    if (word8) {
-        // one 4-byte read of the residual (above) and one 4-byte store
-        uint32_t outw = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
-            const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
-            outw |= ((uint32_t)epi_value(ep, row, cols[e], raw[e], old) & 0xffu) << (8 * e);
-        }
-        *reinterpret_cast<uint32_t*>(c8) = outw;
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int32_t old = ep.add_to ? (u8 ? (int32_t)((const uint8_t*)c8)[e] : (int32_t)c8[e]) : 0;
-        c8[e] = (int8_t)epi_value(ep, row, cols[e], raw[e], old);
-    }
+    out4_store(p, o, nb, raw);
 }
 
 // ---------------------------------------------------------------------------
@@ -1565,17 +1587,19 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
 // row), so every wave load streams 64 * CPL contiguous bytes of one row. Four
 // rows k..k+3 are transposed in registers (two v_perm per column) into one
 // dword of 4 k-bytes per column, which v_dot4 multiplies with A[m][k..k+3]
-// read through the scalar cache (A is uniform across the wave). The 8 waves of
-// a workgroup take consecutive row ranges of the same columns and are summed
-// through LDS (W = 16 for 16-column groups; W = 4 when a 4-column-group sum
-// buffer would exceed 64 KiB, so two workgroups fit a CU); workgroups of different row ranges write raw int32 partials
-// that gemm_i8_reduce sums and passes through the output pass. Bound: HBM.
+// read through the scalar cache (A is uniform across the wave). Split s of S
+// takes k-quads [s Q / S, (s + 1) Q / S) of a column chunk, and the W waves of
+// its workgroup equal parts of that range, summed through LDS (W = 16 for
+// 16-column groups; 4 or 8 for 4-column groups); the workgroups write raw
+// int32 partials that gemm_i8_reduce sums and passes through the output pass.
+// (Meeting the splits inside the kernel, the last-arriving split summing the
+// others through device-coherent loads, measured slower: the handoff costs
+// more than the second launch.) Bound: HBM.
 // ---------------------------------------------------------------------------
 typedef const __attribute__((address_space(4))) int32_t* ScalarI32Ptr;
 
 struct KnSplit {
     int chunks;       // column chunks of 64 * CPL
-    int rows;         // rows per wave (multiple of 16)
 };
 
 // 4 rows (one dword each, byte c = column c) -> 4 column dwords (byte i = row i)
@@ -1597,15 +1621,20 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk,
 {
     constexpr int D = CPL / 4;                   // dwords per lane per row
     constexpr int U = 4;                         // k-quads per batch (16 rows in flight)
-    __shared__ int32_t red[W][MT * CPL][64];
+    __shared__ int32_t red[W][MT * CPL][65];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int chunk = blockIdx.x % ks.chunks;
     const int split = blockIdx.x / ks.chunks;
     const int n = chunk * 64 * CPL + lane * CPL;
     const bool live = n < p.n;
-    const int k0 = (split * W + wave) * ks.rows;
-    const int k1 = min(p.k, k0 + ks.rows);
+    // split s of S takes k-quads [s Q / S, (s + 1) Q / S) and its W waves
+    // equal parts of that range, so any S fills the CUs evenly
+    const int nquad = p.k / 4;
+    const int qs0 = (int)((int64_t)split * nquad / sk.splits);
+    const int qs1 = (int)((int64_t)(split + 1) * nquad / sk.splits);
+    const int qw0 = qs0 + (int)((int64_t)wave * (qs1 - qs0) / W);
+    const int qw1 = qs0 + (int)((int64_t)(wave + 1) * (qs1 - qs0) / W);
 
     int32_t acc[MT][CPL];
 #pragma unroll
@@ -1616,23 +1645,35 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk,
         }
     }
     const int8_t* bcol = p.b + (live ? n : 0);
-    for (int k = k0; k < k1; k += 4 * U) {
+    for (int q = qw0; q < qw1; q += U) {
+        const int nq = min(U, qw1 - q);       // wave-uniform
+        const int k = 4 * q;
         uint32_t rows[4 * U][D];
 #pragma unroll
         for (int r = 0; r < 4 * U; ++r) {
             const int8_t* src = bcol + (int64_t)(k + r) * p.ldb;
-            if constexpr (D == 4) {
-                const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src));
+            if (r < 4 * nq) {
+                if constexpr (D == 4) {
+                    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src));
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    rows[r][d] = (uint32_t)v[d];
+                    for (int d = 0; d < 4; ++d) {
+                        rows[r][d] = (uint32_t)v[d];
+                    }
+                } else {
+                    rows[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
                 }
             } else {
-                rows[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src));
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    rows[r][d] = 0u;
+                }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            if (u >= nq) {
+                break;
+            }
             int32_t aq[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
@@ -1661,17 +1702,22 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk,
         }
     }
     __syncthreads();
-    // sum over the waves; thread t handles (element e = t / 64 .., lane t % 64)
+    // Sum over the waves. Thread t takes chunk column r = t % (64 CPL) (lane
+    // r / CPL, element r % CPL) of row t / (64 CPL), so consecutive threads
+    // store consecutive int32 partials (the odd row pitch of red keeps their
+    // LDS reads on distinct banks).
+    const int nc0 = chunk * 64 * CPL;
     int32_t* part = sk.part + (int64_t)split * p.m * p.n;
-    for (int e = threadIdx.x >> 6; e < MT * CPL; e += W) {
-        int32_t s = 0;
+    for (int idx = threadIdx.x; idx < MT * CPL * 64; idx += W * 64) {
+        const int m = idx / (CPL * 64);
+        const int r = idx % (CPL * 64);
+        int32_t sum = 0;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
-            s += red[w][e][lane];
+            sum += red[w][m * CPL + r % CPL][r / CPL];
         }
-        const int m = e / CPL, c = e % CPL;
-        if (m < p.m && live) {
-            part[(int64_t)m * p.n + n + c] = s;
+        if (m < p.m && nc0 + r < p.n) {
+            part[(int64_t)m * p.n + nc0 + r] = sum;
         }
     }
 }
@@ -1788,7 +1834,7 @@ struct RingPlan {
 struct KnPlan {
     int cpl = 0;            // columns per lane (0: not taken)
     int w = 0;              // waves per workgroup
-    int chunks = 0, rows = 0, splits = 0;
+    int chunks = 0, splits = 0;
 };
 
 inline int kn_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
@@ -1818,17 +1864,23 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
     const int mt = kn_mt(g.m);
     r.cpl = cpl;
     r.chunks = (int)((g.n + 64 * cpl - 1) / (64 * cpl));
+    // 1024-column chunks for M <= 2 (every load a full 1 KiB row segment, the
+    // shape that streams HBM at full rate), 256 columns beyond. K is split so
+    // the workgroups fill the CUs once (no second round whose tail is
+    // exposed), each split at least 16 rows per wave. (Config 3, M = 1: 11
+    // chunks x 23 splits; 16 splits and 46 splits of 8 waves measured the
+    // same or slower.)
     if (cpl == 16) {
-        // 1024-column x 256-row tiles: 16 waves of 16 rows, every load a full
-        // 1 KiB row segment (the shape that streams HBM at full rate)
         r.w = 16;
-        r.rows = 16;
     } else {
         r.w = (mt * cpl >= 64) ? 4 : 8;
-        const int ks_target = std::max(1, 512 / r.chunks);
-        r.rows = std::max<int>(16, (int)(g.k / ((int64_t)ks_target * r.w)) / 16 * 16);
     }
-    r.splits = (int)((g.k + (int64_t)r.rows * r.w - 1) / ((int64_t)r.rows * r.w));
+    const int per_cu = cpl == 16 ? 1 : 2;
+    const int64_t max_splits = std::max<int64_t>(1, g.k / (16 * r.w));
+    r.splits = (int)std::min<int64_t>(max_splits, std::max(1, 256 * per_cu / r.chunks));
+    if ((int64_t)r.splits * g.m * g.n * 4 >= INT32_MAX) {
+        return KnPlan{};    // the partials' 32-bit buffer offsets
+    }
     return r;
 }
 
@@ -2008,7 +2060,13 @@ void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, i
     const dim3 grid((unsigned)(ks.chunks * sk.splits));
     if (cpl == 16) {
         if constexpr (MT <= 2) {
-            hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 16>), grid, dim3(1024), 0, s, k, sk, ks);
+            if (w == 16) {
+                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 16>), grid, dim3(1024), 0, s, k, sk, ks);
+            } else if (w == 8) {
+                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 8>), grid, dim3(512), 0, s, k, sk, ks);
+            } else {
+                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 4>), grid, dim3(256), 0, s, k, sk, ks);
+            }
         }
     } else if (w == 4) {
         hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
@@ -2035,7 +2093,6 @@ void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t 
     sk.part = part;
     KnSplit ks;
     ks.chunks = r.chunks;
-    ks.rows = r.rows;
     switch (k.m) {
     case 1: launch_kn_mt<1>(k, sk, ks, r.cpl, r.w, s); break;
     case 2: launch_kn_mt<2>(k, sk, ks, r.cpl, r.w, s); break;

@@ -2656,12 +2656,6 @@ __global__ __launch_bounds__(256) void prepack_q4_1_kn(const uint8_t* b, int64_t
 
 constexpr size_t kAlign = 256;
 
-// Launch epochs of the split flags: unique in the process, never 0
-inline uint64_t next_epoch()
-{
-    static std::atomic<uint64_t> e{1};
-    return e.fetch_add(1, std::memory_order_relaxed);
-}
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 inline int kn_splits(const NnopsGemmQ41Args& g)
@@ -2906,7 +2900,7 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 kd.kper = pl.kper;
                 kd.part = static_cast<float*>(workspace);
                 kd.flag = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + align_up(kn_dma_part_bytes(pl)));
-                kd.epoch = next_epoch();
+                kd.epoch = next_launch_epoch();
                 const dim3 grid((unsigned)pl.groups, (unsigned)pl.splits);
                 // 8 waves: four row-pair classes per stage hide the LDS and
                 // dot latencies better than 4 (18.0 -> 17.0 us at config 4)

@@ -33,13 +33,17 @@ def graph_replays_match(fn, out, replays=3):
         assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"replay {r} differs"
 
 
-@pytest.mark.parametrize("M,K,N,out", [(4096, 1024, 1024, "s8"), (333, 14336, 1024, "s8"), (1024, 512, 1024, "f16"),
-                                       (16, 4096, 1024, "s32"), (1, 4096, 2048, "s32")])
-def test_int8_routes_under_graph_replay(M, K, N, out):
+@pytest.mark.parametrize("M,K,N,out,trans_b", [(4096, 1024, 1024, "s8", True), (333, 14336, 1024, "s8", True),
+                                               (1024, 512, 1024, "f16", True), (16, 4096, 1024, "s32", True),
+                                               (1, 4096, 2048, "s32", True), (1, 4096, 11008, "s8", False),
+                                               (2, 4096, 2048, "s32", False), (16, 4096, 2048, "s8", False)])
+def test_int8_routes_under_graph_replay(M, K, N, out, trans_b):
+    """[K,N] rows (trans_b False) take the one-launch column GEMV, whose split
+    flags are cleared by the summing workgroup: replays reuse its epoch."""
     import torch
-    announce(f"graph int8 {M}x{K}x{N} {out}")
+    announce(f"graph int8 {M}x{K}x{N} {out} trans_b={trans_b}")
     a = dev(dg.act_s8(M + K, (M, K)))
-    w = dev(dg.ints(N + 1, (N, K), -127, 127))
+    w = dev(dg.ints(N + 1, (N, K) if trans_b else (K, N), -127, 127))
     sb = dev(dg.uniform(3, (N,), 0.001, 0.01))
     tdt = {"s8": torch.int8, "f16": torch.float16, "s32": torch.int32}[out]
     c = torch.zeros((M, N), dtype=tdt, device="cuda")
@@ -47,7 +51,7 @@ def test_int8_routes_under_graph_replay(M, K, N, out):
     ws = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
 
     def fn(s):
-        na.gemm_i8(a, w, c, trans_b=True, out_kind=kind, s_a=0.02, s_b=sb, s_out=0.05,
+        na.gemm_i8(a, w, c, trans_b=trans_b, out_kind=kind, s_a=0.02, s_b=sb, s_out=0.05,
                    act=na.ACT_RELU if out != "s32" else na.ACT_NONE, workspace=ws, stream=s.cuda_stream)
     graph_replays_match(fn, c)
 
