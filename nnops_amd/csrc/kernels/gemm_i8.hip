@@ -872,9 +872,28 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     for (int t = 0; t < kt; ++t) {
         step(t);
     }
+    // The output pass's per-column scales, all 8 loads of a lane in flight
+    // together: loaded where they are used, each 4-column group's load was
+    // waited for on its own, 8 serial cache round trips per tile. (Loading
+    // them during the last stage would raise the loop's register peak past
+    // the 256 of two waves per SIMD.)
+    const EpiParams& ep = p.ep;
+    v4f sbp[FN][4];
+    if constexpr (MODE == RING_S8 || MODE == RING_FP) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                sbp[j][g] = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+                if (ep.s_b != nullptr && n < p.n) {
+                    sbp[j][g] = *reinterpret_cast<const v4f*>(ep.s_b + n);
+                }
+            }
+        }
+    }
     __syncthreads();   // every wave is done with the ring before it is reused for staging
 
-    const EpiParams& ep = p.ep;
     if constexpr (MODE == RING_S8) {
         // Requant in the transposed layout: per lane 4 consecutive columns of
         // one row per register group. Relu is folded into the clamp: with
@@ -899,11 +918,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
-                const int n = n0 + wn0 + nl;
-                v4f sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
-                if (ep.s_b != nullptr && n < p.n) {
-                    sb = *reinterpret_cast<const v4f*>(ep.s_b + n);
-                }
+                const v4f sb = sbp[j][g];
                 float req[4];
                 int32_t lo[4], hi[4];
 #pragma unroll
@@ -977,19 +992,14 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         auto col_fp = [&](int j, int g) {
             ColFp cp;
             cp.n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-            cp.sb = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+            cp.sb = sbp[j][g];
             cp.bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (cp.n < p.n) {
-                if (ep.s_b != nullptr) {
-                    cp.sb = *reinterpret_cast<const v4f*>(ep.s_b + cp.n);
-                }
-                if (ep.bias_fp != nullptr) {
-                    if (f16) {
-                        const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + cp.n;
-                        cp.bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
-                    } else {
-                        cp.bias = *reinterpret_cast<const v4f*>(static_cast<const float*>(ep.bias_fp) + cp.n);
-                    }
+            if (cp.n < p.n && ep.bias_fp != nullptr) {
+                if (f16) {
+                    const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + cp.n;
+                    cp.bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
+                } else {
+                    cp.bias = *reinterpret_cast<const v4f*>(static_cast<const float*>(ep.bias_fp) + cp.n);
                 }
             }
             return cp;
