@@ -116,17 +116,26 @@ class Timer:
         return out
 
     def per_launch(self, fn, steps):
-        """Mean duration of one call, from an event pair around each of K
-        back-to-back calls on the stream (the host stays ahead of a long
-        kernel, so each pair brackets its launch alone): the kernel's own
-        time, without the gaps between steps."""
+        """Mean duration of one call's (first) kernel: before each of K
+        back-to-back calls the library is armed (nnops_hip_time_next_launch)
+        to attach an event pair to that kernel's own dispatch packet, so each
+        pair brackets the kernel's execution alone -- the figure rocprofv3's
+        kernel trace reports -- without the dispatch gap that events recorded
+        on the stream around the call would add."""
         torch = self.torch
+        import nnops_amd as na
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         with torch.cuda.stream(self.stream):
-            for e0, e1 in ev:
+            for e0, e1 in ev:      # torch creates an event's HIP handle at its first record
                 e0.record(self.stream)
-                fn()
                 e1.record(self.stream)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            for e0, e1 in ev:
+                rc = na.lib().nnops_hip_time_next_launch(C.c_void_p(e0.cuda_event), C.c_void_p(e1.cuda_event))
+                assert rc == 0, rc
+                fn()
+        na.lib().nnops_hip_time_next_launch(None, None)
         torch.cuda.synchronize()
         return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
 

@@ -357,6 +357,17 @@ int nnops_hip_dequantize_linear(const NnopsQdqArgs* args, void* stream);
 /* Library version and build target, for the caller's diagnostics. */
 const char* nnops_hip_build_info(void);
 
+/* Kernel timing for benchmarks (no counterpart in nnops; for callers that
+ * measure the library, such as bench.py). Arms the calling thread's next
+ * kernel launch by this library: that one launch carries `start` and `stop`
+ * (hipEvent_t, created with timing enabled) on its own dispatch packet, so
+ * hipEventElapsedTime(start, stop) is the kernel's execution alone, without
+ * the dispatch gap an event pair recorded around the call would include.
+ * One-shot: the next launch disarms it. A call that launches several kernels
+ * times its first. Returns NNOPS_OK; NNOPS_INVALID_ARGUMENT if exactly one of
+ * the two events is null; (null, null) disarms. */
+int nnops_hip_time_next_launch(void* start_event, void* stop_event);
+
 
 #ifdef __cplusplus
 }

@@ -137,6 +137,7 @@ SIGNATURES = {
     "nnops_hip_fp_output_pass": (C.c_int, [C.POINTER(FpOutArgs), C.c_void_p]),
     "nnops_hip_gemm_q4_1_fused": (C.c_int, [C.POINTER(GemmQ41Args), C.POINTER(FpOutArgs), C.c_void_p]),
     "nnops_hip_build_info": (C.c_char_p, []),
+    "nnops_hip_time_next_launch": (C.c_int, [C.c_void_p, C.c_void_p]),
     "nnops_hip_prepack_i8_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
     "nnops_hip_prepack_q4_1_bytes": (C.c_size_t, [C.c_int64, C.c_int64]),
     "nnops_hip_prepack_q4_1": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p,

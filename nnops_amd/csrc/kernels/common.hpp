@@ -5,6 +5,7 @@
 // bit-identical to nnops' scalar requant.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -33,6 +34,33 @@ __device__ __forceinline__ void wait_vmcnt()
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
+
+// The calling thread's armed kernel-timing events (nnops_hip_time_next_launch):
+// the next launch through NNOPS_LAUNCH carries them on its dispatch packet
+// (hipExtLaunchKernelGGL) and disarms them.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+inline LaunchTiming& launch_timing()
+{
+    static thread_local LaunchTiming t;
+    return t;
+}
+
+template <typename F, typename... Args>
+inline void nnops_launch(F kernel, const dim3& grid, const dim3& block, uint32_t shmem, hipStream_t stream,
+                         Args... args)
+{
+    LaunchTiming& t = launch_timing();
+    if (t.start != nullptr) {
+        const LaunchTiming armed = t;
+        t = LaunchTiming{};
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, armed.start, armed.stop, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+    }
+}
+#define NNOPS_LAUNCH(kernel, ...) ::nnops_amd::nnops_launch(kernel, __VA_ARGS__)
 
 // Launch epochs for the split-completion flags of the one-launch split
 // kernels: unique in the process and never 0. Consecutive counter values are

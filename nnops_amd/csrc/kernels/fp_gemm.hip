@@ -510,17 +510,17 @@ void launch_gemv(const FpKern& k, bool tb, bool vec, hipStream_t s)
     if (tb) {
         const dim3 grid((unsigned)((k.n + 15) / 16));      // 4 waves of 4 rows of B
         if (vec) {
-            hipLaunchKernelGGL((gemv_fp_nk<AF16, MT, true>), grid, dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_fp_nk<AF16, MT, true>), grid, dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemv_fp_nk<AF16, MT, false>), grid, dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_fp_nk<AF16, MT, false>), grid, dim3(256), 0, s, k);
         }
     } else {
         const int e = AF16 ? 8 : 4;
         const dim3 grid((unsigned)((k.n + 64 * e - 1) / (64 * e)), (unsigned)k.splits);
         if (vec) {
-            hipLaunchKernelGGL((gemv_fp_kn<AF16, MT, true>), grid, dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_fp_kn<AF16, MT, true>), grid, dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemv_fp_kn<AF16, MT, false>), grid, dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_fp_kn<AF16, MT, false>), grid, dim3(256), 0, s, k);
         }
     }
 }
@@ -616,7 +616,7 @@ extern "C" int nnops_hip_gemm_fp(const NnopsGemmFpArgs* g, void* workspace, size
     if (g->k == 0) {
         // an empty sum: C = 0
         k.splits = 0;
-        hipLaunchKernelGGL(fp_split_sum, dim3((unsigned)((g->m * g->n + 255) / 256)), dim3(256), 0, s, k);
+        NNOPS_LAUNCH(fp_split_sum, dim3((unsigned)((g->m * g->n + 255) / 256)), dim3(256), 0, s, k);
         return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
     }
     if (use_gemv_fp(*g)) {
@@ -642,7 +642,7 @@ extern "C" int nnops_hip_gemm_fp(const NnopsGemmFpArgs* g, void* workspace, size
                 launch_gemv_rows<false>(kk, tb, vec, s);
             }
             if (kk.splits > 1) {
-                hipLaunchKernelGGL(fp_split_sum, dim3((unsigned)(((int64_t)kk.m * kk.n + 255) / 256)), dim3(256), 0,
+                NNOPS_LAUNCH(fp_split_sum, dim3((unsigned)(((int64_t)kk.m * kk.n + 255) / 256)), dim3(256), 0,
                                    s, kk);
             }
         }
@@ -657,14 +657,14 @@ extern "C" int nnops_hip_gemm_fp(const NnopsGemmFpArgs* g, void* workspace, size
     }
     if (f16) {
         if (g->trans_b) {
-            hipLaunchKernelGGL((gemm_fp_tile<true, true>), dim3((unsigned)tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemm_fp_tile<true, true>), dim3((unsigned)tiles), dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_fp_tile<true, false>), dim3((unsigned)tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemm_fp_tile<true, false>), dim3((unsigned)tiles), dim3(256), 0, s, k);
         }
     } else if (g->trans_b) {
-        hipLaunchKernelGGL((gemm_fp_tile<false, true>), dim3((unsigned)tiles), dim3(256), 0, s, k);
+        NNOPS_LAUNCH((gemm_fp_tile<false, true>), dim3((unsigned)tiles), dim3(256), 0, s, k);
     } else {
-        hipLaunchKernelGGL((gemm_fp_tile<false, false>), dim3((unsigned)tiles), dim3(256), 0, s, k);
+        NNOPS_LAUNCH((gemm_fp_tile<false, false>), dim3((unsigned)tiles), dim3(256), 0, s, k);
     }
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }

@@ -128,7 +128,7 @@ extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
     if (cblocks * a->rows > INT32_MAX) {
         return NNOPS_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(fp_out_pass, dim3((unsigned)(cblocks * a->rows)), dim3(256), 0,
+    NNOPS_LAUNCH(fp_out_pass, dim3((unsigned)(cblocks * a->rows)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), p, (int)cblocks);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }

@@ -1994,13 +1994,13 @@ void launch_gemm_epi(const GemmI8Kern& k, int epi, hipStream_t s)
     const int tiles = ((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN);
     const dim3 grid(tiles), block(WM * WN * 64);
     if (k.a_xor != 0u) {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, true, EPI_GENERIC>), grid, block, 0, s, k);
+        NNOPS_LAUNCH((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, true, EPI_GENERIC>), grid, block, 0, s, k);
     } else if (epi == EPI_S8) {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S8>), grid, block, 0, s, k);
+        NNOPS_LAUNCH((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S8>), grid, block, 0, s, k);
     } else if (epi == EPI_S32) {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S32>), grid, block, 0, s, k);
+        NNOPS_LAUNCH((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_S32>), grid, block, 0, s, k);
     } else {
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_GENERIC>), grid, block, 0, s, k);
+        NNOPS_LAUNCH((gemm_i8_mfma<BM, BN, WM, WN, WPE, FULLK, ALIGNED, false, EPI_GENERIC>), grid, block, 0, s, k);
     }
 }
 
@@ -2024,24 +2024,24 @@ void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool fli
     if constexpr (F16) {
         (void)flip;
         if (mode == RING_FP) {
-            hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false, true>), dim3(blocks), block, 0,
+            NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false, true>), dim3(blocks), block, 0,
                                s, k, sk);
         } else {
-            hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false, true>), dim3(blocks), block,
+            NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false, true>), dim3(blocks), block,
                                0, s, k, sk);
         }
         return;
     }
     if (flip) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
+        NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, true>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S8) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
+        NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S8, false>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_S32) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
+        NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S32, false>), dim3(blocks), block, 0, s, k, sk);
     } else if (mode == RING_FP) {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false>), dim3(blocks), block, 0, s, k, sk);
+        NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false>), dim3(blocks), block, 0, s, k, sk);
     } else {
-        hipLaunchKernelGGL((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
+        NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false>), dim3(blocks), block, 0, s, k, sk);
     }
 }
 
@@ -2071,17 +2071,17 @@ void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, i
     if (cpl == 16) {
         if constexpr (MT <= 2) {
             if (w == 16) {
-                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 16>), grid, dim3(1024), 0, s, k, sk, ks);
+                NNOPS_LAUNCH((gemv_i8_kn<MT, 16, 16>), grid, dim3(1024), 0, s, k, sk, ks);
             } else if (w == 8) {
-                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 8>), grid, dim3(512), 0, s, k, sk, ks);
+                NNOPS_LAUNCH((gemv_i8_kn<MT, 16, 8>), grid, dim3(512), 0, s, k, sk, ks);
             } else {
-                hipLaunchKernelGGL((gemv_i8_kn<MT, 16, 4>), grid, dim3(256), 0, s, k, sk, ks);
+                NNOPS_LAUNCH((gemv_i8_kn<MT, 16, 4>), grid, dim3(256), 0, s, k, sk, ks);
             }
         }
     } else if (w == 4) {
-        hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
+        NNOPS_LAUNCH((gemv_i8_kn<MT, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
     } else {
-        hipLaunchKernelGGL((gemv_i8_kn<MT, 4, 8>), grid, dim3(512), 0, s, k, sk, ks);
+        NNOPS_LAUNCH((gemv_i8_kn<MT, 4, 8>), grid, dim3(512), 0, s, k, sk, ks);
     }
 }
 
@@ -2089,9 +2089,9 @@ void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
 {
     const int64_t groups = (int64_t)k.m * (k.n / 4);
     if (sk.splits > 8) {
-        hipLaunchKernelGGL(gemm_i8_reduce<4>, dim3((unsigned)((groups * 4 + 255) / 256)), dim3(256), 0, s, k, sk);
+        NNOPS_LAUNCH(gemm_i8_reduce<4>, dim3((unsigned)((groups * 4 + 255) / 256)), dim3(256), 0, s, k, sk);
     } else {
-        hipLaunchKernelGGL(gemm_i8_reduce<1>, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
+        NNOPS_LAUNCH(gemm_i8_reduce<1>, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
     }
 }
 
@@ -2157,7 +2157,7 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
     }
     if (r.mode == RING_PART) {
         if constexpr (F16) {
-            hipLaunchKernelGGL(ring_f16_reduce, dim3((unsigned)(((int64_t)k.m * k.n + 255) / 256)), dim3(256), 0, s,
+            NNOPS_LAUNCH(ring_f16_reduce, dim3((unsigned)(((int64_t)k.m * k.n + 255) / 256)), dim3(256), 0, s,
                                k, sk);
         } else {
             launch_reduce(k, sk, s);
@@ -2222,13 +2222,13 @@ extern "C" int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64
     int32_t* sums = reinterpret_cast<int32_t*>(static_cast<char*>(out) + align_up((size_t)n * (size_t)kp));
     if (trans_b) {
         const int64_t threads = n * (kp / 16);
-        hipLaunchKernelGGL(pad_rows_i8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, b, ldb, (int)n,
+        NNOPS_LAUNCH(pad_rows_i8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, b, ldb, (int)n,
                            (int)k, rows, kp);
     } else {
         dim3 grid((unsigned)((n + 63) / 64), (unsigned)((kp + 63) / 64));
-        hipLaunchKernelGGL(transpose_i8, grid, dim3(256), 0, s, b, ldb, (int)k, (int)n, rows, kp, (int)kp);
+        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, b, ldb, (int)k, (int)n, rows, kp, (int)kp);
     }
-    hipLaunchKernelGGL(rowsum_i8, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rows, kp, (int)n, (int)k, 0,
+    NNOPS_LAUNCH(rowsum_i8, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rows, kp, (int)n, (int)k, 0,
                        sums);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
@@ -2297,7 +2297,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     if (g->trans_a) {
         int8_t* at = reinterpret_cast<int8_t*>(ws + w.a_t);
         dim3 grid((unsigned)((g->m + 63) / 64), (unsigned)((w.kp + 63) / 64));
-        hipLaunchKernelGGL(transpose_i8, grid, dim3(256), 0, s, static_cast<const int8_t*>(g->a), g->lda,
+        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, static_cast<const int8_t*>(g->a), g->lda,
                            (int)g->k, (int)g->m, at, (int64_t)w.kp, (int)w.kp);
         k.a = at;
         k.lda = w.kp;
@@ -2311,7 +2311,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     } else if (!g->trans_b) {
         int8_t* bt = reinterpret_cast<int8_t*>(ws + w.b_t);
         dim3 grid((unsigned)((g->n + 63) / 64), (unsigned)((w.kp + 63) / 64));
-        hipLaunchKernelGGL(transpose_i8, grid, dim3(256), 0, s, g->b, g->ldb, (int)g->k, (int)g->n, bt,
+        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, g->b, g->ldb, (int)g->k, (int)g->n, bt,
                            (int64_t)w.kp, (int)w.kp);
         k.b = bt;
         k.ldb = w.kp;
@@ -2353,13 +2353,13 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         e.r_b = g->b_col_sums;
     } else if (need_rb) {
         int32_t* rb = reinterpret_cast<int32_t*>(ws + w.r_b);
-        hipLaunchKernelGGL(rowsum_i8, dim3((unsigned)((g->n + 3) / 4)), dim3(256), 0, s, k.b, k.ldb,
+        NNOPS_LAUNCH(rowsum_i8, dim3((unsigned)((g->n + 3) / 4)), dim3(256), 0, s, k.b, k.ldb,
                            (int)g->n, (int)g->k, 0, rb);
         e.r_b = rb;
     }
     if (need_ra) {
         int32_t* ra = reinterpret_cast<int32_t*>(ws + w.r_a);
-        hipLaunchKernelGGL(rowsum_i8, dim3((unsigned)((g->m + 3) / 4)), dim3(256), 0, s, k.a, k.lda,
+        NNOPS_LAUNCH(rowsum_i8, dim3((unsigned)((g->m + 3) / 4)), dim3(256), 0, s, k.a, k.lda,
                            (int)g->m, (int)g->k, (int)g->a_u8, ra);
         e.r_a = ra;
     }
@@ -2370,7 +2370,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     if (w.kn.cpl != 0) {
         launch_kn(k, w.kn, reinterpret_cast<int32_t*>(ws + w.part), s);
     } else if (g->m <= 16 && aligned && g->k % 64 == 0 && gemv_lds_ok(*g)) {
-        hipLaunchKernelGGL((gemv_i8_lds<4>), dim3((unsigned)((g->n + 15) / 16)), dim3(256), 0, s, k);
+        NNOPS_LAUNCH((gemv_i8_lds<4>), dim3((unsigned)((g->n + 15) / 16)), dim3(256), 0, s, k);
     } else if (g->m <= 4 && aligned) {
         const bool flip = k.a_xor != 0u;
         // two rows per wave from M = 3: halves the A re-reads per weight byte
@@ -2379,9 +2379,9 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         {                                                                                           \
             const unsigned blocks = (unsigned)((g->n + 4 * R - 1) / (4 * R));                      \
             if (flip) {                                                                             \
-                hipLaunchKernelGGL((gemv_i8_rows<MT, R, true>), dim3(blocks), dim3(256), 0, s, k);  \
+                NNOPS_LAUNCH((gemv_i8_rows<MT, R, true>), dim3(blocks), dim3(256), 0, s, k);  \
             } else {                                                                                \
-                hipLaunchKernelGGL((gemv_i8_rows<MT, R, false>), dim3(blocks), dim3(256), 0, s, k); \
+                NNOPS_LAUNCH((gemv_i8_rows<MT, R, false>), dim3(blocks), dim3(256), 0, s, k); \
             }                                                                                       \
         }
 #define NNOPS_ROWS(MT)                                                                              \
@@ -2398,9 +2398,9 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     } else if (g->m <= 16) {
         const unsigned blocks = (unsigned)((g->n + 15) / 16);
         if (aligned) {
-            hipLaunchKernelGGL((gemv_i8_mfma<4, true>), dim3(blocks), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_i8_mfma<4, true>), dim3(blocks), dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemv_i8_mfma<4, false>), dim3(blocks), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemv_i8_mfma<4, false>), dim3(blocks), dim3(256), 0, s, k);
         }
     } else if (w.ring.mode >= 0) {
         launch_ring(k, w.ring, reinterpret_cast<int32_t*>(ws + w.part), s);
@@ -2524,7 +2524,7 @@ int ring_gemm_f16(const NnopsGemmFpArgs& g, void* workspace, size_t ws_bytes, hi
     if (f.stage_b) {
         uint16_t* bt = reinterpret_cast<uint16_t*>(ws);
         const dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((f.kp / 2 + 63) / 64));
-        hipLaunchKernelGGL(transpose_b16, grid, dim3(256), 0, s, static_cast<const uint16_t*>(g.b), g.ldb,
+        NNOPS_LAUNCH(transpose_b16, grid, dim3(256), 0, s, static_cast<const uint16_t*>(g.b), g.ldb,
                            (int)g.k, (int)g.n, bt, f.kp / 2, (int)(f.kp / 2));
         k.b = reinterpret_cast<const int8_t*>(bt);
         k.ldb = f.kp;

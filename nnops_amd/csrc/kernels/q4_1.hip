@@ -2835,12 +2835,12 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
             const dim3 grid((unsigned)((g->n + kSkRows - 1) / kSkRows));
             if (!g->a_f16) {
-                hipLaunchKernelGGL(gemv_q4_1_skinny_f32<3>, grid, dim3(128), 0, s, kk);
+                NNOPS_LAUNCH(gemv_q4_1_skinny_f32<3>, grid, dim3(128), 0, s, kk);
             } else if (g->k % 512 == 0) {
                 // two K halves per workgroup: four waves, two stages in flight
-                hipLaunchKernelGGL((gemv_q4_1_skinny<2, 2>), grid, dim3(256), 0, s, kk);
+                NNOPS_LAUNCH((gemv_q4_1_skinny<2, 2>), grid, dim3(256), 0, s, kk);
             } else {
-                hipLaunchKernelGGL((gemv_q4_1_skinny<4, 1>), grid, dim3(128), 0, s, kk);
+                NNOPS_LAUNCH((gemv_q4_1_skinny<4, 1>), grid, dim3(128), 0, s, kk);
             }
         }
     } else if (use_gemv(*g)) {
@@ -2867,32 +2867,32 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                         // 4 rows per wave: 10 KiB per wave in flight, one launch-wide wave of blocks
                         const unsigned rb4 = (unsigned)((g->n + 15) / 16);
                         if (kk.m == 1) {
-                            hipLaunchKernelGGL((gemv_q4_1_pipe<1, 4>), dim3(rb4), dim3(256), 0, s, kk);
+                            NNOPS_LAUNCH((gemv_q4_1_pipe<1, 4>), dim3(rb4), dim3(256), 0, s, kk);
                         } else {
-                            hipLaunchKernelGGL((gemv_q4_1_pipe<2, 4>), dim3(rb4), dim3(256), 0, s, kk);
+                            NNOPS_LAUNCH((gemv_q4_1_pipe<2, 4>), dim3(rb4), dim3(256), 0, s, kk);
                         }
                     } else if (staged) {
                         if (kk.m == 1) {
-                            hipLaunchKernelGGL((gemv_q4_1_lds<1, R>), dim3(rb), dim3(256), 0, s, kk);
+                            NNOPS_LAUNCH((gemv_q4_1_lds<1, R>), dim3(rb), dim3(256), 0, s, kk);
                         } else {
-                            hipLaunchKernelGGL((gemv_q4_1_lds<2, R>), dim3(rb), dim3(256), 0, s, kk);
+                            NNOPS_LAUNCH((gemv_q4_1_lds<2, R>), dim3(rb), dim3(256), 0, s, kk);
                         }
                     } else if (kk.m == 1) {
-                        hipLaunchKernelGGL((gemv_q4_1_rows<1, R>), dim3(rb), dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_rows<1, R>), dim3(rb), dim3(256), 0, s, kk);
                     } else {
-                        hipLaunchKernelGGL((gemv_q4_1_rows<2, R>), dim3(rb), dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_rows<2, R>), dim3(rb), dim3(256), 0, s, kk);
                     }
                 } else {
-                    hipLaunchKernelGGL((gemv_q4_1_nk<1, false>), dim3(blocks), dim3(256), 0, s, kk);
+                    NNOPS_LAUNCH((gemv_q4_1_nk<1, false>), dim3(blocks), dim3(256), 0, s, kk);
                 }
             } else if (bcm_ok(*g)) {
                 // the prepacked planes: one workgroup per block column, whole K
                 // 8 waves, 4 chunks in flight per lane: 10.6 us at config 4
                 // (4 waves x 2 chunks 12.0, 8 x 2 11.2, 4 x 8 10.8)
                 if (kk.m == 1) {
-                    hipLaunchKernelGGL((gemv_q4_1_bcm<1, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                    NNOPS_LAUNCH((gemv_q4_1_bcm<1, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
                 } else {
-                    hipLaunchKernelGGL((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                    NNOPS_LAUNCH((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
                 }
             } else if (const KnDmaPlan pl = plan_kn_dma(*g); pl.groups > 0) {
                 KnDma kd;
@@ -2905,9 +2905,9 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 // 8 waves: four row-pair classes per stage hide the LDS and
                 // dot latencies better than 4 (18.0 -> 17.0 us at config 4)
                 if (kk.m == 1) {
-                    hipLaunchKernelGGL((gemv_q4_1_kn_dma<1, 8>), grid, dim3(512), 0, s, kk, kd);
+                    NNOPS_LAUNCH((gemv_q4_1_kn_dma<1, 8>), grid, dim3(512), 0, s, kk, kd);
                 } else {
-                    hipLaunchKernelGGL((gemv_q4_1_kn_dma<2, 8>), grid, dim3(512), 0, s, kk, kd);
+                    NNOPS_LAUNCH((gemv_q4_1_kn_dma<2, 8>), grid, dim3(512), 0, s, kk, kd);
                 }
             } else {
                 kk.splits = kn_splits(*g);
@@ -2916,26 +2916,26 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 const dim3 grid(bx, kk.splits);
                 if (g->a_f16 && kk.m == 1) {
                     if (soa) {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true, true>), grid, dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_kn<1, true, true>), grid, dim3(256), 0, s, kk);
                     } else {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<1, true, false>), grid, dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_kn<1, true, false>), grid, dim3(256), 0, s, kk);
                     }
                 } else if (g->a_f16) {
                     if (soa) {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true, true>), grid, dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_kn<2, true, true>), grid, dim3(256), 0, s, kk);
                     } else {
-                        hipLaunchKernelGGL((gemv_q4_1_kn<2, true, false>), grid, dim3(256), 0, s, kk);
+                        NNOPS_LAUNCH((gemv_q4_1_kn<2, true, false>), grid, dim3(256), 0, s, kk);
                     }
                 } else if (soa) {
-                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false, true>), grid, dim3(256), 0, s, kk);
+                    NNOPS_LAUNCH((gemv_q4_1_kn<1, false, true>), grid, dim3(256), 0, s, kk);
                 } else {
-                    hipLaunchKernelGGL((gemv_q4_1_kn<1, false, false>), grid, dim3(256), 0, s, kk);
+                    NNOPS_LAUNCH((gemv_q4_1_kn<1, false, false>), grid, dim3(256), 0, s, kk);
                 }
                 const int64_t total = (int64_t)kk.m * kk.n;
                 if (kk.splits >= 32) {
-                    hipLaunchKernelGGL(reduce_q4_1<16>, dim3((unsigned)((total * 16 + 255) / 256)), dim3(256), 0, s, kk);
+                    NNOPS_LAUNCH(reduce_q4_1<16>, dim3((unsigned)((total * 16 + 255) / 256)), dim3(256), 0, s, kk);
                 } else {
-                    hipLaunchKernelGGL(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
+                    NNOPS_LAUNCH(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
                 }
             }
         }
@@ -2952,22 +2952,22 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
             kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
             if (mt == 2) {
-                hipLaunchKernelGGL((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                NNOPS_LAUNCH((gemv_q4_1_bcm<2, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
             } else if (mt == 4) {
-                hipLaunchKernelGGL((gemv_q4_1_bcm<4, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                NNOPS_LAUNCH((gemv_q4_1_bcm<4, 8, 4>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
             } else {
-                hipLaunchKernelGGL((gemv_q4_1_bcm<8, 8, 2>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
+                NNOPS_LAUNCH((gemv_q4_1_bcm<8, 8, 2>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
             }
             m0 += mt;
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
         if (g->trans_b) {
-            hipLaunchKernelGGL(gemm_q4_1_f32<0>, dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH(gemm_q4_1_f32<0>, dim3(tiles), dim3(256), 0, s, k);
         } else if (soa) {
-            hipLaunchKernelGGL(gemm_q4_1_f32<2>, dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH(gemm_q4_1_f32<2>, dim3(tiles), dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL(gemm_q4_1_f32<1>, dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH(gemm_q4_1_f32<1>, dim3(tiles), dim3(256), 0, s, k);
         }
     } else if (g->trans_b && g->k % 64 == 0 && (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0) {
         // blocks along K: the ring kernel (A by DMA, B decoded in registers)
@@ -2975,32 +2975,32 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         // 8 waves (2 per SIMD), each 128 x 32: one wave's decode and stalls
         // overlap the other's matrix-core work, and no B row is decoded twice
         if (k.out_f16) {
-            hipLaunchKernelGGL((gemm_q4_1_ring<true, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_ring<true, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_ring<false, 4, 1, 8>), dim3(tiles), dim3(512), 0, s, k);
         }
     } else if (kn_ring_ok(*g)) {
         // blocks along N: the same ring, B rows staged raw and decoded per lane
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
         if (k.out_f16) {
             if (soa) {
-                hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4, true>), dim3(tiles), dim3(512), 0, s, k);
+                NNOPS_LAUNCH((gemm_q4_1_kn_ring<true, 4, true>), dim3(tiles), dim3(512), 0, s, k);
             } else {
-                hipLaunchKernelGGL((gemm_q4_1_kn_ring<true, 4, false>), dim3(tiles), dim3(512), 0, s, k);
+                NNOPS_LAUNCH((gemm_q4_1_kn_ring<true, 4, false>), dim3(tiles), dim3(512), 0, s, k);
             }
         } else if (soa) {
-            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4, true>), dim3(tiles), dim3(512), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<false, 4, true>), dim3(tiles), dim3(512), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_kn_ring<false, 4, false>), dim3(tiles), dim3(512), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<false, 4, false>), dim3(tiles), dim3(512), 0, s, k);
         }
     } else {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));
         if (g->trans_b) {
-            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, true>), dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_mfma<128, 128, 2, 2, true>), dim3(tiles), dim3(256), 0, s, k);
         } else if (soa) {
-            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false, true>), dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_mfma<128, 128, 2, 2, false, true>), dim3(tiles), dim3(256), 0, s, k);
         } else {
-            hipLaunchKernelGGL((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
+            NNOPS_LAUNCH((gemm_q4_1_mfma<128, 128, 2, 2, false>), dim3(tiles), dim3(256), 0, s, k);
         }
     }
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
@@ -3047,7 +3047,7 @@ extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsF
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t tiles_m = (g->m + 127) / 128;
     const unsigned tiles = (unsigned)(tiles_m * ((pass->n + 127) / 128));
-    hipLaunchKernelGGL((gemm_q4_1_ring<false, 4, 1, 8, true>), dim3(tiles), dim3(512), 0, s, k);
+    NNOPS_LAUNCH((gemm_q4_1_ring<false, 4, 1, 8, true>), dim3(tiles), dim3(512), 0, s, k);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
 
@@ -3076,7 +3076,7 @@ extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, in
     uint8_t* nib = static_cast<uint8_t*>(out);
     uint32_t* dm = reinterpret_cast<uint32_t*>(nib + align_up((size_t)nbn * (size_t)prepack_q41_nib_pitch(k)));
     const int64_t blocks = k * nbn;
-    hipLaunchKernelGGL(prepack_q4_1_kn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+    NNOPS_LAUNCH(prepack_q4_1_kn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), b, ldb_bytes, (int)k, (int)nbn, nib, dm,
                        prepack_q41_dm_pitch(k));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
@@ -3085,4 +3085,14 @@ extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, in
 extern "C" const char* nnops_hip_build_info(void)
 {
     return "nnops_amd gfx950 (hand-written HIP: int8 MFMA GEMM/GEMV, Q4_1 GEMV/MFMA GEMM)";
+}
+
+extern "C" int nnops_hip_time_next_launch(void* start_event, void* stop_event)
+{
+    if ((start_event == nullptr) != (stop_event == nullptr)) {
+        return NNOPS_INVALID_ARGUMENT;
+    }
+    nnops_amd::launch_timing() = nnops_amd::LaunchTiming{static_cast<hipEvent_t>(start_event),
+                                                         static_cast<hipEvent_t>(stop_event)};
+    return NNOPS_OK;
 }

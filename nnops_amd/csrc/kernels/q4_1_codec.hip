@@ -181,7 +181,7 @@ extern "C" int nnops_hip_q4_1_quantize(const void* src, int32_t src_f16, int64_t
         return NNOPS_INVALID_ARGUMENT;
     }
     CodecArgs a{src, dst, rows, cols, ld_src, ld_dst_bytes, src_f16 ? 1 : 0, nb};
-    hipLaunchKernelGGL(q4_1_quantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,
+    NNOPS_LAUNCH(q4_1_quantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), a);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
@@ -202,7 +202,7 @@ extern "C" int nnops_hip_q4_1_dequantize(const void* src, int64_t ld_src_bytes, 
         return NNOPS_INVALID_ARGUMENT;
     }
     CodecArgs a{src, dst, rows, cols, ld_src_bytes, ld_dst, dst_f16 ? 1 : 0, nb};
-    hipLaunchKernelGGL(q4_1_dequantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,
+    NNOPS_LAUNCH(q4_1_dequantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), a);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }

@@ -324,7 +324,7 @@ extern "C" int nnops_hip_quantize_linear(const NnopsQdqArgs* g, void* stream)
         return rc;
     }
     const int64_t threads = g->rows * ((g->cols + 15) / 16);
-    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+    NNOPS_LAUNCH(quantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), qdq_kern(g));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
@@ -336,7 +336,7 @@ extern "C" int nnops_hip_dequantize_linear(const NnopsQdqArgs* g, void* stream)
         return rc;
     }
     const int64_t threads = g->rows * ((g->cols + 15) / 16);
-    hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+    NNOPS_LAUNCH(dequantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), qdq_kern(g));
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }

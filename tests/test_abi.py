@@ -52,6 +52,14 @@ def test_build_info():
     assert b"gfx950" in na.lib().nnops_hip_build_info()
 
 
+def test_time_next_launch_arguments():
+    """The timing hook takes both events or neither; it launches nothing."""
+    lib = na.lib()
+    assert lib.nnops_hip_time_next_launch(C.c_void_p(16), None) == na.INVALID_ARGUMENT
+    assert lib.nnops_hip_time_next_launch(None, C.c_void_p(16)) == na.INVALID_ARGUMENT
+    assert lib.nnops_hip_time_next_launch(None, None) == na.OK
+
+
 def test_gemm_i8_rejects_before_any_launch():
     lib = na.lib()
     g = na.GemmI8Args()

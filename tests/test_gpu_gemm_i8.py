@@ -170,6 +170,29 @@ def test_determinism_repeated_runs():
     np.testing.assert_array_equal(r1, r2)
 
 
+def test_timed_launch_same_result_and_positive_time():
+    """A launch armed with nnops_hip_time_next_launch (events on its dispatch
+    packet) computes the same bits as an unarmed one, and its events measure
+    a positive kernel time."""
+    import ctypes as C
+    import torch
+    announce("timed launch")
+    M, K, N = 256, 1024, 512
+    a = dg.act_s8(61, (M, K))
+    b = dg.ints(62, (N, K), -127, 127)
+    want = oracle.gemm_i8(a, b, trans_b=True, out_kind=oracle.OUT_S32)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    torch.cuda.synchronize()
+    assert na.lib().nnops_hip_time_next_launch(C.c_void_p(e0.cuda_event), C.c_void_p(e1.cuda_event)) == na.OK
+    got = run_gpu(a, b, na.OUT_S32, trans_b=True)
+    assert e0.elapsed_time(e1) > 0.0
+    np.testing.assert_array_equal(got, want)
+    # one-shot: the next call runs unarmed and still matches
+    np.testing.assert_array_equal(run_gpu(a, b, na.OUT_S32, trans_b=True), want)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_config3_full_gemv(M):
     """BASELINE config 3 at full size (K=4096, N=11008), s32 and s8."""
