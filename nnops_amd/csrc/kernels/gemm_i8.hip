@@ -1736,6 +1736,75 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk,
 // Prepasses
 // ---------------------------------------------------------------------------
 // dst[c][r] = src[r][c] for r < R, c < C; dst columns r in [R, Rp) are zeroed.
+// The same transpose in 256-row x 64-column tiles with 16-byte accesses on
+// both sides (source rows, pitch, destination and its pitch 16-byte aligned,
+// Rp % 16 == 0): each thread loads four 16-byte row pieces into LDS (row
+// pitch 17 dwords), then reads a 16-row x 4-column block as 16 dwords,
+// transposes it in registers (v_perm, 4 x 4 bytes at a time) and stores four
+// 16-byte destination pieces (the byte-wise kernel below, kept for unaligned
+// operands, moves one byte per load and store).
+__global__ __launch_bounds__(256) void transpose_i8_v(const int8_t* src, int64_t lds_, int R, int C,
+                                                      int8_t* dst, int64_t ldd, int Rp)
+{
+    constexpr int TR = 256, TC = 64, P = TC / 4 + 1;   // rows, columns, LDS pitch in dwords
+    __shared__ uint32_t tile[TR * P];
+    const int r0 = blockIdx.y * TR;
+    const int c0 = blockIdx.x * TC;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int idx = q * 256 + t;
+        const int row = idx >> 2, seg = idx & 3;
+        const int r = r0 + row, c = c0 + 16 * seg;
+        v4i v = v4i{0, 0, 0, 0};
+        if (r < R && c < C) {
+            const int8_t* sp = src + (int64_t)r * lds_ + c;
+            if (c + 16 <= C) {
+                v = *reinterpret_cast<const v4i*>(sp);
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int b = 0; b < C - c; ++b) {
+                    w[b >> 2] |= (uint32_t)(uint8_t)sp[b] << (8 * (b & 3));
+                }
+                v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            tile[row * P + 4 * seg + d] = (uint32_t)v[d];
+        }
+    }
+    __syncthreads();
+    const int c4 = t & 15, r16 = t >> 4;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        w[i] = tile[(16 * r16 + i) * P + c4];
+    }
+    uint32_t col[4][4];   // [column j][row quad g]
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint32_t cq[4];
+        transpose4x4_bytes(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3], cq);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            col[j][g] = cq[j];
+        }
+    }
+    const int r = r0 + 16 * r16;
+    if (r >= Rp) {
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = c0 + 4 * c4 + j;
+        if (c < C) {
+            *reinterpret_cast<v4i*>(dst + (int64_t)c * ldd + r) =
+                v4i{(int)col[j][0], (int)col[j][1], (int)col[j][2], (int)col[j][3]};
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void transpose_i8(const int8_t* src, int64_t lds_, int R, int C,
                                                    int8_t* dst, int64_t ldd, int Rp)
 {
@@ -1754,6 +1823,21 @@ __global__ __launch_bounds__(256) void transpose_i8(const int8_t* src, int64_t l
         if (c < C && r < Rp) {
             dst[(int64_t)c * ldd + r] = tile[tx][i];
         }
+    }
+}
+
+// dst[c][r] = src[r][c] (r < R, c < C; columns r in [R, Rp) zeroed): the
+// 16-byte tiled kernel where its alignment holds, else the byte-wise one.
+void launch_transpose_i8(const int8_t* src, int64_t lds_, int R, int C, int8_t* dst, int64_t ldd, int Rp,
+                         hipStream_t s)
+{
+    if (((uintptr_t)src % 16) == 0 && lds_ % 16 == 0 && ((uintptr_t)dst % 16) == 0 && ldd % 16 == 0 &&
+        Rp % 16 == 0) {
+        const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((Rp + 255) / 256));
+        NNOPS_LAUNCH(transpose_i8_v, grid, dim3(256), 0, s, src, lds_, R, C, dst, ldd, Rp);
+    } else {
+        const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((Rp + 63) / 64));
+        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, src, lds_, R, C, dst, ldd, Rp);
     }
 }
 
@@ -1930,8 +2014,10 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     const int64_t tiles = ((g.m + r.bm - 1) / r.bm) * ((g.n + r.bn - 1) / r.bn);
     r.bk = (g.k % 128 == 0) ? 128 : 64;
     const int kt = (int)(g.k / r.bk);
-    // at least 512 k per split
-    r.splits = (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / (512 / r.bk)));
+    // at least 512 k per split, and no split below 16 k steps: a short ring
+    // gains less from splitting than the reduce launch costs (config 1,
+    // 128x1024x1024 s32: 10.5 + 3.9 us in two splits, 12.4 us unsplit)
+    r.splits = kt < 16 ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / (512 / r.bk)));
     const bool compensate = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0 || g.zp_b != nullptr ||
                             g.zp_b_scalar != 0;
     const bool tables16 = ((uintptr_t)g.bias % 16 == 0) && ((uintptr_t)g.s_b % 16 == 0);
@@ -2225,8 +2311,7 @@ extern "C" int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64
         NNOPS_LAUNCH(pad_rows_i8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, b, ldb, (int)n,
                            (int)k, rows, kp);
     } else {
-        dim3 grid((unsigned)((n + 63) / 64), (unsigned)((kp + 63) / 64));
-        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, b, ldb, (int)k, (int)n, rows, kp, (int)kp);
+        launch_transpose_i8(b, ldb, (int)k, (int)n, rows, kp, (int)kp, s);
     }
     NNOPS_LAUNCH(rowsum_i8, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rows, kp, (int)n, (int)k, 0,
                        sums);
@@ -2296,9 +2381,8 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     // k-contiguous operands (stage a transposed copy where needed)
     if (g->trans_a) {
         int8_t* at = reinterpret_cast<int8_t*>(ws + w.a_t);
-        dim3 grid((unsigned)((g->m + 63) / 64), (unsigned)((w.kp + 63) / 64));
-        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, static_cast<const int8_t*>(g->a), g->lda,
-                           (int)g->k, (int)g->m, at, (int64_t)w.kp, (int)w.kp);
+        launch_transpose_i8(static_cast<const int8_t*>(g->a), g->lda, (int)g->k, (int)g->m, at, (int64_t)w.kp,
+                            (int)w.kp, s);
         k.a = at;
         k.lda = w.kp;
     } else {
@@ -2310,9 +2394,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         k.ldb = g->ldb;
     } else if (!g->trans_b) {
         int8_t* bt = reinterpret_cast<int8_t*>(ws + w.b_t);
-        dim3 grid((unsigned)((g->n + 63) / 64), (unsigned)((w.kp + 63) / 64));
-        NNOPS_LAUNCH(transpose_i8, grid, dim3(256), 0, s, g->b, g->ldb, (int)g->k, (int)g->n, bt,
-                           (int64_t)w.kp, (int)w.kp);
+        launch_transpose_i8(g->b, g->ldb, (int)g->k, (int)g->n, bt, (int64_t)w.kp, (int)w.kp, s);
         k.b = bt;
         k.ldb = w.kp;
     } else {

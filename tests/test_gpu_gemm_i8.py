@@ -83,6 +83,9 @@ SHAPES = [
     # row GEMV with two rows per wave (M = 3..4), LDS-staged skinny GEMM
     # (4 < M <= 16) with a ragged last group of rows and a K tail past 4 KiB
     (3, 512, 130), (4, 4096, 1000), (8, 5120, 77), (16, 1088, 4099),
+    # [K,N] B staged by the 16-byte tiled transpose: partial 256-row and
+    # 64-column tiles
+    (64, 992, 1040), (130, 1040, 1008),
 ]
 
 
@@ -157,6 +160,18 @@ def test_float_epilogue_add_to_gelu_pitched(M, residual_pre):
                           zp_out=2, float_ep=True, act=oracle.ACT_GELU, add_to=True,
                           residual_pre=residual_pre, c=c0.copy())
     assert np.unique(want).size > 50  # not a saturated comparison
+    np.testing.assert_array_equal(got, want)
+
+
+def test_trans_a_pitched_partial_transpose_segments():
+    """A stored [K][M] with a 16-byte pitch wider than M: the tiled transpose
+    reads the rows' last, partial 16-byte pieces byte by byte."""
+    announce("trans_a pitched")
+    M, K, N = 40, 300, 64
+    at = dg.ints(71, (K, M), -127, 127)
+    b = dg.ints(72, (N, K), -127, 127)
+    got = run_gpu(at, b, na.OUT_S32, trans_b=True, trans_a=True, lda=48)
+    want = oracle.gemm_i8(at, b, trans_b=True, trans_a=True)
     np.testing.assert_array_equal(got, want)
 
 
