@@ -84,8 +84,8 @@ SHAPES = [
     # (4 < M <= 16) with a ragged last group of rows and a K tail past 4 KiB
     (3, 512, 130), (4, 4096, 1000), (8, 5120, 77), (16, 1088, 4099),
     # [K,N] B staged by the 16-byte tiled transpose: partial 256-row and
-    # 64-column tiles
-    (64, 992, 1040), (130, 1040, 1008),
+    # 64-column tiles, and K % 16 != 0 (the zero-filled rows K..Kp-1)
+    (64, 992, 1040), (130, 1040, 1008), (48, 1000, 1040),
 ]
 
 
