@@ -36,10 +36,11 @@ def graph_replays_match(fn, out, replays=3):
 @pytest.mark.parametrize("M,K,N,out,trans_b", [(4096, 1024, 1024, "s8", True), (333, 14336, 1024, "s8", True),
                                                (1024, 512, 1024, "f16", True), (16, 4096, 1024, "s32", True),
                                                (1, 4096, 2048, "s32", True), (1, 4096, 11008, "s8", False),
-                                               (2, 4096, 2048, "s32", False), (16, 4096, 2048, "s8", False)])
+                                               (2, 4096, 2048, "s32", False), (16, 4096, 2048, "s8", False),
+                                               (64, 1000, 1040, "s8", False)])
 def test_int8_routes_under_graph_replay(M, K, N, out, trans_b):
-    """[K,N] rows (trans_b False) take the one-launch column GEMV, whose split
-    flags are cleared by the summing workgroup: replays reuse its epoch."""
+    """[K,N] rows (trans_b False): the column GEMV and its split reduce for
+    M <= 16, the tiled transpose into the workspace and the GEMM beyond."""
     import torch
     announce(f"graph int8 {M}x{K}x{N} {out} trans_b={trans_b}")
     a = dev(dg.act_s8(M + K, (M, K)))
