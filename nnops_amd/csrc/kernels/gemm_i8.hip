@@ -872,11 +872,11 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     for (int t = 0; t < kt; ++t) {
         step(t);
     }
-    // The output pass's per-column scales, all 8 loads of a lane in flight
-    // together: loaded where they are used, each 4-column group's load was
-    // waited for on its own, 8 serial cache round trips per tile. (Loading
-    // them during the last stage would raise the loop's register peak past
-    // the 256 of two waves per SIMD.)
+    // The output pass's per-column scales: a lane's 8 loads issued together
+    // with one wait, rather than one load and wait per 4-column group (8
+    // serial cache round trips). They are not issued during the last stage:
+    // that would raise the loop's register peak past the 256 of two waves
+    // per SIMD.
     const EpiParams& ep = p.ep;
     v4f sbp[FN][4];
     if constexpr (MODE == RING_S8 || MODE == RING_FP) {
@@ -1196,12 +1196,6 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     }
 }
 
-// Sum of the K-split partial accumulators and the full output pass
-// (compensation, bias, Relu, requant or the float epilogue, add_to). TPG
-// threads share a group of 4 consecutive columns of a row (N % 4 == 0), each
-// summing every TPG-th split with its loads in flight together, then combine
-// with lane shuffles; the first of them runs the output pass. TPG = 4 suits
-// many splits of a small output, TPG = 1 a few splits of a large one.
 // The output pass of 4 consecutive columns nb..nb+3 of row m: its row and
 // column constants and the residual word, loaded before the raw sums arrive
 // (out4_prepare), then the pass itself (out4_store).
@@ -1270,6 +1264,12 @@ __device__ __forceinline__ void out4_store(const GemmI8Kern& p, const Out4& o, i
     }
 }
 
+// Sum of the K-split partial accumulators and the full output pass
+// (compensation, bias, Relu, requant or the float epilogue, add_to). TPG
+// threads share a group of 4 consecutive columns of a row (N % 4 == 0), each
+// summing every TPG-th split with its loads in flight together, then combine
+// with lane shuffles; the first of them runs the output pass. TPG = 4 suits
+// many splits of a small output, TPG = 1 a few splits of a large one.
 template <int TPG>
 __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk)
 {
