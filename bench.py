@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
+import math
 import os
 import sys
 import time
@@ -267,7 +268,11 @@ def gemv_i8_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=11008, nbu
            "bytes": nbytes, "M": M, "K": K, "N": N, "out": "s8 (requant)" if out_s8 else "s32",
            "weight_layout": "prepacked [K,N] -> [N][kp]" if prepacked else ("[N,K]" if trans_b else "[K,N]"),
            "rotated_weight_bytes": nbuf * K * N, "timing": t["timing"]}
-    if cpu_seconds > 0:
+    if cpu_seconds > 0 and prepacked:
+        out["cpu_baseline"] = cpu_i8_packed(a_h, w_h, trans_b, nbytes, cpu_seconds,
+                                            f"config 3 M={M} (s32 out, weight {'[N,K]' if trans_b else '[K,N]'} "
+                                            f"prepacked)")
+    elif cpu_seconds > 0:
         out["cpu_baseline"] = cpu_i8(a_h, w_h, trans_b, out_s8, sb_h, nbytes, cpu_seconds, "GB/s",
                                      f"config 3 M={M} ({'s8' if out_s8 else 's32'} out, weight "
                                      f"{'[N,K]' if trans_b else '[K,N]'})")
@@ -297,6 +302,61 @@ def cpu_i8(a, w, trans_b, out_s8, sb, nbytes, seconds, unit, what):
     return {"value": v, "unit": unit, "cores": cores, "kind": "reference", "us": sec * 1e6,
             "sample": f"{what} in full, {reps} calls; nnops' CPU MatMul (src/backend/cpu/matmul, AVX-512-VNNI) "
                       f"compiled from source, {cores} threads"}
+
+
+def _cpu_na(unit):
+    return {"value": None, "unit": unit, "cores": 0, "kind": "reference",
+            "sample": "n/a: oracle/_ref/libnnops_cpu.so not loadable on this host (no AVX-512 VNNI)"}
+
+
+def cpu_i8_packed(a, w, trans_b, nbytes, seconds, what):
+    """nnops' CPU MatMul over its own prepacked s8 weight (MatMul::
+    prepackWeights, src/ops/matmul.cpp:96-141, packed once outside the timed
+    calls), s32 out; GB/s of the GPU line's algorithmic bytes."""
+    import numpy as np
+    cpu = nnops_cpu()
+    if cpu is None:
+        return _cpu_na("GB/s")
+    M, K = a.shape
+    N = w.shape[0] if trans_b else w.shape[1]
+    cores = cpu_cores()
+    h = cpu.ref_cpu_prepack_i8(w.ctypes.data, N, K, int(trans_b), 0, None, cores)
+    if not h:
+        return {"value": None, "unit": "GB/s", "cores": cores, "kind": "reference",
+                "sample": "n/a: nnops' prepackWeights gave no packed form for this weight"}
+    c = np.zeros((M, N), np.int32)
+
+    def call():
+        rc = cpu.ref_cpu_matmul_i8_packed(a.ctypes.data, h, None, c.ctypes.data, M, N, K, 1.0, None, 1.0, 0, 0,
+                                          cores)
+        if rc != 0:
+            raise RuntimeError(f"nnops CPU packed MatMul failed: status {rc}")
+    try:
+        sec, reps = cpu_time(call, seconds)
+    finally:
+        cpu.ref_cpu_packed_free(h)
+    return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": cores, "kind": "reference", "us": sec * 1e6,
+            "sample": f"{what} in full, {reps} calls over nnops' own prepacked weight (MatMul::prepackWeights, "
+                      f"once, outside the timing); nnops' CPU MatMul (AVX-512-VNNI) compiled from source, "
+                      f"{cores} threads"}
+
+
+def cpu_call(call, seconds, work, unit, what):
+    """Times one nnops CPU call (a closure returning its status) in full;
+    `work` is the GPU line's algorithmic bytes (GB/s) or ops (TOPS/TFLOPS)."""
+    cpu = nnops_cpu()
+    if cpu is None:
+        return _cpu_na(unit)
+    cores = cpu_cores()
+
+    def once():
+        rc = call(cpu, cores)
+        if rc != 0:
+            raise RuntimeError(f"nnops CPU call failed: status {rc}")
+    sec, reps = cpu_time(once, seconds)
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {"value": work / sec / scale, "unit": unit, "cores": cores, "kind": "reference", "us": sec * 1e6,
+            "sample": f"{what} in full, {reps} calls; compiled from the nnops sources, {cores} threads"}
 
 
 def cpu_q4_1(a, blk, N, trans_b, nbytes, seconds, what):
@@ -361,6 +421,7 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
     """Config 4's GEMM; trans_b=False times the literal [K][N/32] layout
     (blocks along N) instead of the GGUF/Linear [N][K/32] one; a_f32 an f32
     A (nnops computes that product in f32: the f32 MFMA GEMM)."""
+    import numpy as np
     a_h = dg.normal(403, (M, K)).astype("float32" if a_f32 else "float16")
     b_h = dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)
     a = torch.from_numpy(a_h).cuda()
@@ -393,21 +454,34 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
         by = N * (K // 32) * 20 + M * K * (4 if a_f32 else 2) + M * N * 4
         out["gbs"] = by / (t["mean_ms"] * 1e-3) / 1e9
         out["frac_hbm"] = out["gbs"] / PEAK_HBM_GBS
-    if cpu_seconds > 0:
-        out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, 0, cpu_seconds,
+    if cpu_seconds > 0 and a_f32:
+        # nnops' f32 x q4_1 MatMul (f32 output, its FpRoute<float>)
+        cf = np.zeros((M, N), np.float32)
+        out["cpu_baseline"] = cpu_call(
+            lambda cpu, cores: cpu.ref_cpu_matmul_q4_1_ep(a_h.ctypes.data, 0, b_h.ctypes.data, None, cf.ctypes.data,
+                                                          M, N, K, int(trans_b), 1.0, 0.0, 0, 0, 0.0, 1.0,
+                                                          -math.inf, math.inf, cores),
+            cpu_seconds, fl, "TFLOPS", f"config 4 M={M} with an f32 A (nnops' f32 x q4_1 MatMul, f32 out)")
+    elif cpu_seconds > 0:
+        by = N * (K // 32) * 20 + M * K * 2 + M * N * 2
+        out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, trans_b, by, cpu_seconds,
                                        f"config 4 M={M} (weight {out['weight_layout']})")
     return out
 
 
-def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=4):
+def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, nbuf=4, cpu_seconds=0.0):
     """Linear's gated form (SwiGLU) over a q4_1 [2N, K] weight (blocks along
     K, the GGUF form) with bias, f16 X [M, K] -> f16 [M, N], through the
     operator API: the Q4_1 GEMM / GEMV into the workspace and the combine.
     M=1 rotates over nbuf weights (more than the MALL) so HBM is measured."""
-    x = torch.from_numpy(dg.normal(420 + M, (M, K)).astype("float16")).cuda()
+    import numpy as np
+    x_h = dg.normal(420 + M, (M, K)).astype("float16")
+    x = torch.from_numpy(x_h).cuda()
     nb = nbuf if M <= 48 else 1
-    ws_ = [torch.from_numpy(dg.q4_1_blocks(421 + i, 2 * N, K)).cuda() for i in range(nb)]
-    bias = torch.from_numpy((0.1 * dg.normal(425, (2 * N,))).astype("float16")).cuda()
+    w0_h = dg.q4_1_blocks(421, 2 * N, K)
+    ws_ = [torch.from_numpy(w0_h if i == 0 else dg.q4_1_blocks(421 + i, 2 * N, K)).cuda() for i in range(nb)]
+    bias_h = (0.1 * dg.normal(425, (2 * N,))).astype("float16")
+    bias = torch.from_numpy(bias_h).cuda()
     y = torch.zeros((M, N), dtype=torch.float16, device="cuda")
     op = na.Linear(gated=True, gate_activation=na.EP_SILU)
     ins = [[na.tensor(x), na.tensor(w, dtype=na.DT_Q4_1, shape=[2 * N, K]), na.tensor(bias)] for w in ws_]
@@ -425,19 +499,34 @@ def gated_ffn_case(torch, dg, na, stream, steps, warmup, M=1, K=4096, N=14336, n
     t = Timer(stream).time(step, steps, warmup)
     wbytes = 2 * N * (K // 32) * 20
     by = wbytes + M * K * 2 + M * N * 2 + 2 * N * 2
-    return {"us": t["mean_ms"] * 1e3, "gbs": by / (t["mean_ms"] * 1e-3) / 1e9,
-            "frac_hbm": by / (t["mean_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": by,
-            "tflops": 2.0 * M * 2 * N * K / (t["mean_ms"] * 1e-3) / 1e12,
-            "M": M, "K": K, "N": N, "weight_layout": "[2N][K/32 blocks] (gate rows, then value rows)",
-            "op": "Linear gated (SwiGLU) + bias, f16", "timing": t["timing"]}
+    fl = 2.0 * M * 2 * N * K
+    out = {"us": t["mean_ms"] * 1e3, "gbs": by / (t["mean_ms"] * 1e-3) / 1e9,
+           "frac_hbm": by / (t["mean_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": by,
+           "tflops": fl / (t["mean_ms"] * 1e-3) / 1e12,
+           "M": M, "K": K, "N": N, "weight_layout": "[2N][K/32 blocks] (gate rows, then value rows)",
+           "op": "Linear gated (SwiGLU) + bias, f16", "timing": t["timing"]}
+    if M > 48:
+        out["frac_f16_mfma"] = out["tflops"] / PEAK_F16_TFLOPS
+    if cpu_seconds > 0:
+        yc = np.zeros((M, N), np.float16)
+        # nnops' linear_cpu, gated (src/backend/cpu/matmul/linear.cpp:84-170, 199-309), Silu gate
+        out["cpu_baseline"] = cpu_call(
+            lambda cpu, cores: cpu.ref_cpu_linear_q4_1(x_h.ctypes.data, 1, w0_h.ctypes.data, bias_h.ctypes.data,
+                                                       yc.ctypes.data, M, 2 * N, K, 0, 0.0, 1.0, -math.inf,
+                                                       math.inf, 0, 0, 1, 6, 1.0, 0.0, math.inf, cores),
+            cpu_seconds, by if M <= 16 else fl, "GB/s" if M <= 16 else "TFLOPS",
+            f"gated FFN M={M} (nnops' linear_cpu, gated SwiGLU over the q4_1 [2N,K] weight, f16)")
+    return out
 
 
-def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8):
+def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nbuf=8, cpu_seconds=0.0):
     """Config 4 with the [K][N/32] weight prepacked (MatMul.prepackWeights:
     the nibble and d|m planes), through the operator API. Up to 48 rows of A
     rotate over nbuf packed weights (more than the MALL) so HBM is measured."""
-    a = torch.from_numpy(dg.normal(405, (M, K)).astype("float16")).cuda()
-    base = torch.from_numpy(dg.q4_1_blocks(406, K, N)).cuda()
+    a_h = dg.normal(405, (M, K)).astype("float16")
+    b_h = dg.q4_1_blocks(406, K, N)
+    a = torch.from_numpy(a_h).cuda()
+    base = torch.from_numpy(b_h).cuda()
     op = na.MatMul(transpose_b=False)
     nb = nbuf if M <= 48 else 1
     packed = []
@@ -467,6 +556,13 @@ def q41_packed_case(torch, dg, na, stream, steps, warmup, M, K=4096, N=14336, nb
     else:
         out["tflops"] = 2.0 * M * N * K / (t["mean_ms"] * 1e-3) / 1e12
         out["frac_f16_mfma"] = out["tflops"] / PEAK_F16_TFLOPS
+    if cpu_seconds > 0:
+        # nnops packs no q4_1 form (matmul_helper.cpp:695-723): its route for
+        # this weight reads the raw [K][N/32] blocks
+        by = N * (K // 32) * 20 + K * M * 2 + N * M * 2
+        out["cpu_baseline"] = cpu_q4_1(a_h, b_h, N, False, by, cpu_seconds,
+                                       f"config 4 M={M} over the raw [K][N/32] weight (nnops has no packed "
+                                       f"q4_1 form)")
     return out
 
 
@@ -558,14 +654,17 @@ def cfg5_case(torch, dg, na, stream, steps, warmup):
                                        "(src/backend/cpu/matmul/linear.cpp:226) nor a GELU on an integer one"}}
 
 
-def dense_fp_case(torch, dg, na, stream, steps, warmup, M, N=4096, K=4096, f16=True, nbuf=1):
+def dense_fp_case(torch, dg, na, stream, steps, warmup, M, N=4096, K=4096, f16=True, nbuf=1, cpu_seconds=0.0):
     """nnops' dense float route (MatMul f16 x f16 or f32 x f32, B [N, K]):
     C = A B with f32 accumulation. M <= 16 rotates over nbuf weights (more
     than the MALL) so HBM is measured."""
     dt = torch.float16 if f16 else torch.float32
     npdt = "float16" if f16 else "float32"
-    a = torch.from_numpy(dg.normal(440 + M, (M, K)).astype(npdt)).cuda()
-    base = torch.from_numpy(dg.normal(441, (N, K)).astype(npdt)).cuda()
+    import numpy as np
+    a_h = dg.normal(440 + M, (M, K)).astype(npdt)
+    b_h = dg.normal(441, (N, K)).astype(npdt)
+    a = torch.from_numpy(a_h).cuda()
+    base = torch.from_numpy(b_h).cuda()
     bs = [base] + [torch.roll(base, shifts=i, dims=1).contiguous() for i in range(1, nbuf)]
     c = torch.empty((M, N), dtype=dt, device="cuda")
     s = stream.cuda_stream
@@ -588,21 +687,31 @@ def dense_fp_case(torch, dg, na, stream, steps, warmup, M, N=4096, K=4096, f16=T
         out["bytes"] = by
     else:
         out["frac_mfma"] = out["tflops"] / (PEAK_F16_TFLOPS if f16 else PEAK_F32_TFLOPS)
+    if cpu_seconds > 0:
+        cc = np.zeros((M, N), npdt)
+        out["cpu_baseline"] = cpu_call(
+            lambda cpu, cores: cpu.ref_cpu_matmul_fp(a_h.ctypes.data, b_h.ctypes.data, cc.ctypes.data, M, N, K, 1,
+                                                     int(f16), cores),
+            cpu_seconds, by if M <= 16 else fl, "GB/s" if M <= 16 else "TFLOPS",
+            f"dense {npdt} {M}x{K}x{N} (nnops' CPU MatMul)")
     return out
 
 
-def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False):
+def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False, cpu_seconds=0.0):
     """QuantizeLinear f16 [R,C] -> s8 (per-token scales and zero points), or
     DequantizeLinear s8 -> f16, through the operator API. HBM-bound."""
     import numpy as np
-    scale = torch.from_numpy(dg.uniform(601, (R,), 0.01, 0.05)).cuda()
-    zp = torch.from_numpy(dg.ints(602, (R,), -8, 8, np.int8)).cuda()
+    sc_h = dg.uniform(601, (R,), 0.01, 0.05)
+    zp_h = dg.ints(602, (R,), -8, 8, np.int8)
+    x_h = dg.ints(603, (R, C), -128, 127) if dequant else dg.normal(603, (R, C), 1.0).astype("float16")
+    scale = torch.from_numpy(sc_h).cuda()
+    zp = torch.from_numpy(zp_h).cuda()
     if dequant:
-        x = torch.from_numpy(dg.ints(603, (R, C), -128, 127)).cuda()
+        x = torch.from_numpy(x_h).cuda()
         y = torch.empty((R, C), dtype=torch.float16, device="cuda")
         op = na.DequantizeLinear(axis=-1, output_dtype=na.DT_F16)
     else:
-        x = torch.from_numpy(dg.normal(603, (R, C), 1.0).astype("float16")).cuda()
+        x = torch.from_numpy(x_h).cuda()
         y = torch.empty((R, C), dtype=torch.int8, device="cuda")
         op = na.QuantizeLinear(axis=-1, output_dtype=na.DT_S8)
     ins = [na.tensor(x), na.tensor(scale), na.tensor(zp)]
@@ -611,29 +720,41 @@ def qdq_case(torch, dg, na, stream, steps, warmup, R=4096, C=4096, dequant=False
     t = Timer(stream).time(lambda: op.compute(outs, ins, stream=s), steps, warmup)
     nbytes = R * C * 3 + R * 5
     gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
-    return {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
-            "shape": [R, C], "op": "DequantizeLinear s8->f16" if dequant else "QuantizeLinear f16->s8",
-            "granularity": "per token"}
+    out = {"gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us": t["mean_ms"] * 1e3, "bytes": nbytes,
+           "shape": [R, C], "op": "DequantizeLinear s8->f16" if dequant else "QuantizeLinear f16->s8",
+           "granularity": "per token"}
+    if cpu_seconds > 0:
+        yc = np.zeros((R, C), np.float16 if dequant else np.int8)
+        out["cpu_baseline"] = cpu_call(
+            lambda cpu, cores: cpu.ref_cpu_qdq_f16(x_h.ctypes.data, sc_h.ctypes.data, zp_h.ctypes.data,
+                                                   yc.ctypes.data, R, C, int(dequant), cores),
+            cpu_seconds, nbytes, "GB/s", f"{out['op']} {R}x{C} per token (nnops' CPU operator)")
+    return out
 
 
-def fp_act_case(torch, dg, na, stream, steps, warmup, M=4096, N=4096, K=4096, dq_only=False):
+def fp_act_case(torch, dg, na, stream, steps, warmup, M=4096, N=4096, K=4096, dq_only=False, cpu_seconds=0.0):
     """The fp-activation int8 MatMul at config 2's shape: f16 A with per-token
     scales, s8 [N,K] weights with per-channel scales, f16 out (quantize A into
     the workspace, int8 GEMM, dequantize). dq_only: the int8 pair with an f16
     destination (the dequantizing output pass alone)."""
     import numpy as np
-    w = torch.from_numpy(dg.ints(702, (N, K), -127, 127)).cuda()
-    sb = torch.from_numpy(dg.uniform(703, (N,), 0.001, 0.01)).cuda()
-    bias = torch.from_numpy(dg.normal(704, (N,)).astype("float16")).cuda()
+    w_h = dg.ints(702, (N, K), -127, 127)
+    sb_h = dg.uniform(703, (N,), 0.001, 0.01)
+    bias_h = dg.normal(704, (N,)).astype("float16")
+    sa_h = dg.uniform(705, (M,), 0.01, 0.03)
+    a_h = dg.act_s8(701, (M, K)) if dq_only else dg.normal(701, (M, K), 1.0).astype("float16")
+    w = torch.from_numpy(w_h).cuda()
+    sb = torch.from_numpy(sb_h).cuda()
+    bias = torch.from_numpy(bias_h).cuda()
     c = torch.empty((M, N), dtype=torch.float16, device="cuda")
-    sa = torch.from_numpy(dg.uniform(705, (M,), 0.01, 0.03)).cuda()
+    sa = torch.from_numpy(sa_h).cuda()
     if dq_only:
-        a = torch.from_numpy(dg.act_s8(701, (M, K))).cuda()
+        a = torch.from_numpy(a_h).cuda()
         op = na.Linear(output_dtype=na.DT_F16, act=na.EP_RELU)
         ins = [na.tensor(a, scale_data=sa, granularity=1), na.tensor(w, scale_data=sb, granularity=2),
                na.tensor(bias)]
     else:
-        a = torch.from_numpy(dg.normal(701, (M, K), 1.0).astype("float16")).cuda()
+        a = torch.from_numpy(a_h).cuda()
         op = na.MatMul(transpose_b=True, act=na.EP_RELU)
         ins = [na.tensor(a, scale_data=sa, granularity=1), na.tensor(w, scale_data=sb, granularity=2),
                na.tensor(bias)]
@@ -643,9 +764,19 @@ def fp_act_case(torch, dg, na, stream, steps, warmup, M=4096, N=4096, K=4096, dq
     t = Timer(stream).time(lambda: op.compute(outs, ins, stream=s, workspace=ws), steps, warmup)
     ops = 2.0 * M * N * K
     tops = ops / (t["mean_ms"] * 1e-3) / 1e12
-    return {"tops": tops, "frac_int8_mfma": tops / PEAK_INT8_TOPS, "us": t["mean_ms"] * 1e3, "M": M, "N": N,
-            "K": K, "route": "int8 pair -> f16 (dequantizing destination)" if dq_only
-            else "f16 A (per-token QuantParams) x s8 -> f16"}
+    out = {"tops": tops, "frac_int8_mfma": tops / PEAK_INT8_TOPS, "us": t["mean_ms"] * 1e3, "M": M, "N": N,
+           "K": K, "route": "int8 pair -> f16 (dequantizing destination)" if dq_only
+           else "f16 A (per-token QuantParams) x s8 -> f16"}
+    if cpu_seconds > 0:
+        import numpy as np
+        cc = np.zeros((M, N), np.float16)
+        out["cpu_baseline"] = cpu_call(
+            lambda cpu, cores: cpu.ref_cpu_matmul_dq_f16(a_h.ctypes.data, int(not dq_only), sa_h.ctypes.data,
+                                                         w_h.ctypes.data, sb_h.ctypes.data, bias_h.ctypes.data,
+                                                         cc.ctypes.data, M, N, K, 1, cores),
+            cpu_seconds, ops, "TOPS", f"{out['route']} {M}x{K}x{N} (nnops' CPU MatMul: "
+                                      f"{'DqRoute' if dq_only else 'matmul_dq_from_fp'})")
+    return out
 
 
 def ceilings(torch, na, stream):
@@ -779,6 +910,28 @@ def cpu_baseline(seconds):
                       + f", {cores} threads"}
 
 
+def summarize(secondary):
+    """One compact entry per secondary line: step time, fraction of the
+    bounding roofline, and the CPU baseline (value, unit, threads) or null
+    with the reason."""
+    out = {}
+    for key, r in secondary.items():
+        frac = next((r[k] for k in ("frac_hbm", "frac_int8_mfma", "frac_f16_mfma", "frac_f32_mfma", "frac_mfma")
+                     if k in r), None)
+        bound = next((b for k, b in (("frac_hbm", "hbm"), ("frac_int8_mfma", "int8"), ("frac_f16_mfma", "f16"),
+                                     ("frac_f32_mfma", "f32"), ("frac_mfma", "mfma")) if k in r), None)
+        e = {"us": round(r["us"], 2), "frac": None if frac is None else round(frac, 3), "of": bound}
+        cb = r.get("cpu_baseline")
+        if cb is None:
+            e["cpu"] = None
+        elif cb.get("value") is None:
+            e["cpu"] = cb.get("sample", "n/a")[:90]
+        else:
+            e["cpu"] = [round(cb["value"], 2), cb["unit"], cb["cores"]]
+        out[key] = e
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -841,31 +994,38 @@ def main():
             for s8 in (False, True):
                 secondary[f"cfg3_int8_gemv_m{M}_kn_{'s8' if s8 else 's32'}"] = gemv_i8_case(
                     torch, dg, na, stream, st, wu, M=M, trans_b=False, out_s8=s8, cpu_seconds=cs)
-            secondary[f"cfg3_int8_gemv_m{M}_nk_s32"] = gemv_i8_case(torch, dg, na, stream, st, wu, M=M, trans_b=True)
+            secondary[f"cfg3_int8_gemv_m{M}_nk_s32"] = gemv_i8_case(torch, dg, na, stream, st, wu, M=M, trans_b=True,
+                                                                   cpu_seconds=cs)
         for M in (1, 16):
             secondary[f"cfg3_int8_gemv_m{M}_kn_prepacked"] = gemv_i8_case(torch, dg, na, stream, st, wu, M=M,
-                                                                         prepacked=True)
+                                                                         prepacked=True, cpu_seconds=cs)
         secondary["cfg4_q4_1_gemv_m1"] = gemv_q41_case(torch, dg, na, stream, st, wu, cpu_seconds=cs)
         secondary["cfg4_q4_1_gemm_m512"] = q41_gemm_case(torch, dg, na, stream, few, wu, cpu_seconds=cs)
         secondary["cfg4_q4_1_gemv_m1_kn"] = gemv_q41_case(torch, dg, na, stream, st, wu, trans_b=False,
                                                           cpu_seconds=cs)
         secondary["cfg4_q4_1_gemm_m512_kn"] = q41_gemm_case(torch, dg, na, stream, few, wu, trans_b=False,
                                                             cpu_seconds=cs)
-        secondary["cfg4_q4_1_m8_decode_batch"] = q41_gemm_case(torch, dg, na, stream, st, wu, M=8)
-        secondary["cfg4_q4_1_gemm_m512_f32a"] = q41_gemm_case(torch, dg, na, stream, few, wu, a_f32=True)
-        secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1)
-        secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512)
-        secondary["cfg4_q4_1_m8_decode_batch_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=8)
-        secondary["gated_ffn_swiglu_m1"] = gated_ffn_case(torch, dg, na, stream, st, wu)
-        secondary["gated_ffn_swiglu_m512"] = gated_ffn_case(torch, dg, na, stream, few, wu, M=512)
+        secondary["cfg4_q4_1_m8_decode_batch"] = q41_gemm_case(torch, dg, na, stream, st, wu, M=8, cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemm_m512_f32a"] = q41_gemm_case(torch, dg, na, stream, few, wu, a_f32=True,
+                                                              cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemv_m1_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=1,
+                                                                      cpu_seconds=cs)
+        secondary["cfg4_q4_1_gemm_m512_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, few, wu, M=512,
+                                                                        cpu_seconds=cs)
+        secondary["cfg4_q4_1_m8_decode_batch_kn_prepacked"] = q41_packed_case(torch, dg, na, stream, st, wu, M=8,
+                                                                              cpu_seconds=cs)
+        secondary["gated_ffn_swiglu_m1"] = gated_ffn_case(torch, dg, na, stream, st, wu, cpu_seconds=cs)
+        secondary["gated_ffn_swiglu_m512"] = gated_ffn_case(torch, dg, na, stream, few, wu, M=512, cpu_seconds=cs)
         secondary["cfg5_s8_addto_gelu"] = cfg5_case(torch, dg, na, stream, few, wu)
-        secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, few, wu, dq_only=True)
-        secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, few, wu)
-        secondary["dense_f16_gemm_4096"] = dense_fp_case(torch, dg, na, stream, few, wu, M=4096)
+        secondary["dq_gemm_4096_f16_out"] = fp_act_case(torch, dg, na, stream, few, wu, dq_only=True,
+                                                        cpu_seconds=cs)
+        secondary["fp_act_matmul_4096_f16"] = fp_act_case(torch, dg, na, stream, few, wu, cpu_seconds=cs)
+        secondary["dense_f16_gemm_4096"] = dense_fp_case(torch, dg, na, stream, few, wu, M=4096, cpu_seconds=cs)
         secondary["dense_f16_gemv_m1_14336x4096"] = dense_fp_case(torch, dg, na, stream, st, wu, M=1, N=14336,
-                                                                   nbuf=4)
-        secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu)
-        secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu, dequant=True)
+                                                                   nbuf=4, cpu_seconds=cs)
+        secondary["quantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu, cpu_seconds=cs)
+        secondary["dequantize_linear_4096x4096_f16"] = qdq_case(torch, dg, na, stream, st, wu, dequant=True,
+                                                                cpu_seconds=cs)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC, "value": main_res["value"], "unit": main_res["unit"], "n_gpus": 1,
@@ -875,8 +1035,12 @@ def main():
         "config": main_res["config"], "roofline": main_res["roofline"], "cpu_baseline": cpu,
         "timing": main_res["timing"], "eager_ms_per_step": main_res["eager_ms_per_step"],
         "graph_ms_per_step": main_res["t"].get("graph_ms"),
-        "secondary": secondary,
+        "summary": summarize(secondary),
     }
+    # the full per-line records first, then the headline line (the last one,
+    # kept short enough for a log tail to hold it whole)
+    if secondary:
+        print(json.dumps({"secondary_detail": secondary}))
     print(json.dumps(line))
 
 

@@ -62,6 +62,16 @@ inline void nnops_launch(F kernel, const dim3& grid, const dim3& block, uint32_t
 }
 #define NNOPS_LAUNCH(kernel, ...) ::nnops_amd::nnops_launch(kernel, __VA_ARGS__)
 
+// Disarms the calling thread's timing events when a public entry point
+// returns, so a call that returns before launching (a rejected argument, an
+// empty problem) leaves no armed pair for an unrelated later kernel.
+struct TimingDisarm {
+    TimingDisarm() = default;
+    TimingDisarm(const TimingDisarm&) = delete;
+    TimingDisarm& operator=(const TimingDisarm&) = delete;
+    ~TimingDisarm() { launch_timing() = LaunchTiming{}; }
+};
+
 // Launch epochs for the split-completion flags of the one-launch split
 // kernels: unique in the process and never 0. Consecutive counter values are
 // spread over 64 bits (splitmix64's finalizer), so a flag word that a caller's

@@ -493,7 +493,6 @@ __global__ __launch_bounds__(256, 1) void gemm_fp_tile(FpKern p)
 constexpr int kGemvRows = 16;    // rows of A per GEMV launch
 constexpr int64_t kGemvMaxM = 16;
 
-// K split of the [K][N] GEMV: about 512 workgroups, at least 64 rows each
 // K split of the [K][N] GEMV: about 512 workgroups (each 1 KiB of columns),
 // at least 128 rows (32 per wave) per split
 int kn_splits_fp(int64_t n, int64_t k, bool f16)
@@ -574,6 +573,7 @@ extern "C" size_t nnops_hip_gemm_fp_workspace_size(const NnopsGemmFpArgs* g)
 
 extern "C" int nnops_hip_gemm_fp(const NnopsGemmFpArgs* g, void* workspace, size_t ws_bytes, void* stream)
 {
+    const TimingDisarm disarm;
     if (g == nullptr) {
         return NNOPS_INVALID_ARGUMENT;
     }

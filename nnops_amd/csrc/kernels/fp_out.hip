@@ -111,6 +111,7 @@ using namespace nnops_amd;
 
 extern "C" int nnops_hip_fp_output_pass(const NnopsFpOutArgs* a, void* stream)
 {
+    const TimingDisarm disarm;
     if (a == nullptr || a->rows < 0 || a->n < 0 || a->n > INT32_MAX) {
         return NNOPS_INVALID_ARGUMENT;
     }

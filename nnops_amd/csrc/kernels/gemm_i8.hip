@@ -1314,6 +1314,88 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     out4_store(p, o, nb, raw);
 }
 
+// The same sum and output pass for s8 / u8 destinations with row-uniform
+// parameters (per-tensor s_a, s_out and zp_out, no zero-point terms, 16-byte
+// aligned tables, 4-byte aligned destination rows), with the activation,
+// float epilogue and residual order fixed at compile time: every load a
+// thread needs (its splits' partial groups, the column tables and the
+// residual word) is issued before the first is used, and the arithmetic is
+// straight-line. One thread per 4-column group; element for element the
+// operations of epi_value, so the bytes equal gemm_i8_reduce's.
+template <int ACT, bool FEP, bool ADD, bool PRE>
+__global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit sk)
+{
+    const EpiParams& ep = p.ep;
+    const int groups = p.n >> 2;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (int64_t)p.m * groups) {
+        return;
+    }
+    const int m = (int)(gid / groups);
+    const int nb = (int)(gid - (int64_t)m * groups) * 4;
+    const int64_t slab = (int64_t)p.m * p.n;
+    const int32_t* src = sk.part + (int64_t)m * p.n + nb;
+    v4i raw = v4i{0, 0, 0, 0};
+    int s = 0;
+    for (; s + 3 < sk.splits; s += 4) {
+        const v4i x0 = *reinterpret_cast<const v4i*>(src + s * slab);
+        const v4i x1 = *reinterpret_cast<const v4i*>(src + (s + 1) * slab);
+        const v4i x2 = *reinterpret_cast<const v4i*>(src + (s + 2) * slab);
+        const v4i x3 = *reinterpret_cast<const v4i*>(src + (s + 3) * slab);
+        raw += (x0 + x1) + (x2 + x3);
+    }
+    for (; s < sk.splits; ++s) {
+        raw += *reinterpret_cast<const v4i*>(src + s * slab);
+    }
+    int8_t* c8 = static_cast<int8_t*>(p.c) + (int64_t)m * p.ldc_bytes + nb;
+    uint32_t oldw = 0;
+    if constexpr (ADD) {
+        oldw = *reinterpret_cast<const uint32_t*>(c8);
+    }
+    const v4f sb = ep.s_b != nullptr ? *reinterpret_cast<const v4f*>(ep.s_b + nb)
+                                     : v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+    const v4i bias = ep.bias != nullptr ? *reinterpret_cast<const v4i*>(ep.bias + nb) : v4i{0, 0, 0, 0};
+    const bool u8 = ep.out_kind == NNOPS_OUT_U8;
+    const bool even = ep.round_even != 0;
+    const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
+    uint32_t outw = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        int32_t v = raw[e] + bias[e];
+        int32_t q;
+        if constexpr (!FEP) {
+            if constexpr (ACT == NNOPS_ACT_RELU) {
+                v = v < 0 ? 0 : v;
+            }
+            q = requant_clamped(__fmul_rn((float)v, __fmul_rn(row_k, sb[e])), ep.zp_out, u8, even);
+        } else {
+            float f = __fmul_rn((float)v, __fmul_rn(ep.s_a_scalar, sb[e]));
+            float res = 0.0f;
+            if constexpr (ADD) {
+                const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
+                const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
+                res = __fmul_rn((float)(old - ep.zp_out), ep.s_out);
+                if constexpr (PRE) {
+                    f = __fadd_rn(f, res);
+                }
+            }
+            f = f < ep.min_clip ? ep.min_clip : f;
+            f = ep.max_clip < f ? ep.max_clip : f;
+            if constexpr (ACT == NNOPS_ACT_RELU) {
+                f = f > 0.0f ? f : 0.0f;
+            } else if constexpr (ACT == NNOPS_ACT_GELU) {
+                f = gelu_tanh(f);
+            }
+            if constexpr (ADD && !PRE) {
+                f = __fadd_rn(f, res);
+            }
+            q = requant_clamped(__fdiv_rn(f, ep.s_out), ep.zp_out, u8, even);
+        }
+        outw |= ((uint32_t)q & 0xffu) << (8 * e);
+    }
+    *reinterpret_cast<uint32_t*>(c8) = outw;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV / skinny GEMM, M <= 16.
 // ---------------------------------------------------------------------------
@@ -2168,9 +2250,50 @@ void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, i
     }
 }
 
+// gemm_i8_reduce_q's conditions: an s8 / u8 destination with row-uniform
+// parameters and no zero-point terms, 16-byte-aligned tables and 4-byte
+// aligned destination rows, an identity / Relu / GELU activation (GELU only
+// with the float epilogue).
+bool reduce_q_ok(const GemmI8Kern& k)
+{
+    const EpiParams& e = k.ep;
+    return (e.out_kind == NNOPS_OUT_S8 || e.out_kind == NNOPS_OUT_U8) && !e.compensate && e.s_a == nullptr &&
+           e.s_out_rows == nullptr && e.zp_out_rows == nullptr && ((uintptr_t)e.s_b % 16) == 0 &&
+           ((uintptr_t)e.bias % 16) == 0 && ((uintptr_t)k.c % 4) == 0 && (k.ldc_bytes % 4) == 0 &&
+           (e.act == NNOPS_ACT_NONE || e.act == NNOPS_ACT_RELU || (e.act == NNOPS_ACT_GELU && e.float_ep));
+}
+
+template <int ACT>
+void launch_reduce_q_act(const GemmI8Kern& k, const RingSplit& sk, const dim3& grid, hipStream_t s)
+{
+    const EpiParams& e = k.ep;
+    if (!e.float_ep) {
+        if constexpr (ACT != NNOPS_ACT_GELU) {
+            NNOPS_LAUNCH((gemm_i8_reduce_q<ACT, false, false, false>), grid, dim3(256), 0, s, k, sk);
+        }
+    } else if (!e.add_to) {
+        NNOPS_LAUNCH((gemm_i8_reduce_q<ACT, true, false, false>), grid, dim3(256), 0, s, k, sk);
+    } else if (e.residual_pre) {
+        NNOPS_LAUNCH((gemm_i8_reduce_q<ACT, true, true, true>), grid, dim3(256), 0, s, k, sk);
+    } else {
+        NNOPS_LAUNCH((gemm_i8_reduce_q<ACT, true, true, false>), grid, dim3(256), 0, s, k, sk);
+    }
+}
+
 void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
 {
     const int64_t groups = (int64_t)k.m * (k.n / 4);
+    if (sk.splits <= 8 && reduce_q_ok(k)) {
+        const dim3 grid((unsigned)((groups + 255) / 256));
+        if (k.ep.act == NNOPS_ACT_GELU) {
+            launch_reduce_q_act<NNOPS_ACT_GELU>(k, sk, grid, s);
+        } else if (k.ep.act == NNOPS_ACT_RELU) {
+            launch_reduce_q_act<NNOPS_ACT_RELU>(k, sk, grid, s);
+        } else {
+            launch_reduce_q_act<NNOPS_ACT_NONE>(k, sk, grid, s);
+        }
+        return;
+    }
     if (sk.splits > 8) {
         NNOPS_LAUNCH(gemm_i8_reduce<4>, dim3((unsigned)((groups * 4 + 255) / 256)), dim3(256), 0, s, k, sk);
     } else {
@@ -2290,6 +2413,7 @@ extern "C" size_t nnops_hip_prepack_i8_bytes(int64_t k, int64_t n)
 extern "C" int nnops_hip_prepack_i8(const int8_t* b, int64_t k, int64_t n, int64_t ldb, int32_t trans_b,
                                     void* out, void* stream)
 {
+    const TimingDisarm disarm;
     if (k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX) {
         return NNOPS_INVALID_ARGUMENT;
     }
@@ -2325,6 +2449,7 @@ extern "C" size_t nnops_hip_gemm_i8_workspace_size(const NnopsGemmI8Args* g)
 
 extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size_t ws_bytes, void* stream)
 {
+    const TimingDisarm disarm;
     if (g == nullptr || g->m < 0 || g->n < 0 || g->k < 0) {
         return NNOPS_INVALID_ARGUMENT;
     }

@@ -16,6 +16,7 @@
 
 #include <mutex>
 
+#include "common.hpp"
 #include "nnops_amd.h"
 
 namespace {
@@ -34,8 +35,18 @@ void* scratch_on(int dev)
 {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
+        // The first call on a device may come while the caller's stream is
+        // being captured into a graph: the lookup enqueues nothing, so this
+        // thread's capture mode is relaxed around it (a global-mode capture
+        // would otherwise reject an API call it cannot vet) and restored.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
         void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+        const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (exchanged) {
+            (void)hipThreadExchangeStreamCaptureMode(&mode);
+        }
+        if (rc != hipSuccess || p == nullptr) {
             (void)hipGetLastError();
             return nullptr;
         }
@@ -48,6 +59,7 @@ void* scratch_on(int dev)
 
 extern "C" int nnops_hip_gemm_i8_noalloc(const NnopsGemmI8Args* args, void* stream)
 {
+    const nnops_amd::TimingDisarm disarm;
     if (args == nullptr) {
         return NNOPS_INVALID_ARGUMENT;
     }

@@ -2779,6 +2779,7 @@ extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
 
 extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, size_t ws_bytes, void* stream)
 {
+    const TimingDisarm disarm;
     if (g == nullptr || g->m < 0 || g->n < 0 || g->k < 0) {
         return NNOPS_INVALID_ARGUMENT;
     }
@@ -3008,6 +3009,7 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
 
 extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsFpOutArgs* pass, void* stream)
 {
+    const TimingDisarm disarm;
     if (g == nullptr || pass == nullptr) {
         return NNOPS_INVALID_ARGUMENT;
     }
@@ -3063,6 +3065,7 @@ extern "C" size_t nnops_hip_prepack_q4_1_bytes(int64_t k, int64_t n)
 extern "C" int nnops_hip_prepack_q4_1(const uint8_t* b, int64_t k, int64_t n, int64_t ldb_bytes, int32_t trans_b,
                                       void* out, void* stream)
 {
+    const TimingDisarm disarm;
     if (trans_b) {
         return NNOPS_UNSUPPORTED;  // blocks along K: no packed form
     }

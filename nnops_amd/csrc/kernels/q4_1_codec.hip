@@ -160,6 +160,10 @@ int check_codec(const void* src, const void* dst, int64_t rows, int64_t cols)
 
 unsigned codec_grid(int64_t blocks) { return (unsigned)((blocks + 31) / 32); }
 
+// 32 blocks per 256-thread workgroup: the grid's work-items must fit a
+// dispatch's 32-bit count.
+bool codec_grid_fits(int64_t blocks) { return (blocks + 31) / 32 <= (int64_t)(UINT32_MAX / 256); }
+
 }  // namespace
 }  // namespace nnops_amd
 
@@ -168,6 +172,7 @@ using namespace nnops_amd;
 extern "C" int nnops_hip_q4_1_quantize(const void* src, int32_t src_f16, int64_t rows, int64_t cols, int64_t ld_src,
                                        void* dst, int64_t ld_dst_bytes, void* stream)
 {
+    const TimingDisarm disarm;
     if (int rc = check_codec(src, dst, rows, cols); rc != NNOPS_OK) {
         return rc;
     }
@@ -177,8 +182,11 @@ extern "C" int nnops_hip_q4_1_quantize(const void* src, int32_t src_f16, int64_t
     const int64_t nb = (cols + 31) / 32;
     const size_t esz = src_f16 ? 2 : 4;
     if (ld_src < cols || ld_dst_bytes < nb * 20 || (ld_dst_bytes & 3) || ((uintptr_t)dst & 3) ||
-        ((uintptr_t)src % esz) != 0 || rows * nb > (int64_t)INT32_MAX * 32) {
+        ((uintptr_t)src % esz) != 0) {
         return NNOPS_INVALID_ARGUMENT;
+    }
+    if (!codec_grid_fits(rows * nb)) {
+        return NNOPS_UNSUPPORTED;   // one dispatch holds at most 2^32 - 1 work-items
     }
     CodecArgs a{src, dst, rows, cols, ld_src, ld_dst_bytes, src_f16 ? 1 : 0, nb};
     NNOPS_LAUNCH(q4_1_quantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,
@@ -189,6 +197,7 @@ extern "C" int nnops_hip_q4_1_quantize(const void* src, int32_t src_f16, int64_t
 extern "C" int nnops_hip_q4_1_dequantize(const void* src, int64_t ld_src_bytes, int64_t rows, int64_t cols, void* dst,
                                          int32_t dst_f16, int64_t ld_dst, void* stream)
 {
+    const TimingDisarm disarm;
     if (int rc = check_codec(src, dst, rows, cols); rc != NNOPS_OK) {
         return rc;
     }
@@ -198,8 +207,11 @@ extern "C" int nnops_hip_q4_1_dequantize(const void* src, int64_t ld_src_bytes, 
     const int64_t nb = (cols + 31) / 32;
     const size_t esz = dst_f16 ? 2 : 4;
     if (ld_dst < cols || ld_src_bytes < nb * 20 || (ld_src_bytes & 3) || ((uintptr_t)src & 3) ||
-        ((uintptr_t)dst % esz) != 0 || rows * nb > (int64_t)INT32_MAX * 32) {
+        ((uintptr_t)dst % esz) != 0) {
         return NNOPS_INVALID_ARGUMENT;
+    }
+    if (!codec_grid_fits(rows * nb)) {
+        return NNOPS_UNSUPPORTED;   // one dispatch holds at most 2^32 - 1 work-items
     }
     CodecArgs a{src, dst, rows, cols, ld_src_bytes, ld_dst, dst_f16 ? 1 : 0, nb};
     NNOPS_LAUNCH(q4_1_dequantize_kernel, dim3(codec_grid(rows * nb)), dim3(256), 0,

@@ -319,6 +319,7 @@ using namespace nnops_amd;
 
 extern "C" int nnops_hip_quantize_linear(const NnopsQdqArgs* g, void* stream)
 {
+    const TimingDisarm disarm;
     const int rc = qdq_check(g, true);
     if (rc >= 0) {
         return rc;
@@ -331,6 +332,7 @@ extern "C" int nnops_hip_quantize_linear(const NnopsQdqArgs* g, void* stream)
 
 extern "C" int nnops_hip_dequantize_linear(const NnopsQdqArgs* g, void* stream)
 {
+    const TimingDisarm disarm;
     const int rc = qdq_check(g, false);
     if (rc >= 0) {
         return rc;

@@ -177,6 +177,22 @@ def cpu_lib():
                                              C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
                                              C.c_float, C.c_int]
         _cpu.ref_cpu_linear_q4_1.restype = C.c_int
+        _cpu.ref_cpu_prepack_i8.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_int, C.c_void_p,
+                                            C.c_int]
+        _cpu.ref_cpu_prepack_i8.restype = C.c_void_p
+        _cpu.ref_cpu_packed_free.argtypes = [C.c_void_p]
+        _cpu.ref_cpu_packed_free.restype = None
+        _cpu.ref_cpu_matmul_i8_packed.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                                  C.c_int64, C.c_int64, C.c_float, C.c_void_p, C.c_float,
+                                                  C.c_int32, C.c_int, C.c_int]
+        _cpu.ref_cpu_matmul_i8_packed.restype = C.c_int
+        _cpu.ref_cpu_matmul_dq_f16.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int,
+                                               C.c_int]
+        _cpu.ref_cpu_matmul_dq_f16.restype = C.c_int
+        _cpu.ref_cpu_qdq_f16.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
+                                         C.c_int, C.c_int]
+        _cpu.ref_cpu_qdq_f16.restype = C.c_int
     return _cpu
 
 

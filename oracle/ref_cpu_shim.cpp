@@ -9,9 +9,11 @@
 // parallel_for.hpp:60-110) run on a small std::thread pool defined below.
 #include "nnops/ops/linear.hpp"
 #include "nnops/ops/matmul.hpp"
+#include "nnops/ops/quant_linear.hpp"
 
 #include <atomic>
 #include <condition_variable>
+#include <cstdlib>
 #include <cstdint>
 #include <functional>
 #include <mutex>
@@ -327,6 +329,172 @@ int ref_cpu_matmul_fp(const void* a, const void* b, void* c, int64_t M, int64_t 
     const TensorView ins[] = {av, bv};
     TensorView outs[] = {cv};
     const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 2), ctx);
+    return static_cast<int>(st);
+}
+
+// nnops' two-step prepackWeights of an s8 weight for the integer route
+// (src/ops/matmul.cpp:96-141: the query for the packed descriptor, then the
+// fill), kept in a heap blob; the handle is freed by ref_cpu_packed_free.
+struct PackedI8 {
+    void* blob = nullptr;
+    int64_t shape[2] = {0, 0};
+    int64_t pitch = 0;
+    DataType dtype = DataType::s8;
+    TensorLayout layout = TensorLayout::Dense;
+    int trans_b = 0, out_s8 = 0;
+};
+
+void* ref_cpu_prepack_i8(const int8_t* w, int64_t N, int64_t K, int trans_b, int out_s8, const float* s_b,
+                         int threads)
+{
+    Pool* p = pool_of(threads);
+    QuantParams qb;
+    if (s_b != nullptr) {
+        qb.granularity = QuantGranularity::PerChannel;
+        qb.scale_data = s_b;
+        qb.num_scales = N;
+    }
+    const int64_t wshape_t[] = {N, K}, wshape[] = {K, N};
+    TensorView wv(trans_b ? std::span<const int64_t>(wshape_t) : std::span<const int64_t>(wshape), DataType::s8,
+                  const_cast<int8_t*>(w), TensorLayout::Dense, qb);
+    MatMulAttributes attrs{};
+    attrs.transpose_b = trans_b != 0;
+    attrs.output_dtype = out_s8 ? DataType::s8 : DataType::s32;
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView bq[] = {wv};
+    TensorView q;
+    TensorView oq[] = {q};
+    op->prepackWeights(bq, oq, ctx);
+    if (oq[0].rank() != 2) {
+        return nullptr;     // no packed form
+    }
+    auto* h = new PackedI8;
+    h->shape[0] = oq[0].shape(0);
+    h->shape[1] = oq[0].shape(1);
+    h->pitch = oq[0].pitch();
+    h->dtype = oq[0].data_type();
+    h->layout = oq[0].layout();
+    h->trans_b = trans_b;
+    h->out_s8 = out_s8;
+    const size_t bytes = (size_t)h->pitch * (size_t)h->shape[0];
+    h->blob = std::aligned_alloc(64, (bytes + 63) / 64 * 64);
+    TensorView fill(std::span<const int64_t>(h->shape, 2), h->dtype, h->blob, h->pitch, h->layout, qb);
+    TensorView oq2[] = {fill};
+    op->prepackWeights(bq, oq2, ctx);
+    return h;
+}
+
+void ref_cpu_packed_free(void* handle)
+{
+    auto* h = static_cast<PackedI8*>(handle);
+    if (h != nullptr) {
+        std::free(h->blob);
+        delete h;
+    }
+}
+
+// The int8 MatMul of ref_cpu_matmul_i8 over a prepacked weight.
+int ref_cpu_matmul_i8_packed(const int8_t* a, const void* handle, const int32_t* bias, void* c, int64_t M,
+                             int64_t N, int64_t K, float s_a, const float* s_b, float s_out, int32_t zp_out,
+                             int relu, int threads)
+{
+    const auto* h = static_cast<const PackedI8*>(handle);
+    Pool* p = pool_of(threads);
+    QuantParams qa;
+    qa.scale = s_a;
+    QuantParams qb;
+    if (s_b != nullptr) {
+        qb.granularity = QuantGranularity::PerChannel;
+        qb.scale_data = s_b;
+        qb.num_scales = N;
+    }
+    QuantParams qc;
+    qc.scale = s_out;
+    qc.zero_point = zp_out;
+    const int64_t ashape[] = {M, K}, cshape[] = {M, N}, bshape[] = {N};
+    TensorView av(ashape, DataType::s8, const_cast<int8_t*>(a), TensorLayout::Dense, qa);
+    TensorView wv(std::span<const int64_t>(h->shape, 2), h->dtype, h->blob, h->pitch, h->layout, qb);
+    TensorView bv(bshape, DataType::s32, const_cast<int32_t*>(bias));
+    const DataType odt = h->out_s8 ? DataType::s8 : DataType::s32;
+    TensorView cv(cshape, odt, c, TensorLayout::Dense, h->out_s8 ? qc : QuantParams{});
+    MatMulAttributes attrs{};
+    attrs.transpose_b = h->trans_b != 0;
+    attrs.output_dtype = odt;
+    if (relu) {
+        attrs.epilogue.type = EpilogueActivateType::Relu;
+    }
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {av, wv, bv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, bias ? 3 : 2), ctx);
+    return static_cast<int>(st);
+}
+
+// The int8 pair with a dequantizing f16 destination (nnops' DqRoute): s8 A
+// [M,K] with per-token scales (or an f16 A with per-token QuantParams,
+// quantized by nnops' matmul_dq_from_fp when a_f16), s8 W [N,K] with
+// per-channel scales, f16 bias [N] or NULL, Relu, f16 C [M,N].
+int ref_cpu_matmul_dq_f16(const void* a, int a_f16, const float* s_a_rows, const int8_t* w, const float* s_b,
+                          const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int relu,
+                          int threads)
+{
+    Pool* p = pool_of(threads);
+    QuantParams qa;
+    qa.granularity = QuantGranularity::PerToken;
+    qa.scale_data = s_a_rows;
+    qa.num_scales = M;
+    QuantParams qb;
+    qb.granularity = QuantGranularity::PerChannel;
+    qb.scale_data = s_b;
+    qb.num_scales = N;
+    const int64_t ashape[] = {M, K}, wshape[] = {N, K}, cshape[] = {M, N}, bshape[] = {N};
+    TensorView av(ashape, a_f16 ? DataType::f16 : DataType::s8, const_cast<void*>(a), TensorLayout::Dense, qa);
+    TensorView wv(wshape, DataType::s8, const_cast<int8_t*>(w), TensorLayout::Dense, qb);
+    TensorView bv(bshape, DataType::f16, const_cast<uint16_t*>(bias));
+    TensorView cv(cshape, DataType::f16, c);
+    MatMulAttributes attrs{};
+    attrs.transpose_b = true;
+    attrs.output_dtype = DataType::f16;
+    if (relu) {
+        attrs.epilogue.type = EpilogueActivateType::Relu;
+    }
+    auto op = MatMul::create(attrs, Backend::CPU);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {av, wv, bv};
+    TensorView outs[] = {cv};
+    const Status st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, bias ? 3 : 2), ctx);
+    return static_cast<int>(st);
+}
+
+// nnops' QuantizeLinear (f16 x [R,C] -> s8) or DequantizeLinear (s8 -> f16)
+// with per-token scales and s8 zero points (axis -1), through
+// QuantizeLinear / DequantizeLinear::create / compute
+// (include/nnops/ops/quant_linear.hpp:47-122).
+int ref_cpu_qdq_f16(const void* x, const float* scale, const int8_t* zp, void* y, int64_t R, int64_t Cc,
+                    int dequant, int threads)
+{
+    Pool* p = pool_of(threads);
+    const int64_t shape[] = {R, Cc}, pshape[] = {R};
+    QuantLinearAttributes attrs{};
+    attrs.axis = -1;
+    attrs.output_dtype = dequant ? DataType::f16 : DataType::s8;
+    TensorView xv(shape, dequant ? DataType::s8 : DataType::f16, const_cast<void*>(x));
+    TensorView sv(pshape, DataType::f32, const_cast<float*>(scale));
+    TensorView zv(pshape, DataType::s8, const_cast<int8_t*>(zp));
+    TensorView yv(shape, dequant ? DataType::f16 : DataType::s8, y);
+    const ComputeContext ctx = context_on(p);
+    const TensorView ins[] = {xv, sv, zv};
+    TensorView outs[] = {yv};
+    Status st;
+    if (dequant) {
+        auto op = DequantizeLinear::create(attrs, Backend::CPU);
+        st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 3), ctx);
+    } else {
+        auto op = QuantizeLinear::create(attrs, Backend::CPU);
+        st = op->compute(std::span<TensorView>(outs), std::span<const TensorView>(ins, 3), ctx);
+    }
     return static_cast<int>(st);
 }
 

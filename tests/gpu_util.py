@@ -41,3 +41,18 @@ def norm_err(got, want):
     rms = np.sqrt(np.mean(want * want)) if want.size else 1.0
     den = np.maximum(np.abs(want), rms)
     return float(np.max(np.abs(got - want) / den)) if want.size else 0.0
+
+
+def oracle_rows(fn, m, band=16, threads=None):
+    """Every row of an M-row oracle result, computed in row bands of `band`
+    on a thread pool (the oracle's C calls release the GIL): fn(r0, r1)
+    returns rows [r0, r1) of the result. Lets the full-size configurations
+    be compared in full within seconds."""
+    import concurrent.futures as cf
+    import os
+    if threads is None:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    starts = list(range(0, m, band))
+    with cf.ThreadPoolExecutor(threads) as ex:
+        parts = list(ex.map(lambda r0: fn(r0, min(m, r0 + band)), starts))
+    return np.concatenate(parts, axis=0)

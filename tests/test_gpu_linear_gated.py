@@ -18,7 +18,7 @@ import pytest
 import oracle
 import datagen as dg
 import nnops_amd as na
-from gpu_util import dev, host, announce, norm_err
+from gpu_util import dev, host, announce, norm_err, oracle_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -55,18 +55,18 @@ GATE = {na.EP_SILU: oracle.ACT_SILU, na.EP_GELU: oracle.ACT_GELU, na.EP_RELU: or
 @pytest.mark.parametrize("gate", [na.EP_SILU, na.EP_GELU])
 def test_gated_ffn_config4_shape(M, gate):
     """The decode / prefill FFN: f16 X [M, 4096] x q4_1 [2 x 14336, 4096]
-    (gate rows, then value rows) with bias -> f16 [M, 14336]. M=1 checked in
-    full (the GEMV route), M=512 on sampled rows (the ring route)."""
+    (gate rows, then value rows) with bias -> f16 [M, 14336]; every output
+    checked, for M=1 (the GEMV route) and M=512 (the ring route)."""
     announce(f"gated ffn M={M} gate={gate}")
     K, N = 4096, 14336
     x = dg.normal(800 + M, (M, K)).astype(np.float16)
     blk = dg.q4_1_blocks(801, 2 * N, K)
     bias = (0.1 * dg.normal(802, (2 * N,))).astype(np.float16)
     got = run_linear(x, blk, 2 * N, gated=True, bias=bias, gate_activation=gate)
-    rows = (0, M) if M == 1 else (300, 304)
-    want = oracle.q4_1_linear(x, blk, 2 * N, rows=rows, w_round_f16=M > 2, gated=True, out_f16=True, bias=bias,
-                              gate_act=GATE[gate]).astype(np.float32)
-    err = norm_err(got[rows[0]:rows[1]], want)
+    want = oracle_rows(lambda r0, r1: oracle.q4_1_linear(x, blk, 2 * N, rows=(r0, r1), w_round_f16=M > 2, gated=True,
+                                                         out_f16=True, bias=bias, gate_act=GATE[gate]), M,
+                       band=4).astype(np.float32)
+    err = norm_err(got, want)
     assert err <= TOL, err
 
 

@@ -12,7 +12,7 @@ import pytest
 import oracle
 import datagen as dg
 import nnops_amd as na
-from gpu_util import dev, host, announce, norm_err
+from gpu_util import dev, host, announce, norm_err, oracle_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -124,29 +124,27 @@ def test_q4_1_f16_out_nnops_semantics(M):
 @pytest.mark.parametrize("M", [1, 512])
 def test_config4_full(M):
     """BASELINE config 4 at full size: K=4096, N=14336, f16 A ~ N(0,1), f32 out;
-    M=1 fully checked, M=512 on sampled rows."""
+    every output checked (the oracle in row bands over the host's cores)."""
     announce(f"config4 M={M}")
     K, N = 4096, 14336
     a = dg.normal(100 + M, (M, K)).astype(np.float16)
     blk = dg.q4_1_blocks(101, N, K)
     got = run_gpu(a, blk, N, trans_b=True)
-    rows = (0, M) if M <= 4 else (200, 216)
-    want = oracle.gemm_q4_1(a, blk, N, trans_b=True, rows=rows)
-    err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
+    want = oracle_rows(lambda r0, r1: oracle.gemm_q4_1(a, blk, N, trans_b=True, rows=(r0, r1))[r0:r1], M, band=4)
+    err = norm_err(got, want)
     assert err <= TOL, err
 
 
 def test_config4_kn_m512():
     """Config 4 with the [K][N/32] weight layout (blocks along N), M=512,
-    sampled rows."""
+    every output checked."""
     announce("config4 kn M=512")
     M, K, N = 512, 4096, 14336
     a = dg.normal(612, (M, K)).astype(np.float16)
     blk = dg.q4_1_blocks(613, K, N)
     got = run_gpu(a, blk, N, trans_b=False)
-    rows = (120, 136)
-    want = oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=rows)
-    err = norm_err(got[rows[0]:rows[1]], want[rows[0]:rows[1]])
+    want = oracle_rows(lambda r0, r1: oracle.gemm_q4_1(a, blk, N, trans_b=False, rows=(r0, r1))[r0:r1], M, band=4)
+    err = norm_err(got, want)
     assert err <= TOL, err
 
 

@@ -36,6 +36,42 @@ def _need(M, N, K, trans_b, **fields):
     return na.lib().nnops_hip_gemm_i8_workspace_size(C.byref(g))
 
 
+def test_noalloc_first_call_under_graph_capture():
+    """The entry point's first call in the process is made while a stream is
+    captured (its one-time scratch lookup then runs inside the capture): the
+    K-split plan (int32 partials in the scratch, then the reduce with the
+    float epilogue and add_to) replayed three times, C restored eagerly
+    between replays, each replay equal bit for bit to the workspace route."""
+    import torch
+    M, K, N = 333, 14336, 1024
+    assert _need(M, N, K, True, out_kind=na.OUT_S8, float_ep=1, add_to=1, act=na.ACT_GELU) > (1 << 20)
+    announce("noalloc under graph capture: 333x14336x1024 float epilogue, K split")
+    a = pitched(dg.act_s8(531, (M, K)), 14400)
+    w = dev(dg.ints(532, (N, K), -127, 127))
+    sb = dev(dg.uniform(533, (N,), 0.001, 0.01))
+    bias = dev(dg.ints(534, (N,), -5000, 5000, np.int32))
+    c0 = pitched(dg.ints(535, (M, N), -128, 127), 1040)
+    kw = dict(trans_b=True, bias=bias, out_kind=na.OUT_S8, s_a=0.02, s_b=sb, s_out=2.0, float_ep=True,
+              act=na.ACT_GELU, add_to=True)
+    want = c0.clone()
+    na.gemm_i8(a, w, want, **kw)
+    torch.cuda.synchronize()
+    want = host(want)
+    c = c0.clone()
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        na.gemm_i8(a, w, c, noalloc=True, stream=s.cuda_stream, **kw)
+    for r in range(3):
+        c.copy_(c0)                       # eager work between replays: the residual restored
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(c), want, err_msg=f"replay {r}")
+    assert np.unique(want).size > 50
+
+
 def test_noalloc_matches_workspace_route_two_calls():
     import torch
     # 1: config 5's Linear form (K split 4 ways: ~21.8 MB of int32 partials in
