@@ -913,35 +913,58 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         constexpr bool kWhole = BM * kWholeP <= NS * kStage && (BN % 128) == 0 && (BM * BN / 16) % (W * 64) == 0;
         constexpr int kSP = kWhole ? kWholeP : kPitch8;
         int8_t* stage8 = kWhole ? ring + wm0 * kSP + wn0 : ring + wave * (TM * kPitch8);
+        // Two instructions per element are dropped where the parameters
+        // allow: with Relu, only the rounding of values on the unclamped side
+        // of 0 reaches the output (the other side clamps to 0 whichever way it
+        // rounds), so the half-away addend is the column's constant
+        // +-0.5 (the sign of req) instead of copysign(0.5, x); and a zero
+        // output zero point needs no add.
+        auto requant = [&](auto relu_c, auto zp_c) {
+            constexpr bool kRelu = decltype(relu_c)::value;
+            constexpr bool kZp = decltype(zp_c)::value;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+            for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
-                const v4f sb = sbp[j][g];
-                float req[4];
-                int32_t lo[4], hi[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    req[e] = __fmul_rn(row_k, sb[e]);
-                    lo[e] = (relu && req[e] >= 0.0f) ? max(lo_i, 0) : lo_i;
-                    hi[e] = (relu && !(req[e] >= 0.0f)) ? min(hi_i, 0) : hi_i;
-                }
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-                    uint32_t q[4];
+                for (int g = 0; g < 4; ++g) {
+                    const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+                    const v4f sb = sbp[j][g];
+                    float req[4], half[4];
+                    int32_t lo[4], hi[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float x = __fmul_rn((float)acc[i][j][4 * g + e], req[e]);
-                        // round half away from zero: the conversion truncates as trunc() does
-                        const int32_t r = (int32_t)__fadd_rn(x, __builtin_copysignf(0.5f, x));
-                        q[e] = (uint32_t)(med3_i32(r, lo[e], hi[e]) + ep.zp_out);
+                        req[e] = __fmul_rn(row_k, sb[e]);
+                        lo[e] = (kRelu && req[e] >= 0.0f) ? max(lo_i, 0) : lo_i;
+                        hi[e] = (kRelu && !(req[e] >= 0.0f)) ? min(hi_i, 0) : hi_i;
+                        half[e] = req[e] >= 0.0f ? 0.5f : -0.5f;
                     }
-                    const uint32_t w = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
-                                       __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
-                    *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kSP + nl) = w;
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        uint32_t q[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float x = __fmul_rn((float)acc[i][j][4 * g + e], req[e]);
+                            // round half away from zero: the conversion truncates as trunc() does
+                            const float h = kRelu ? half[e] : __builtin_copysignf(0.5f, x);
+                            const int32_t r = (int32_t)__fadd_rn(x, h);
+                            q[e] = (uint32_t)(kZp ? med3_i32(r, lo[e], hi[e]) + ep.zp_out : med3_i32(r, lo[e], hi[e]));
+                        }
+                        const uint32_t w = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
+                                           __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
+                        *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kSP + nl) = w;
+                    }
                 }
             }
+        };
+        using TrueC = std::integral_constant<bool, true>;
+        using FalseC = std::integral_constant<bool, false>;
+        if (relu && ep.zp_out == 0) {
+            requant(TrueC{}, FalseC{});
+        } else if (relu) {
+            requant(TrueC{}, TrueC{});
+        } else if (ep.zp_out == 0) {
+            requant(FalseC{}, FalseC{});
+        } else {
+            requant(FalseC{}, TrueC{});
         }
         if constexpr (kWhole) {
             __syncthreads();
@@ -1268,8 +1291,9 @@ __device__ __forceinline__ void out4_store(const GemmI8Kern& p, const Out4& o, i
 // (compensation, bias, Relu, requant or the float epilogue, add_to). TPG
 // threads share a group of 4 consecutive columns of a row (N % 4 == 0), each
 // summing every TPG-th split with its loads in flight together, then combine
-// with lane shuffles; the first of them runs the output pass. TPG = 4 suits
-// many splits of a small output, TPG = 1 a few splits of a large one.
+// with lane shuffles; the first of them runs the output pass. TPG = 16 suits
+// many splits of a small output (each thread's loads in one round trip), TPG =
+// 1 a few splits of a large one.
 template <int TPG>
 __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk)
 {
@@ -1304,8 +1328,10 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
     if constexpr (TPG > 1) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            raw[e] += __shfl_xor(raw[e], 1);
-            raw[e] += __shfl_xor(raw[e], 2);
+#pragma unroll
+            for (int o = 1; o < TPG; o <<= 1) {
+                raw[e] += __shfl_xor(raw[e], o);
+            }
         }
     }
     if (!in || j != 0) {
@@ -1358,6 +1384,7 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit 
     const bool u8 = ep.out_kind == NNOPS_OUT_U8;
     const bool even = ep.round_even != 0;
     const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
+    const float inv_out = __fdiv_rn(1.0f, ep.s_out);
     uint32_t outw = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1389,7 +1416,7 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit 
             if constexpr (ADD && !PRE) {
                 f = __fadd_rn(f, res);
             }
-            q = requant_clamped(__fdiv_rn(f, ep.s_out), ep.zp_out, u8, even);
+            q = requant_clamped(div_by_fixed(f, ep.s_out, inv_out), ep.zp_out, u8, even);
         }
         outw |= ((uint32_t)q & 0xffu) << (8 * e);
     }
@@ -2295,7 +2322,7 @@ void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
         return;
     }
     if (sk.splits > 8) {
-        NNOPS_LAUNCH(gemm_i8_reduce<4>, dim3((unsigned)((groups * 4 + 255) / 256)), dim3(256), 0, s, k, sk);
+        NNOPS_LAUNCH(gemm_i8_reduce<16>, dim3((unsigned)((groups * 16 + 255) / 256)), dim3(256), 0, s, k, sk);
     } else {
         NNOPS_LAUNCH(gemm_i8_reduce<1>, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, k, sk);
     }

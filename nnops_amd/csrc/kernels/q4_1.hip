@@ -658,16 +658,24 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
 // pieces it needs have landed, so the decode ALU work overlaps the HBM stream
 // instead of following it (every wave of the launch is resident at once).
 // ---------------------------------------------------------------------------
-template <int MT, int R>
+//
+// GATED: Linear's gated form with its output pass p.fo fused. p.n = 2 p.fo.n
+// weight rows (gate rows, then value rows); a wave stages gate rows n0, n0 + 1
+// and value rows p.fo.n + n0, p.fo.n + n0 + 1 (two 5 KiB spans) and combines
+// its two outputs with fp_out_value, from the same f32 products the two-step
+// form stages, so the bits are the two-step form's.
+template <int MT, int R, bool GATED = false>
 __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
 {
     constexpr int kRow = 128 * 20;
     constexpr int C = (R * kRow + 1023) / 1024;      // DMA pieces per wave
+    static_assert(!GATED || R == 4, "gated: two gate and two value rows per wave");
     __shared__ __attribute__((aligned(16))) uint8_t stage[4][C * 1024];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * 4 + wave) * R;
-    if (n0 >= p.n) {
+    const int nout = GATED ? p.fo.n : p.n;              // outputs (gated: half the weight rows)
+    const int n0 = (blockIdx.x * 4 + wave) * (GATED ? R / 2 : R);
+    if (n0 >= nout) {
         return;
     }
     // A first: its loads retire before the DMA pieces queued behind them
@@ -691,13 +699,26 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
     }
     // every lane issues every piece (past the last row: a re-read of the
     // span's start), so the piece count, and the waits below, are static
-    const uint8_t* first = p.b + (int64_t)n0 * kRow;
-    const int valid = min(R, p.n - n0) * kRow;
+    if constexpr (GATED) {
+        // pieces 0-4: the gate rows' span, 5-9: the value rows' (2 x 2560 bytes each)
+        const uint8_t* span[2] = {p.b + (int64_t)n0 * kRow, p.b + (int64_t)(nout + n0) * kRow};
+        const int valid = min(R / 2, nout - n0) * kRow;
 #pragma unroll
-    for (int q = 0; q < C; ++q) {
-        const int off = q * 1024 + lane * 16;
-        __builtin_amdgcn_global_load_lds(NNOPS_GPTR(first + (off + 16 <= valid ? off : 0)),
-                                         NNOPS_LPTR(&stage[wave][q * 1024]), 16, 0, 2);
+        for (int q = 0; q < C; ++q) {
+            const int h = q < C / 2 ? 0 : 1;
+            const int off = (q - h * (C / 2)) * 1024 + lane * 16;
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(span[h] + (off + 16 <= valid ? off : 0)),
+                                             NNOPS_LPTR(&stage[wave][q * 1024]), 16, 0, 2);
+        }
+    } else {
+        const uint8_t* first = p.b + (int64_t)n0 * kRow;
+        const int valid = min(R, p.n - n0) * kRow;
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            const int off = q * 1024 + lane * 16;
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(first + (off + 16 <= valid ? off : 0)),
+                                             NNOPS_LPTR(&stage[wave][q * 1024]), 16, 0, 2);
+        }
     }
     const v2h one = __builtin_bit_cast(v2h, 0x3c003c00u);
     float asum[2][MT];
@@ -770,6 +791,23 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
             }
             acc[r][m] = v;
         }
+    }
+    if constexpr (GATED) {
+        // lanes (r, m) each finish one output: gate product acc[r], value acc[2 + r]
+        const FpOut& fo = p.fo;
+#pragma unroll
+        for (int r = 0; r < R / 2; ++r) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int n = n0 + r;
+                if (lane == r * MT + m && n < nout && m < p.m) {
+                    char* orow = static_cast<char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
+                    fp_out_store(fo, orow, n, fp_out_value(fo, acc[r][m], acc[R / 2 + r][m], fp_out_old(fo, orow, n),
+                                                           bias_at(fo, n), bias_at(fo, nout + n)));
+                }
+            }
+        }
+        return;
     }
     if (lane == 0) {
 #pragma unroll
@@ -3013,12 +3051,18 @@ extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsF
     if (g == nullptr || pass == nullptr) {
         return NNOPS_INVALID_ARGUMENT;
     }
-    // the blocks-along-K ring route only (f16 A past the GEMV and skinny
-    // shapes); anything else is the caller's two-step form
+    // the blocks-along-K ring route (f16 A past the GEMV and skinny shapes)
+    // and, gated, the pipelined GEMV (M <= 2, K = 4096, rows back to back);
+    // anything else is the caller's two-step form
     if (!g->trans_b || g->b_soa || !g->a_f16 || g->m <= 0 || g->n <= 0 || g->k <= 0 || g->m > INT32_MAX ||
-        g->n > INT32_MAX || g->k > INT32_MAX || g->a == nullptr || g->b == nullptr || use_gemv(*g) ||
-        skinny_ok(*g) || g->k % 64 != 0 || (g->lda % 8) != 0 || ((uintptr_t)g->a & 15) != 0 || g->lda < g->k ||
+        g->n > INT32_MAX || g->k > INT32_MAX || g->a == nullptr || g->b == nullptr || g->lda < g->k ||
         g->ldb_bytes < (g->k + 31) / 32 * 20 || (g->ldb_bytes & 3) || ((uintptr_t)g->b & 3)) {
+        return NNOPS_UNSUPPORTED;
+    }
+    const bool pipe_gemv = g->m <= 2 && g->k == 128 * 32 && g->ldb_bytes == 128 * 20 && ((uintptr_t)g->b & 15) == 0 &&
+                           (g->lda % 8) == 0 && ((uintptr_t)g->a & 15) == 0 && pass->gated && g->n % 2 == 0;
+    if (!pipe_gemv && (use_gemv(*g) || skinny_ok(*g) || g->k % 64 != 0 || (g->lda % 8) != 0 ||
+                       ((uintptr_t)g->a & 15) != 0)) {
         return NNOPS_UNSUPPORTED;
     }
     FpOut fo;
@@ -3047,6 +3091,16 @@ extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsF
     k.ldb = g->ldb_bytes;
     k.fo = fo;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (pipe_gemv) {
+        // two outputs per wave, four waves per workgroup
+        const unsigned rb = (unsigned)((pass->n + 7) / 8);
+        if (g->m == 1) {
+            NNOPS_LAUNCH((gemv_q4_1_pipe<1, 4, true>), dim3(rb), dim3(256), 0, s, k);
+        } else {
+            NNOPS_LAUNCH((gemv_q4_1_pipe<2, 4, true>), dim3(rb), dim3(256), 0, s, k);
+        }
+        return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+    }
     const int64_t tiles_m = (g->m + 127) / 128;
     const unsigned tiles = (unsigned)(tiles_m * ((pass->n + 127) / 128));
     NNOPS_LAUNCH((gemm_q4_1_ring<false, 4, 1, 8, true>), dim3(tiles), dim3(512), 0, s, k);

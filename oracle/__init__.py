@@ -82,6 +82,8 @@ def lib():
         _lib.orc_tanhf.restype = C.c_float
         _lib.orc_gelu_tanh.argtypes = [C.c_float]
         _lib.orc_gelu_tanh.restype = C.c_float
+        _lib.orc_markstein_mismatches.argtypes = [C.c_float, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]
+        _lib.orc_markstein_mismatches.restype = C.c_int64
         _lib.orc_f32_to_f16.argtypes = [C.c_float]
         _lib.orc_f32_to_f16.restype = C.c_uint16
         _lib.orc_f16_to_f32.argtypes = [C.c_uint16]

@@ -155,6 +155,31 @@ float orc_tanhf(float x)
     return copysignf(th, x);
 }
 
+/* Division by a fixed divisor as the HIP output passes evaluate it:
+ * y = RN(1/b) once, q0 = RN(a*y), r = fma(-q0, b, a) (exact), q = fma(r, y, q0).
+ * Markstein's theorem (IBM J. Res. Dev. 34(1), 1990: with y the correctly
+ * rounded reciprocal and q0 within an ulp of a/b, one such correction gives
+ * the correctly rounded quotient) says q = RN(a/b) barring overflow and
+ * underflow. Counts the a in [lo, hi) (float bit patterns, every `step`-th)
+ * where the sequence and IEEE division differ: the tests check that it is 0
+ * (corrected = 0 stops at q0, the plain reciprocal multiply, which differs). */
+int64_t orc_markstein_mismatches(float b, uint32_t lo, uint32_t hi, uint32_t step, int32_t corrected)
+{
+    volatile float one = 1.0f;
+    const float y = one / b;
+    int64_t bad = 0;
+    for (uint64_t u = lo; u < hi; u += step) {
+        const float a = bits_to_f32((uint32_t)u);
+        const float q0 = a * y;
+        const float r = fmaf(-q0, b, a);
+        const float q = corrected ? fmaf(r, y, q0) : q0;
+        if (f32_to_bits(q) != f32_to_bits(a / b)) {
+            ++bad;
+        }
+    }
+    return bad;
+}
+
 /* GELU, tanh approximation, with the reference's operation order
  * (simd_epilogue.hpp:76-79). */
 float orc_gelu_tanh(float x)

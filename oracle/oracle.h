@@ -81,6 +81,7 @@ int32_t orc_requant(int32_t acc, float req, int32_t zp, int32_t u8, int32_t roun
 float orc_requant_scale(float s_a, float s_b, float s_out);
 
 float orc_tanhf(float x);
+int64_t orc_markstein_mismatches(float b, uint32_t lo, uint32_t hi, uint32_t step, int32_t corrected);
 float orc_gelu_tanh(float x);
 
 uint16_t orc_f32_to_f16(float f);

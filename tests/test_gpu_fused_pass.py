@@ -1,5 +1,5 @@
-"""The Q4_1 ring GEMM with Linear's gated combine fused into the write-back
-(nnops_hip_gemm_q4_1_fused) against the two-step form it replaces
+"""The Q4_1 ring GEMM and the M <= 2 pipelined GEMV with Linear's gated
+combine fused into the write-back (nnops_hip_gemm_q4_1_fused) against the two-step form it replaces
 (nnops_hip_gemm_q4_1 into an f32 staging buffer, then
 nnops_hip_fp_output_pass): the same products and the same pass arithmetic, so
 the destinations must agree bit for bit. Covers gate activations, limit,
@@ -49,7 +49,7 @@ def _args(kw, M, n, out, bias, f16):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("M,K,N", [(70, 512, 520), (200, 256, 1000)])
+@pytest.mark.parametrize("M,K,N", [(70, 512, 520), (200, 256, 1000), (1, 4096, 1001), (2, 4096, 520)])
 @pytest.mark.parametrize("vi", range(len(VARIANTS)))
 def test_fused_pass_matches_two_step(f16, M, K, N, vi):
     import torch

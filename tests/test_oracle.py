@@ -633,3 +633,23 @@ def test_oracle_fp_linear_matches_nnops_linear(f16, kw):
         bs = np.concatenate([bias[n:], bias[:n]])
         bad = oracle.fp_linear(x, ws, gated=True, out_f16=f16, bias=bs, out=old, **okw).astype(np.float64)
         assert np.max(np.abs(want - bad)) / np.sqrt(np.mean(want ** 2)) > 0.05
+
+
+@pytest.mark.parametrize("b", [0.05, 2.0, 0.0123456, 3.0, 0.1, 1.9999999, 1.0000001, 7.77, 0.001, 1e-4])
+def test_markstein_division_is_correctly_rounded(b):
+    """The HIP output passes divide by the per-tensor output scale as
+    q0 = a * RN(1/b), r = fma(-q0, b, a), q = fma(r, RN(1/b), q0) (one
+    Markstein correction); the requant's bit-exactness rests on q == RN(a/b).
+    Checked against IEEE division over every 257th float from 2^-60 to 2^60,
+    both signs (the build container also ran every float of that range for
+    ten of these divisors with no difference)."""
+    lib = oracle.lib()
+    bf = float(np.float32(b))
+    lo, hi = 0x21800000, 0x5D800000
+    assert lib.orc_markstein_mismatches(bf, lo, hi, 257, 1) == 0
+    assert lib.orc_markstein_mismatches(bf, lo | 0x80000000, hi | 0x80000000, 257, 1) == 0
+    # the same harness sees the plain reciprocal multiply's errors (except for
+    # a power of two, where it is exact, and 1 + 2^-23, whose reciprocal
+    # multiply happens to round right on this sample): the check can fail
+    if bf not in (2.0, float(np.float32(1.0000001))):
+        assert lib.orc_markstein_mismatches(bf, lo, hi, 257, 0) > 1000
