@@ -592,13 +592,29 @@ struct BufRsrc {
 };
 #endif
 
-__device__ __forceinline__ BufRsrc buffer_rsrc(const void* base)
+__device__ __forceinline__ BufRsrc buffer_rsrc(const void* base, int bytes = 0x7fffffff)
 {
 #if __HIP_DEVICE_COMPILE__
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 #else
-    (void)base;
+    (void)base, (void)bytes;
     return BufRsrc{};
+#endif
+}
+
+// ds_read_b64_tr_b8: each 16-lane group reads 16 rows of 8 bytes (one address
+// per lane) and lane L of the group receives byte L & 7 of rows 2j + (L >> 3),
+// j = 0..7. With lane i addressing row k0 + (i >> 1), columns c0 + 8 (i & 1)
+// of a row-major byte tile, lane L receives column c0 + L at rows k0 .. k0 + 7:
+// a k-contiguous fragment of a tile stored n-contiguous.
+typedef int v2i __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2i lds_read_tr8(const int8_t* p)
+{
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(p));
+#else
+    (void)p;
+    return v2i{0, 0};
 #endif
 }
 
@@ -656,12 +672,18 @@ __device__ __forceinline__ void ring_coords(int tiles_m, int tiles_n, int& tm, i
 // a 16-byte lane fragment is 8 halves of v_mfma_f32_32x32x16_f16 as it is 16
 // int8 of v_mfma_i32_32x32x32_i8), the accumulators f32; RING_FP then writes
 // acc * s_a_scalar (alpha) and RING_PART the f32 partials' bits.
-template <int BM, int BN, int WM, int WN, int BK, int NS, int MODE, bool FLIP, bool F16 = false>
+//
+// TRB: B is [K,N] row-major (ldb its row pitch in bytes), staged as it lies: a
+// stage holds BK k rows of BN bytes, 16-byte chunk c of row r in slot
+// c ^ swzb(r), and the B fragments are built by lds_read_tr8 (two per
+// fragment: k rows +0..7 and +8..15 of the lane's 16). No transposed copy.
+template <int BM, int BN, int WM, int WN, int BK, int NS, int MODE, bool FLIP, bool F16 = false, bool TRB = false>
 __global__ __launch_bounds__(WM * WN * 64)
-__attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+__attribute__((amdgpu_waves_per_eu((WM * WN + 3) / 4, (WM * WN + 3) / 4)))
 void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 {
     static_assert(!F16 || MODE == RING_FP || MODE == RING_PART, "f16 operands: fp or partial outputs");
+    static_assert(!TRB || !F16, "row-major B: int8 operands");
     constexpr int W = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
@@ -675,6 +697,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     constexpr int kPitch8 = TN + 16;              // staged byte row pitch: 2-way bank conflicts at most
     static_assert(BK == 64 || BK == 128, "stage depth");
     static_assert(QA * W * RPI == BM && QB * W * RPI == BN, "rows per stage");
+    // TRB staging: 1024 / BN k rows per load instruction, CPRB chunks per row
+    constexpr int RPIB = TRB ? 1024 / BN : 1;
+    constexpr int CPRB = BN / 16;
+    static_assert(!TRB || (1024 % BN == 0 && BN >= 64 && (BK / RPIB) == QB * W), "row-major B staging");
     static_assert(FM * 32 == TM && FN * 32 == TN, "wave tile");
     static_assert(W * TM * kPitch8 <= NS * kStage, "byte staging fits the ring");
     static_assert(NS >= 2 && (NS - 1) * L < 64, "vmcnt range");
@@ -696,11 +722,20 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     // bank groups (BK = 64: 4 rows per 256 bytes, swz = (r >> 2) & 3;
     // BK = 128: 2 rows per 256 bytes, swz = (r >> 1) & 7).
     auto swz = [](int r) { return BK == 64 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
+    // TRB: a transposed read serves 8 k rows x two 16-byte chunks per 32
+    // lanes; rows sharing a 256-byte bank row (256 / BN of them) keep their
+    // slots, and the bank rows' 8 slot pairs differ in slot bits 1.., so the
+    // 16 chunks fall in 16 distinct 16-byte bank groups.
+    auto swzb = [](int r) { return ((r / (BN >= 256 ? 1 : 256 / BN)) & (CPRB / 2 - 1)) << 1; };
 
     // Descriptors over this tile's row panels from this split's first k; rows
     // past M/N are clamped to the last row (computed, never stored).
     const BufRsrc rsa = buffer_rsrc(p.a + (int64_t)m0 * p.lda + (int64_t)kt0 * BK);
-    const BufRsrc rsb = buffer_rsrc(p.b + (int64_t)n0 * p.ldb + (int64_t)kt0 * BK);
+    // TRB: the descriptor ends at B's last byte, so chunks past column N of
+    // the last k row read 0 (earlier rows' read the next row: never stored)
+    const BufRsrc rsb = TRB ? buffer_rsrc(p.b + (int64_t)kt0 * BK * p.ldb + n0,
+                                          (int)((int64_t)(p.k - kt0 * BK - 1) * p.ldb + (p.n - n0)))
+                            : buffer_rsrc(p.b + (int64_t)n0 * p.ldb + (int64_t)kt0 * BK);
     int a_off[QA], b_off[QB];
 #pragma unroll
     for (int q = 0; q < QA; ++q) {
@@ -710,10 +745,17 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     }
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
-        const int r = (wave * QB + q) * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ swz(r);
-        b_off[q] = min(r, p.n - 1 - n0) * (int)p.ldb + c * 16;
+        if constexpr (TRB) {
+            const int r = (wave * QB + q) * RPIB + lane / CPRB;
+            const int c = (lane % CPRB) ^ swzb(r);
+            b_off[q] = r * (int)p.ldb + c * 16;
+        } else {
+            const int r = (wave * QB + q) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ swz(r);
+            b_off[q] = min(r, p.n - 1 - n0) * (int)p.ldb + c * 16;
+        }
     }
+    const int b_step = TRB ? BK * (int)p.ldb : BK;     // bytes from one stage's B rows to the next's
     auto issue = [&](int s) {
         int8_t* base = ring + (s % NS) * kStage;
 #pragma unroll
@@ -722,7 +764,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
 #pragma unroll
         for (int q = 0; q < QB; ++q) {
-            buffer_load_lds16(rsb, base + BM * BK + (wave * QB + q) * 1024, b_off[q], s * BK);
+            buffer_load_lds16(rsb, base + BM * BK + (wave * QB + q) * 1024, b_off[q], s * b_step);
         }
     };
 
@@ -768,15 +810,37 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         const int c = (2 * ks + (lane >> 5)) ^ swz(row);
         return *reinterpret_cast<const v4i*>(st + row * BK + c * 16);
     };
+    // TRB: the B fragment of columns col .. col + 31 at slice ks from the
+    // row-major stage: lane (group g, index i) addresses k row 32 ks + 16 (g
+    // >> 1) + (i >> 1) (+8 for the second read), columns col + 16 (g & 1) +
+    // 8 (i & 1); lane l receives column col + (l & 31) at k 32 ks + 16 (l >>
+    // 5) + 0..15, the layout of the A fragments.
+    const int tr_k = 16 * (lane >> 5) + ((lane & 15) >> 1);
+    const int tr_c = 16 * ((lane >> 4) & 1) + 8 * (lane & 1);
+    auto frag_tr = [&](const int8_t* stb, int col, int ks) {
+        const int k0 = 32 * ks + tr_k;
+        const int c = col + tr_c;
+        const v2i lo = lds_read_tr8(stb + k0 * BN + (((c >> 4) ^ swzb(k0)) << 4) + (c & 15));
+        const v2i hi = lds_read_tr8(stb + (k0 + 8) * BN + (((c >> 4) ^ swzb(k0 + 8)) << 4) + (c & 15));
+        return v4i{lo.x, lo.y, hi.x, hi.y};
+    };
     auto read_frags = [&](const int8_t* st, int ks, v4i (&fa)[FM], v4i (&fb)[FN]) {
-        fb[0] = frag(st + BM * BK, wn0 + fr, ks);
+        if constexpr (TRB) {
+            fb[0] = frag_tr(st + BM * BK, wn0, ks);
+        } else {
+            fb[0] = frag(st + BM * BK, wn0 + fr, ks);
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             fa[i] = frag(st, wm0 + i * 32 + fr, ks);
         }
 #pragma unroll
         for (int j = 1; j < FN; ++j) {
-            fb[j] = frag(st + BM * BK, wn0 + j * 32 + fr, ks);
+            if constexpr (TRB) {
+                fb[j] = frag_tr(st + BM * BK, wn0 + j * 32, ks);
+            } else {
+                fb[j] = frag(st + BM * BK, wn0 + j * 32 + fr, ks);
+            }
         }
     };
     auto mfma_all = [&](v4i (&fa)[FM], const v4i (&fb)[FN]) {
@@ -803,12 +867,18 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     // One fragment read after each of the first FM + FN MFMAs, so every read
     // has part of a slice of matrix work to land before it is needed; with
     // loads, they go on the last MFMAs of the slice.
+    constexpr int NR = FM + (TRB ? 2 : 1) * FN;     // LDS reads per slice
     auto schedule = [&](bool loads) {
 #pragma unroll
         for (int q = 0; q < FM * FN; ++q) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (q < FM + FN) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (q < NR) {
+                if (q + 1 < FM * FN) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                } else {
+                    // the last MFMA takes the reads left over
+                    __builtin_amdgcn_sched_group_barrier(0x100, NR - FM * FN + 1, 0);
+                }
             }
             if (loads && q >= FM * FN - L && q - (FM * FN - L) < L) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -2032,6 +2102,7 @@ struct RingPlan {
     int bk = 64;            // k bytes per staged row (128 when K allows)
     int splits = 0;         // K splits (1: no split)
     int mode = -1;          // RING_S8 / RING_S32 / RING_PART
+    bool trb = false;       // B is [K,N] row-major, read in place (TRB)
 };
 
 // Column GEMV plan ([K,N] B consumed in place, M <= 16).
@@ -2100,12 +2171,21 @@ inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 
 // fused output modes need row-uniform parameters, no zero-point terms,
 // half-away rounding, 16-byte-aligned tables and destination, and no split;
 // everything else writes raw partials and runs gemm_i8_reduce.
-RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb)
+// trb: B is the caller's [K,N] (row pitch ldb), read in place (its whole
+// span within 32-bit buffer offsets). small_tiles: grids of fewer than 32
+// tiles take 64 x 64 tiles of 4 waves instead (config 1, 128 x 1024 x 1024:
+// 32 workgroups in place of 4).
+RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                   bool trb = false, bool small_tiles = false)
 {
     RingPlan r;
     if (g.m <= 16 || g.k % 64 != 0 || g.n % 4 != 0 || g.m < 64 || !aligned16(a, lda) || !aligned16(b, ldb)) {
         return r;
     }
+    if (trb && (g.k * ldb + g.n >= (int64_t)INT32_MAX || ldb < g.n)) {
+        return r;
+    }
+    r.trb = trb;
     if (g.m > 256 && g.m <= 384 && g.k % 128 == 0) {
         // two 192-row tiles: twice the tiles of one 384-row tile, so half the
         // K splits (and half the partial-sum traffic) fill the CUs
@@ -2119,7 +2199,10 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     } else {
         r.bm = 256; r.bn = 256;
     }
-    if ((int64_t)r.bm * lda >= (int64_t)INT32_MAX || (int64_t)r.bn * ldb >= (int64_t)INT32_MAX) {
+    if (small_tiles && ((g.m + r.bm - 1) / r.bm) * ((g.n + r.bn - 1) / r.bn) < 32) {
+        r.bm = 64; r.bn = 64;
+    }
+    if ((int64_t)r.bm * lda >= (int64_t)INT32_MAX || (!trb && (int64_t)r.bn * ldb >= (int64_t)INT32_MAX)) {
         r = RingPlan{};
         return r;
     }
@@ -2130,6 +2213,8 @@ RingPlan plan_ring(const NnopsGemmI8Args& g, const int8_t* a, int64_t lda, const
     // gains less from splitting than the reduce launch costs (config 1,
     // 128x1024x1024 s32: 10.5 + 3.9 us in two splits, 12.4 us unsplit)
     r.splits = kt < 16 ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(256 / tiles, kt / (512 / r.bk)));
+    // (the 64 x 64 tiles of config 1 split 4 ways: 4.2 us ring + 3.4 us
+    // reduce against 6.4 us unsplit)
     const bool compensate = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0 || g.zp_b != nullptr ||
                             g.zp_b_scalar != 0;
     const bool tables16 = ((uintptr_t)g.bias % 16 == 0) && ((uintptr_t)g.s_b % 16 == 0);
@@ -2173,12 +2258,20 @@ WsPlan plan_workspace(const NnopsGemmI8Args& g)
         w.total = off;
         return w;
     }
-    if (!g.trans_b) {
+    // a [K,N] B goes to the ring in place when it takes it and no column
+    // sums of B are needed (they are summed over the staged copy's rows)
+    const bool need_rb = g.a_u8 || g.zp_a != nullptr || g.zp_a_scalar != 0;
+    if (!g.trans_b && !need_rb) {
+        w.ring = plan_ring(g, a, lda, b, ldb, true, true);
+    }
+    if (!g.trans_b && w.ring.mode < 0) {
         w.b_t = off; off += align_up((size_t)g.n * (size_t)w.kp);
         b = nullptr;
         ldb = w.kp;
     }
-    w.ring = plan_ring(g, a, lda, b, ldb);
+    if (!w.ring.trb) {
+        w.ring = plan_ring(g, a, lda, b, ldb, false, true);
+    }
     if (w.ring.mode == RING_PART) {
         w.part = off; off += align_up((size_t)w.ring.splits * (size_t)g.m * (size_t)g.n * 4);
     }
@@ -2215,10 +2308,29 @@ void launch_gemm(const GemmI8Kern& k, bool aligned, bool fullk, int epi, hipStre
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int NS, bool F16 = false>
-void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, hipStream_t s)
+void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool flip, bool trb, hipStream_t s)
 {
     const unsigned blocks = (unsigned)(((k.m + BM - 1) / BM) * ((k.n + BN - 1) / BN) * sk.splits);
     const dim3 block(WM * WN * 64);
+    if (trb) {
+        // [K,N] B in place; plain A (no u8 flip: its column sums need the copy)
+        if constexpr (!F16) {
+            if (mode == RING_S8) {
+                NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S8, false, false, true>), dim3(blocks), block,
+                             0, s, k, sk);
+            } else if (mode == RING_S32) {
+                NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_S32, false, false, true>), dim3(blocks),
+                             block, 0, s, k, sk);
+            } else if (mode == RING_FP) {
+                NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_FP, false, false, true>), dim3(blocks), block,
+                             0, s, k, sk);
+            } else {
+                NNOPS_LAUNCH((gemm_i8_ring<BM, BN, WM, WN, BK, NS, RING_PART, false, false, true>), dim3(blocks),
+                             block, 0, s, k, sk);
+            }
+        }
+        return;
+    }
     if constexpr (F16) {
         (void)flip;
         if (mode == RING_FP) {
@@ -2247,18 +2359,21 @@ void launch_ring_bk(const GemmI8Kern& k, const RingSplit& sk, int mode, bool fli
 // 64-byte rows, which is what limits a CU's load rate) in 2 slots when K
 // allows, else 64-byte rows in 4 slots.
 template <int BM, int BN, int WM, int WN, bool F16 = false>
-void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode, bool flip, hipStream_t s)
+void launch_ring_cfg(const GemmI8Kern& k, const RingSplit& sk, int bk, int mode, bool flip, bool trb, hipStream_t s)
 {
     if (bk == 128) {
         // three stage slots where the LDS holds them (config 5's 192x128 tiles:
-        // 33.7 -> 32.9 us), two for the 256x256 tile
-        if constexpr ((BM + BN) * 128 * 3 <= 160 * 1024 && BM + BN < 512) {
-            launch_ring_bk<BM, BN, WM, WN, 128, 3, F16>(k, sk, mode, flip, s);
+        // 33.7 -> 32.9 us), two for the 256x256 tile; the 64 x 64 tiles of
+        // small grids keep 8 stages in flight (their latency is the call's)
+        if constexpr (BM + BN <= 128) {
+            launch_ring_bk<BM, BN, WM, WN, 128, 8, F16>(k, sk, mode, flip, trb, s);
+        } else if constexpr ((BM + BN) * 128 * 3 <= 160 * 1024 && BM + BN < 512) {
+            launch_ring_bk<BM, BN, WM, WN, 128, 3, F16>(k, sk, mode, flip, trb, s);
         } else {
-            launch_ring_bk<BM, BN, WM, WN, 128, 2, F16>(k, sk, mode, flip, s);
+            launch_ring_bk<BM, BN, WM, WN, 128, 2, F16>(k, sk, mode, flip, trb, s);
         }
     } else if constexpr (BM % (16 * WM * WN) == 0 && BN % (16 * WM * WN) == 0) {
-        launch_ring_bk<BM, BN, WM, WN, 64, 4, F16>(k, sk, mode, flip, s);
+        launch_ring_bk<BM, BN, WM, WN, 64, 4, F16>(k, sk, mode, flip, trb, s);
     }
 }
 
@@ -2378,15 +2493,19 @@ void launch_ring(const GemmI8Kern& k, const RingPlan& r, int32_t* part, hipStrea
     sk.part = part;
     const bool flip = k.a_xor != 0u;
     if (r.bm == 384) {
-        launch_ring_cfg<384, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<384, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, r.trb, s);
     } else if (r.bm == 192) {
-        launch_ring_cfg<192, 128, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<192, 128, 2, 4, F16>(k, sk, r.bk, r.mode, flip, r.trb, s);
     } else if (r.bm == 128) {
-        launch_ring_cfg<128, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<128, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, r.trb, s);
+    } else if (r.bm == 64) {
+        if constexpr (!F16) {
+            launch_ring_cfg<64, 64, 2, 2>(k, sk, r.bk, r.mode, flip, r.trb, s);
+        }
     } else if (r.bn == 128) {
-        launch_ring_cfg<256, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<256, 128, 4, 2, F16>(k, sk, r.bk, r.mode, flip, r.trb, s);
     } else {
-        launch_ring_cfg<256, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, s);
+        launch_ring_cfg<256, 256, 2, 4, F16>(k, sk, r.bk, r.mode, flip, r.trb, s);
     }
     if (r.mode == RING_PART) {
         if constexpr (F16) {
@@ -2538,8 +2657,8 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
         k.a = static_cast<const int8_t*>(g->a);
         k.lda = g->lda;
     }
-    if (w.kn.cpl != 0) {
-        k.b = g->b;               // [K,N], consumed in place by the column GEMV
+    if (w.kn.cpl != 0 || w.ring.trb) {
+        k.b = g->b;               // [K,N], consumed in place by the column GEMV or the TRB ring
         k.ldb = g->ldb;
     } else if (!g->trans_b) {
         int8_t* bt = reinterpret_cast<int8_t*>(ws + w.b_t);

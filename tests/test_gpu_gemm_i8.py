@@ -86,6 +86,9 @@ SHAPES = [
     # [K,N] B staged by the 16-byte tiled transpose: partial 256-row and
     # 64-column tiles, and K % 16 != 0 (the zero-filled rows K..Kp-1)
     (64, 992, 1040), (130, 1040, 1008), (48, 1000, 1040),
+    # [K,N] B read in place by the ring (transposed LDS reads): N past the last
+    # 16-byte chunk, 64-byte stages (K % 128 != 0), 64 x 64 tiles of small grids
+    (200, 1024, 252), (96, 640, 1000), (64, 256, 200), (128, 1024, 1024),
 ]
 
 

@@ -111,17 +111,18 @@ def test_noalloc_matches_workspace_route_two_calls():
 
 
 def test_noalloc_rejects_a_plan_beyond_the_scratch():
-    # a raw [K,N] weight at config 5's shape is staged transposed (58.7 MB)
+    # a raw [K,N] weight at config 5's shape with an A zero point (the
+    # compensation needs B's column sums, so B is staged transposed: 58.7 MB)
     # beside the partials: more than the scratch holds, rejected before any launch
     import torch
     M, K, N = 333, 14336, 4096
-    assert _need(M, N, K, False, out_kind=na.OUT_S8, float_ep=1, add_to=1) > LIMIT
+    assert _need(M, N, K, False, out_kind=na.OUT_S8, float_ep=1, add_to=1, zp_a_scalar=3) > LIMIT
     announce("noalloc rejection")
     a = torch.zeros((M, K), dtype=torch.int8, device="cuda")
     b = torch.zeros((K, N), dtype=torch.int8, device="cuda")
     c = torch.full((M, N), 7, dtype=torch.int8, device="cuda")
-    rc = na.gemm_i8(a, b, c, trans_b=False, out_kind=na.OUT_S8, float_ep=True, add_to=True, noalloc=True,
-                    check=False)
+    rc = na.gemm_i8(a, b, c, trans_b=False, out_kind=na.OUT_S8, float_ep=True, add_to=True, zp_a=3,
+                    noalloc=True, check=False)
     torch.cuda.synchronize()
     assert rc == na.OUT_OF_MEMORY
     assert bool((c == 7).all())
