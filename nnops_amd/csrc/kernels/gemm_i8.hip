@@ -1805,6 +1805,154 @@ __device__ __forceinline__ void transpose4x4_bytes(uint32_t r0, uint32_t r1, uin
     col[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM over a [K,N] B in place, M <= 16 (A rows padded to 16):
+// v_mfma_i32_16x16x64_i8 with each B fragment built by two transposed LDS
+// reads (lds_read_tr8) from k rows staged as they lie in memory. A workgroup
+// of 4 waves owns a group of 16 CB columns and one of sk.splits K ranges;
+// wave w streams its own contiguous run of 64-row steps (16 CB bytes per
+// row, whole cache lines, in 1 KiB DMA instructions) through an NSW-slot
+// ring of its own, with the step's A fragments (16 bytes per lane, from L2)
+// loaded beside it. The waves meet in LDS and the workgroup
+// writes its int32 partials [split][M][N]; gemm_i8_reduce sums the splits
+// and runs the output pass.
+// ---------------------------------------------------------------------------
+template <int NSW, int CB>
+__global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk, int groups)
+{
+    constexpr int CW = 16 * CB;             // columns per workgroup: CB blocks of 16
+    constexpr int STEP = 64 * CW;           // bytes per 64-row step
+    constexpr int Q = STEP / 1024;          // DMA instructions per step
+    constexpr int RPQ = 1024 / CW;          // rows per DMA instruction
+    constexpr int L = Q + 1;                // vector-memory ops per step: the DMA + 1 A load
+    static_assert(CB == 8 || CB == 16, "128- or 256-byte row segments");
+    static_assert(NSW >= 1 && (NSW - 1) * L < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) int8_t ring[4][NSW][STEP];
+    static_assert(3 * CB * 64 * 16 <= 4 * NSW * STEP, "the waves' partial tiles fit the ring");
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cg = blockIdx.x % groups, sp = blockIdx.x / groups;
+    const int n0 = cg * CW;
+    const int T = p.k / 64;
+    const int s0 = (int)((int64_t)T * sp / sk.splits), s1 = (int)((int64_t)T * (sp + 1) / sk.splits);
+    const int w0 = s0 + (s1 - s0) * wave / 4, w1 = s0 + (s1 - s0) * (wave + 1) / 4;
+    const int nst = w1 - w0;
+
+    // slot of 16-byte chunk c in k row r: the transposed reads of 32 lanes
+    // (rows r0..r0+7 and r0+16..r0+23 of one chunk) fall in 16 distinct
+    // 16-byte bank groups (128-byte rows: two rows per 256-byte bank row)
+    auto swz = [](int r) {
+        return CB == 8 ? ((((r >> 1) & 3) << 1) | ((r >> 4) & 1)) : (((r & 7) << 1) | ((r >> 4) & 1));
+    };
+    // the descriptor ends at B's last byte: chunks past column N of the last
+    // row read 0 (earlier rows' read the next row: never stored)
+    const BufRsrc rsb = buffer_rsrc(p.b + n0, (int)((int64_t)(p.k - 1) * p.ldb + (p.n - n0)));
+    int b_off[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int r = q * RPQ + lane / CB;
+        b_off[q] = r * (int)p.ldb + (((lane % CB) ^ swz(r)) << 4);
+    }
+    const int arow = lane & 15;
+    const int8_t* a_row = p.a + (int64_t)min(arow, p.m - 1) * p.lda;
+    const int kq = 16 * (lane >> 4);
+    v4i fa[NSW];
+    auto issue = [&](int st, int u) {
+        int8_t* dst = ring[wave][u];
+        fa[u] = *reinterpret_cast<const v4i*>(a_row + st * 64 + kq);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            buffer_load_lds16<2>(rsb, dst + q * 1024, b_off[q], st * 64 * (int)p.ldb);
+        }
+    };
+    // B fragment of column block cb (16 columns) from a staged step: lane
+    // (group g, index i) reads k row 16 g + (i >> 1) (+8), columns 16 cb +
+    // 8 (i & 1); lane l receives column 16 cb + (l & 15) at k 16 g + 0..15
+    const int tr_k = 16 * (lane >> 4) + ((lane & 15) >> 1);
+    const int tr_b = 8 * (lane & 1);
+    v4i acc[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        acc[cb] = v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < NSW; ++u) {
+        if (u < nst) {
+            issue(w0 + u, u);
+        }
+    }
+    for (int t = 0; t < nst; t += NSW) {
+#pragma unroll
+        for (int u = 0; u < NSW; ++u) {
+            if (t + u < nst) {
+                const int ahead = min(nst - 1 - (t + u), NSW - 1);
+                if (ahead <= 0) {
+                    wait_vmcnt<0>();
+                } else if (NSW >= 2 && ahead == 1) {
+                    wait_vmcnt<(NSW >= 2 ? L : 0)>();
+                } else if (NSW >= 3 && ahead == 2) {
+                    wait_vmcnt<(NSW >= 3 ? 2 * L : 0)>();
+                } else {
+                    wait_vmcnt<(NSW >= 4 ? 3 * L : 0)>();
+                }
+                asm volatile("" ::: "memory");
+                const int8_t* st = ring[wave][u];
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    // the column block is chunk cb of the staged row
+                    const int k0 = tr_k;
+                    const v2i lo = lds_read_tr8(st + k0 * CW + ((cb ^ swz(k0)) << 4) + tr_b);
+                    const v2i hi = lds_read_tr8(st + (k0 + 8) * CW + ((cb ^ swz(k0 + 8)) << 4) + tr_b);
+                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u], v4i{lo.x, lo.y, hi.x, hi.y}, acc[cb], 0,
+                                                                   0, 0);
+                }
+                // the slot's reads are done before the next step's DMA reuses it
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                asm volatile("" ::: "memory");
+                if (t + u + NSW < nst) {
+                    issue(w0 + t + u + NSW, u);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    v4i* red = reinterpret_cast<v4i*>(&ring[0][0][0]);
+    if (wave > 0) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            red[((wave - 1) * CB + cb) * 64 + lane] = acc[cb];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+    // 16x16 layout: lane holds column (lane & 15) of the block, rows 4 (lane >> 4) + r;
+    // one K range: the output pass here, else the partials for gemm_i8_reduce
+    int32_t* part = sk.part + (int64_t)sp * p.m * p.n;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        v4i v = acc[cb] + red[(0 * CB + cb) * 64 + lane] + red[(1 * CB + cb) * 64 + lane] +
+                red[(2 * CB + cb) * 64 + lane];
+        const int n = n0 + 16 * cb + (lane & 15);
+        if (n < p.n) {
+            const EpiCol c = epi_col(p.ep, n);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * (lane >> 4) + r;
+                if (m < p.m) {
+                    if (sk.splits == 1) {
+                        epi_store(p.ep, epi_row(p.ep, m), c, v[r], static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes,
+                                  n);
+                    } else {
+                        part[(int64_t)m * p.n + n] = v[r];
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int MT, int CPL, int W, int U>
 __global__ __launch_bounds__(W * 64) void gemv_i8_kn(GemmI8Kern p, RingSplit sk, KnSplit ks)
 {
@@ -2110,6 +2258,7 @@ struct KnPlan {
     int cpl = 0;            // columns per lane (0: not taken)
     int w = 0;              // waves per workgroup
     int chunks = 0, splits = 0;
+    bool tr = false;        // gemv_i8_kn_tr (chunks: its 128-column groups)
 };
 
 inline int kn_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
@@ -2120,6 +2269,8 @@ struct WsPlan {
     RingPlan ring;
     KnPlan kn;
 };
+
+inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 0) && (ld % 16 == 0); }
 
 // M <= 16 with a [K,N] B: 16-byte (M <= 2) or 4-byte column groups per lane,
 // K % 16 == 0, dword-aligned A rows (scalar loads), no term that needs the
@@ -2133,6 +2284,25 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
     }
     // (8 columns per lane with 32 rows in flight measured slower for
     // 4 <= M <= 16: 17.1 / 32.1 us against 14.8 / 28.3 at M = 4 / 16)
+    // 3 <= M <= 16, 64-row steps, 16-byte rows: the transposed-read MFMA
+    // kernel, K split so about two workgroups per CU stream at once
+    // (measured at config 3, N = 11008, call totals with the reduce: 128-byte
+    // row segments and ~512 workgroups 15.2 / 16.6 us at M = 4 / 16; 256-byte
+    // segments 18.7 / 20.0 (256 workgroups) and 21.8 / 27.0 (512); no K split
+    // (86 workgroups) 37.8 / 38.5; at M = 1..2 the column GEMV stays faster,
+    // 13.8 against 14.9 us)
+    if (g.m >= 3 && g.k % 64 == 0 && g.n % 4 == 0 && aligned16(g.b, g.ldb) &&
+        aligned16(static_cast<const int8_t*>(g.a), g.lda) && g.k * g.ldb + g.n < (int64_t)INT32_MAX) {
+        r.tr = true;
+        r.cpl = 8;          // column blocks of 16 per workgroup
+        r.w = 4;
+        r.chunks = (int)((g.n + 127) / 128);
+        r.splits = (int)std::max<int64_t>(1, std::min<int64_t>(512 / r.chunks, g.k / 64 / 4));
+        if ((int64_t)r.splits * g.m * g.n * 4 >= INT32_MAX) {
+            return KnPlan{};
+        }
+        return r;
+    }
     const int cpl = g.m <= 2 ? 16 : 4;
     if (g.n % cpl != 0 || g.n % 4 != 0 || ((uintptr_t)g.b % cpl) != 0 || (g.ldb % cpl) != 0 ||
         ((uintptr_t)g.a % 4) != 0 || (g.lda % 4) != 0) {
@@ -2161,7 +2331,6 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
     return r;
 }
 
-inline bool aligned16(const void* p, int64_t ld) { return ((uintptr_t)p % 16 == 0) && (ld % 16 == 0); }
 
 // The ring kernel needs 64-byte k steps, 16-byte-aligned k-contiguous rows,
 // N % 4 == 0 (int32 groups), and 32-bit buffer offsets within a row panel.
@@ -2449,6 +2618,14 @@ void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t 
     sk.splits = r.splits;
     sk.kt_per = 0;
     sk.part = part;
+    if (r.tr) {
+        NNOPS_LAUNCH((gemv_i8_kn_tr<2, 8>), dim3((unsigned)(r.chunks * r.splits)), dim3(256), 0, s, k, sk,
+                     r.chunks);
+        if (r.splits > 1) {
+            launch_reduce(k, sk, s);
+        }
+        return;
+    }
     KnSplit ks;
     ks.chunks = r.chunks;
     switch (k.m) {
