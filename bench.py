@@ -910,17 +910,60 @@ def cpu_baseline(seconds):
                       + f", {cores} threads"}
 
 
+# the kernels of each bench line whose HBM traffic per call the committed
+# counter summary holds (profiles/traffic_counters.txt)
+LINE_TRAFFIC = {
+    "cfg1_s32_128x1024x1024": ["gemm_i8_ring_cfg1"],
+    "cfg3_int8_gemv_m1_kn_s32": ["gemv_i8_kn_cfg3_m1", "gemm_i8_reduce_cfg3_m1"],
+    "cfg3_int8_gemv_m1_nk_s32": ["gemv_i8_rows_cfg3_m1"],
+    "cfg3_int8_gemv_m4_nk_s32": ["gemv_i8_rows_cfg3_m4"],
+    "cfg3_int8_gemv_m16_nk_s32": ["gemv_i8_lds_cfg3_m16"],
+    "cfg3_int8_gemv_m1_kn_prepacked": ["gemv_i8_rows_cfg3_m1"],
+    "cfg3_int8_gemv_m16_kn_prepacked": ["gemv_i8_lds_cfg3_m16"],
+    "cfg4_q4_1_gemv_m1": ["gemv_q4_1_pipe_cfg4_m1"],
+    "cfg4_q4_1_gemm_m512": ["gemm_q4_1_ring_cfg4_m512"],
+    "cfg4_q4_1_gemv_m1_kn": ["gemv_q4_1_kn_dma_cfg4_m1"],
+    "cfg4_q4_1_gemm_m512_kn": ["gemm_q4_1_kn_ring_cfg4_m512"],
+    "cfg4_q4_1_m8_decode_batch": ["gemv_q4_1_skinny_cfg4_m8"],
+    "cfg4_q4_1_gemm_m512_f32a": ["gemm_q4_1_f32_cfg4_m512"],
+    "cfg4_q4_1_gemv_m1_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m1_packed"],
+    "cfg4_q4_1_gemm_m512_kn_prepacked": ["gemm_q4_1_kn_ring_cfg4_m512_packed"],
+    "cfg4_q4_1_m8_decode_batch_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m8_packed"],
+    "gated_ffn_swiglu_m1": ["gemv_q4_1_pipe_gated_m1"],
+    "gated_ffn_swiglu_m512": ["gemm_q4_1_ring_gated_m512"],
+    "cfg5_s8_addto_gelu": ["gemm_i8_ring_cfg5", "gemm_i8_reduce_cfg5"],
+    "dq_gemm_4096_f16_out": ["gemm_i8_ring_dq_f16"],
+    "fp_act_matmul_4096_f16": ["quantize_linear_4096", "gemm_i8_ring_dq_f16"],
+    "dense_f16_gemm_4096": ["gemm_f16_ring_4096"],
+    "dense_f16_gemv_m1_14336x4096": ["gemv_fp_nk_f16_m1"],
+    "quantize_linear_4096x4096_f16": ["quantize_linear_4096"],
+    "dequantize_linear_4096x4096_f16": ["dequantize_linear_4096"],
+}
+
+
+def line_traffic(key):
+    """HBM megabytes per call of a bench line's kernels from the counter
+    summary, or None where it holds no figure for them."""
+    keys = LINE_TRAFFIC.get(key)
+    if not keys:
+        return None
+    vals = [measured_traffic(k) for k in keys]
+    return None if any(v is None for v in vals) else round(sum(vals) / 1e6, 2)
+
+
 def summarize(secondary):
     """One compact entry per secondary line: step time, fraction of the
-    bounding roofline, and the CPU baseline (value, unit, threads) or null
-    with the reason."""
+    bounding roofline, the HBM megabytes per call its kernels moved (counter
+    summary; null where none) and the CPU baseline (value, unit, threads) or
+    the reason it is absent."""
     out = {}
     for key, r in secondary.items():
         frac = next((r[k] for k in ("frac_hbm", "frac_int8_mfma", "frac_f16_mfma", "frac_f32_mfma", "frac_mfma")
                      if k in r), None)
         bound = next((b for k, b in (("frac_hbm", "hbm"), ("frac_int8_mfma", "int8"), ("frac_f16_mfma", "f16"),
                                      ("frac_f32_mfma", "f32"), ("frac_mfma", "mfma")) if k in r), None)
-        e = {"us": round(r["us"], 2), "frac": None if frac is None else round(frac, 3), "of": bound}
+        e = {"us": round(r["us"], 2), "frac": None if frac is None else round(frac, 3), "of": bound,
+             "traffic_mb": line_traffic(key)}
         cb = r.get("cpu_baseline")
         if cb is None:
             e["cpu"] = None
