@@ -618,6 +618,21 @@ __device__ __forceinline__ v2i lds_read_tr8(const int8_t* p)
 #endif
 }
 
+// Exchanges x's lanes 32..63 with y's lanes 0..31 (v_permlane32_swap): with
+// x = a word of lane half h = 0 / 1 and y the same for another word, lane
+// l < 32 ends with (x, y) = (x_l, x_{l+32}) and lane l + 32 with
+// (y_l, y_{l+32}).
+__device__ __forceinline__ void swap_half_waves(uint32_t& x, uint32_t& y)
+{
+#if __HIP_DEVICE_COMPILE__
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    x = r[0];
+    y = r[1];
+#else
+    (void)x, (void)y;
+#endif
+}
+
 // 16 bytes per lane from base + voff + soff into LDS at lds + 16 * lane.
 // AUX: the cache policy bits (2: non-temporal, for data read once).
 template <int AUX = 0>
@@ -768,40 +783,8 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     };
 
-    // Accumulators (transposed layout); the fused modes start from bias[n].
+    // Accumulators (transposed layout), initialised after the first stage loads.
     std::conditional_t<F16, v16f, v16i> acc[FM][FN];
-#pragma unroll
-    for (int j = 0; j < FN && F16; ++j) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            acc[i][j] = std::conditional_t<F16, v16f, v16i>{0};
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < FN && !F16; ++j) {
-        int32_t b0[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v4i bv = v4i{0, 0, 0, 0};
-            if constexpr (MODE != RING_PART) {
-                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-                if (p.ep.bias != nullptr && n < p.n) {
-                    bv = *reinterpret_cast<const v4i*>(p.ep.bias + n);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                b0[4 * g + e] = bv[e];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[i][j][r] = b0[r];
-            }
-        }
-    }
 
     // Fragment reads of slice ks: row (lane & 31) of each 32-row fragment,
     // logical chunk 2 ks + (lane >> 5).
@@ -894,6 +877,41 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             issue(s);
         }
     }
+    // Accumulators (transposed layout); the fused modes start from bias[n],
+    // whose loads go out after the first stages' so their latencies overlap.
+#pragma unroll
+    for (int j = 0; j < FN && F16; ++j) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            acc[i][j] = std::conditional_t<F16, v16f, v16i>{0};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < FN && !F16; ++j) {
+        int32_t b0[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i bv = v4i{0, 0, 0, 0};
+            if constexpr (MODE != RING_PART) {
+                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                if (p.ep.bias != nullptr && n < p.n) {
+                    bv = *reinterpret_cast<const v4i*>(p.ep.bias + n);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b0[4 * g + e] = bv[e];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = b0[r];
+            }
+        }
+    }
+
     if (kt >= NS - 1) {
         wait_vmcnt<(NS - 2) * L>();   // stage 0 landed, stages 1..NS-2 may be in flight
     } else {
@@ -989,14 +1007,20 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         // rounds), so the half-away addend is the column's constant
         // +-0.5 (the sign of req) instead of copysign(0.5, x); and a zero
         // output zero point needs no add.
+        // Each lane packs one row's 4 columns per register group g (columns
+        // 8g + 4h .. +3, h = lane / 32); a permlane32 swap of groups (0, 2)
+        // and (1, 3) then gives lane h the row's 16 contiguous columns 16h ..
+        // 16h + 15 of the fragment, written to the stage as one 16-byte LDS
+        // store (four 4-byte stores with 2-way bank conflicts before: the
+        // largest part of the output pass).
         auto requant = [&](auto relu_c, auto zp_c) {
             constexpr bool kRelu = decltype(relu_c)::value;
             constexpr bool kZp = decltype(zp_c)::value;
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
+                uint32_t w[FM][4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
                     const v4f sb = sbp[j][g];
                     float req[4], half[4];
                     int32_t lo[4], hi[4];
@@ -1018,10 +1042,16 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                             const int32_t r = (int32_t)__fadd_rn(x, h);
                             q[e] = (uint32_t)(kZp ? med3_i32(r, lo[e], hi[e]) + ep.zp_out : med3_i32(r, lo[e], hi[e]));
                         }
-                        const uint32_t w = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
-                                           __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
-                        *reinterpret_cast<uint32_t*>(stage8 + (i * 32 + (lane & 31)) * kSP + nl) = w;
+                        w[i][g] = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) |
+                                  __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu);
                     }
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    swap_half_waves(w[i][0], w[i][2]);
+                    swap_half_waves(w[i][1], w[i][3]);
+                    const v4i v = v4i{(int)w[i][0], (int)w[i][2], (int)w[i][1], (int)w[i][3]};
+                    *reinterpret_cast<v4i*>(stage8 + (i * 32 + (lane & 31)) * kSP + j * 32 + 16 * (lane >> 5)) = v;
                 }
             }
         };
@@ -1246,7 +1276,14 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             }
         }
     } else {
-        // int32 groups straight from the accumulators (host-checked: N % 4 == 0)
+        // int32 groups (host-checked: N % 4 == 0, 16-byte-aligned rows),
+        // staged through the ring so every store is a 16-byte piece of a
+        // whole tile row: 32 lanes write one row's BN * 4 bytes. Straight
+        // from the accumulator layout a store instruction would touch 32 rows
+        // with 32 bytes each, which writes at a fraction of the HBM rate
+        // (config 5's 22 MB of partials: 9.6 us against 3 us for the same
+        // bytes in row pieces). Passes of PI fragment rows per wave row keep
+        // the staged slab within the ring.
         const int32_t floor_v = (MODE == RING_S32 && ep.act == NNOPS_ACT_RELU) ? 0 : INT32_MIN;
         char* cbase;
         int64_t ld;
@@ -1257,33 +1294,54 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             cbase = reinterpret_cast<char*>(sk.part + (int64_t)sp * p.m * p.n);
             ld = (int64_t)p.n * 4;
         }
+        constexpr int kRowB = BN * 4 + 16;            // staged row pitch: rows 16 bytes apart in the banks
+        constexpr int PI = (WM * FM * 32 * kRowB <= NS * kStage) ? FM
+                           : (FM % 2 == 0 && WM * (FM / 2) * 32 * kRowB <= NS * kStage) ? FM / 2 : 1;
+        static_assert(WM * PI * 32 * kRowB <= NS * kStage, "int32 staging fits the ring");
+        constexpr int kCPR = BN / 4;                  // 16-byte chunks per tile row
+        constexpr int kRows = WM * PI * 32;           // staged rows per pass
+        static_assert((kRows * kCPR) % (W * 64) == 0, "whole chunks per thread");
+        const int wmi = wave / WN;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int m = m0 + wm0 + i * 32 + (lane & 31);
-            if (m >= p.m) {
-                continue;
-            }
-            char* crow = cbase + (int64_t)m * ld;
+        for (int pass = 0; pass < FM / PI; ++pass) {
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
+            for (int ii = 0; ii < PI; ++ii) {
+                const int i = pass * PI + ii;
+                const int sr = (wmi * PI + ii) * 32 + (lane & 31);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-                    if (n < p.n) {
+                for (int j = 0; j < FN; ++j) {
+                    v16i a;
+                    if constexpr (F16) {
+                        a = __builtin_bit_cast(v16i, acc[i][j]);
+                    } else {
+                        a = acc[i][j];
+                    }
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
                         v4i v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            if constexpr (F16) {
-                                // the f32 bits (bit-cast as a whole vector: a cast of
-                                // one subscripted element read element 0 here)
-                                v[e] = __builtin_bit_cast(v16i, acc[i][j])[4 * g + e];
-                            } else {
-                                v[e] = max(acc[i][j][4 * g + e], floor_v);
-                            }
+                            v[e] = F16 ? a[4 * g + e] : max(a[4 * g + e], floor_v);
                         }
-                        *reinterpret_cast<v4i*>(crow + (int64_t)n * 4) = v;
+                        const int col = wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                        *reinterpret_cast<v4i*>(ring + sr * kRowB + col * 4) = v;
                     }
                 }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kRows * kCPR / (W * 64); ++q) {
+                const int idx = (q * W + wave) * 64 + lane;
+                const int sr = idx / kCPR, cc = idx % kCPR;
+                const int m = m0 + (sr / (PI * 32)) * TM + (pass * PI + (sr / 32) % PI) * 32 + (sr & 31);
+                const int n = n0 + cc * 4;
+                const v4i v = *reinterpret_cast<const v4i*>(ring + sr * kRowB + cc * 16);
+                if (m < p.m && n < p.n) {
+                    *reinterpret_cast<v4i*>(cbase + (int64_t)m * ld + (int64_t)n * 4) = v;
+                }
+            }
+            if (pass + 1 < FM / PI) {
+                __syncthreads();
             }
         }
     }
