@@ -722,6 +722,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     static_assert(MODE == RING_PART || !FLIP, "u8 A needs the compensating output pass");
 
     __shared__ __attribute__((aligned(1024))) int8_t ring[NS * kStage];
+    // the output pass's per-column scales, staged at the start (their load
+    // latency then hides behind the first stage's) where the LDS holds them
+    constexpr bool kSbl = (MODE == RING_S8 || MODE == RING_FP) && NS * kStage + BN * 4 <= 160 * 1024;
+    __shared__ __attribute__((aligned(16))) float sbl[kSbl ? BN : 4];
 
     int tm, tn, sp;
     ring_coords(ceil_div(p.m, BM), ceil_div(p.n, BN), tm, tn, sp);
@@ -912,6 +916,16 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     }
 
+    if constexpr (kSbl) {
+        if (threadIdx.x < BN / 4) {
+            const int n = n0 + 4 * (int)threadIdx.x;
+            v4f v = v4f{p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar};
+            if (p.ep.s_b != nullptr && n < p.n) {
+                v = *reinterpret_cast<const v4f*>(p.ep.s_b + n);
+            }
+            *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = v;
+        }
+    }
     if (kt >= NS - 1) {
         wait_vmcnt<(NS - 2) * L>();   // stage 0 landed, stages 1..NS-2 may be in flight
     } else {
@@ -960,11 +974,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     for (int t = 0; t < kt; ++t) {
         step(t);
     }
-    // The output pass's per-column scales: a lane's 8 loads issued together
-    // with one wait, rather than one load and wait per 4-column group (8
-    // serial cache round trips). They are not issued during the last stage:
-    // that would raise the loop's register peak past the 256 of two waves
-    // per SIMD.
+    // The output pass's per-column scales: from the LDS copy staged at the
+    // start, or else a lane's 8 loads issued together with one wait. They are
+    // not read during the last stage: that would raise the loop's register
+    // peak past the 256 of two waves per SIMD.
     const EpiParams& ep = p.ep;
     v4f sbp[FN][4];
     if constexpr (MODE == RING_S8 || MODE == RING_FP) {
@@ -972,10 +985,14 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         for (int j = 0; j < FN; ++j) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-                sbp[j][g] = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
-                if (ep.s_b != nullptr && n < p.n) {
-                    sbp[j][g] = *reinterpret_cast<const v4f*>(ep.s_b + n);
+                const int nl = wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                if constexpr (kSbl) {
+                    sbp[j][g] = *reinterpret_cast<const v4f*>(&sbl[nl]);
+                } else {
+                    sbp[j][g] = v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
+                    if (ep.s_b != nullptr && n0 + nl < p.n) {
+                        sbp[j][g] = *reinterpret_cast<const v4f*>(ep.s_b + n0 + nl);
+                    }
                 }
             }
         }
