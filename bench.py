@@ -420,7 +420,8 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
                   a_f32=False):
     """Config 4's GEMM; trans_b=False times the literal [K][N/32] layout
     (blocks along N) instead of the GGUF/Linear [N][K/32] one; a_f32 an f32
-    A (nnops computes that product in f32: the f32 MFMA GEMM)."""
+    A (nnops computes that product in f32; here the split-f16 ring past the
+    skinny rows, blocks along K)."""
     import numpy as np
     a_h = dg.normal(403, (M, K)).astype("float32" if a_f32 else "float16")
     b_h = dg.q4_1_blocks(404, N, K) if trans_b else dg.q4_1_blocks(404, K, N)
@@ -444,7 +445,13 @@ def q41_gemm_case(torch, dg, na, stream, steps, warmup, M=512, K=4096, N=14336, 
     out = {"tflops": tf, "us": t["mean_ms"] * 1e3,
            "M": M, "K": K, "N": N, "weight_layout": "[N][K/32 blocks]" if trans_b else "[K][N/32 blocks]",
            "timing": t["timing"]}
-    if a_f32:
+    if a_f32 and trans_b and M > 48 and K % 64 == 0:
+        # the split-f16 ring: A as two f16 parts, two f16 products per decoded
+        # weight on the f16 matrix cores (the fraction counts the algorithmic
+        # 2 M N K flops against the f16 peak)
+        out["a"] = "f32 (split into two f16 parts)"
+        out["frac_f16_mfma"] = tf / PEAK_F16_TFLOPS
+    elif a_f32:
         out["a"] = "f32"
         out["frac_f32_mfma"] = tf / PEAK_F32_TFLOPS
     else:
@@ -925,7 +932,7 @@ LINE_TRAFFIC = {
     "cfg4_q4_1_gemv_m1_kn": ["gemv_q4_1_kn_dma_cfg4_m1"],
     "cfg4_q4_1_gemm_m512_kn": ["gemm_q4_1_kn_ring_cfg4_m512"],
     "cfg4_q4_1_m8_decode_batch": ["gemv_q4_1_skinny_cfg4_m8"],
-    "cfg4_q4_1_gemm_m512_f32a": ["gemm_q4_1_f32_cfg4_m512"],
+    "cfg4_q4_1_gemm_m512_f32a": ["split_a_f32_cfg4_m512", "gemm_q4_1_ring_split_cfg4_m512"],
     "cfg4_q4_1_gemv_m1_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m1_packed"],
     "cfg4_q4_1_gemm_m512_kn_prepacked": ["gemm_q4_1_kn_ring_cfg4_m512_packed"],
     "cfg4_q4_1_m8_decode_batch_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m8_packed"],

@@ -61,6 +61,8 @@ struct Q41Kern {
     const uint32_t* bdm; // SoA d|m plane, block column j at j * ldbdm (prepacked blocks along N)
     int64_t ldbdm;       // u32 elements
     FpOut fo;            // the fused gated combine (gemm_q4_1_ring with GATED)
+    const float* row_scale;  // SPLIT ring: [M] power-of-two factor of each row of A
+    int64_t plane;           // SPLIT ring: bytes from the hi plane of A to the lo plane
 };
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
@@ -2105,6 +2107,53 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_f32(Q41Kern p)
     }
 }
 
+
+// f32 A for the SPLIT ring: two f16 planes with a = (hi + lo) 2^e per row.
+// The row's largest magnitude is scaled into [2^14, 2^15) (a power of two,
+// exact), hi = RN_f16(a 2^-e) and lo = RN_f16(a 2^-e - hi) (the difference is
+// exact in f32), so every value within 2^-28 of the row's largest keeps 22
+// significant bits. One workgroup per row; e is clamped so 2^e and 2^-e are
+// normal floats, and a row without a finite nonzero maximum keeps e = 0 (its
+// infinities and NaNs pass into hi).
+__global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, int k, _Float16* hi, _Float16* lo,
+                                                   float* row_scale)
+{
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const float* row = a + (int64_t)m * lda;
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < k; i += 256) {
+        mx = fmaxf(mx, __builtin_fabsf(row[i]));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = mx;
+    }
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.402823466e38f) {
+        // the exponent of mx (a subnormal one counts as -127: clamped below)
+        const int ex = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 127;
+        e = min(max(ex - 14, -126), 113);
+    }
+    const float down = __uint_as_float((uint32_t)(127 - e) << 23);    // 2^-e
+    if (threadIdx.x == 0) {
+        row_scale[m] = __uint_as_float((uint32_t)(127 + e) << 23);    // 2^e
+    }
+    _Float16* h_row = hi + (int64_t)m * k;
+    _Float16* l_row = lo + (int64_t)m * k;
+    for (int i = threadIdx.x; i < k; i += 256) {
+        const float x = row[i] * down;
+        const _Float16 h = (_Float16)x;
+        h_row[i] = h;
+        l_row[i] = (_Float16)(x - (float)h);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // MFMA GEMM, f16 A, B blocks along K ([N][K/32], 2 blocks = 40 bytes per row
 // per 64-k stage), K % 64 == 0. 128 x 256 tiles, WM x WN waves (the launch
@@ -2148,17 +2197,19 @@ __device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v
 // activation -- measured slower than the separate pass: 108 against 98 us at
 // 512 x 14336 x 4096, the pass's arithmetic then running with the matrix
 // cores idle; the gated form saves the larger staging: 196 -> 184 us.)
-template <bool OUT16, int NS, int WM, int WN = 4, bool GATED = false>
+template <bool OUT16, int NS, int WM, int WN = 4, bool GATED = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 {
     static_assert(!GATED || (WM == 1 && WN == 8), "gated: one wave per 32 columns, halves 4 waves apart");
+    static_assert(!SPLIT || (!GATED && WM == 1), "split A: one wave row");
     constexpr int W = WM * WN;                      // waves: WM along M x WN along N
-    constexpr int QA = 16 / W, QB = 16 / W;         // 1 KiB pieces per wave per stage
+    constexpr int AP = SPLIT ? 2 : 1;               // planes of A (SPLIT: hi and lo f16 parts)
+    constexpr int QA = 16 * AP / W, QB = 16 / W;    // 1 KiB pieces per wave per stage
     constexpr int L = QA + QB;
     static_assert(NS >= 3 && (NS - 2) * L < 64, "stages");
     constexpr int BM = 128, BN = 256;
     constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int kA = BM * 128, kB = BN * 64, kStage = kA + kB;
+    constexpr int kA = AP * BM * 128, kB = BN * 64, kStage = kA + kB;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
 
     const int tiles_m = (p.m + BM - 1) / BM;
@@ -2184,9 +2235,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
     int a_off[QA], b_off[QB];
 #pragma unroll
     for (int i = 0; i < QA; ++i) {
+        // SPLIT: staged rows 128..255 are the lo plane's rows 0..127
         const int ra = 8 * (QA * wave + i) + (lane >> 3);
         const int ca = (lane & 7) ^ ((ra >> 1) & 7);
-        a_off[i] = min(ra, p.m - 1 - m0) * (int)p.lda * 2 + ca * 16;
+        a_off[i] = min(ra & (BM - 1), p.m - 1 - m0) * (int)p.lda * 2 + ca * 16 + (ra >= BM ? (int)p.plane : 0);
     }
 #pragma unroll
     for (int i = 0; i < QB; ++i) {
@@ -2217,7 +2269,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
     // wn0 + 32 j + (lane & 31); k values 16 ks + 8 (lane >> 5) .. + 7
     const int fr = lane & 31, kh = lane >> 5;
     auto a_frag = [&](const uint8_t* st, int i, int ks) {
-        const int r = wm0 + i * 32 + fr;
+        const int r = (i >= FM ? BM : 0) + wm0 + (i % FM) * 32 + fr;
         const int c = (2 * ks + kh) ^ ((r >> 1) & 7);
         return *reinterpret_cast<const v8h*>(st + r * 128 + c * 16);
     };
@@ -2267,10 +2319,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
     // Within a step the fragments of the next slice are read and decoded
     // while the matrix cores run this one (B for both slices of a block at
     // once; two register sets, alternating).
-    v8h fa0[FM], fb0[FN], fa1[FM], fb1[FN], fb2[FN], fb3[FN];
-    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[FM]) {
+    v8h fa0[AP * FM], fb0[FN], fa1[AP * FM], fb1[FN], fb2[FN], fb3[FN];
+    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[AP * FM]) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < AP * FM; ++i) {
             fa[i] = a_frag(st, i, ks);
         }
     };
@@ -2280,12 +2332,17 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
             b_frag2(st, j, blk, lo[j], hi[j]);
         }
     };
-    auto mfma_slice = [&](const v8h (&fa)[FM], const v8h (&fb)[FN]) {
+    // SPLIT: the hi parts' products first, then the lo parts' into the same
+    // accumulators (FM * FN independent products apart)
+    auto mfma_slice = [&](const v8h (&fa)[AP * FM], const v8h (&fb)[FN]) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+        for (int h = 0; h < AP; ++h) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[h * FM + i], fb[j], acc[i][j], 0, 0, 0);
+                }
             }
         }
     };
@@ -2372,10 +2429,12 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < p.m) {
+                    // SPLIT: the row's power-of-two factor (exact)
+                    const float v = SPLIT ? acc[i][j][r] * p.row_scale[m] : acc[i][j][r];
                     if constexpr (OUT16) {
-                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)acc[i][j][r];
+                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
                     } else {
-                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = acc[i][j][r];
+                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
                     }
                 }
             }
@@ -2791,6 +2850,21 @@ inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
 }
 
 
+// f32 A past the skinny and GEMV shapes, blocks along K, K % 64 == 0: split
+// into two f16 planes in the workspace (split_a_f32) and run the SPLIT ring
+// (two f16 MFMAs per decoded weight fragment) instead of the f32 MFMA GEMM
+// (config 4's shape at M = 512: 555 us on the f32 matrix cores).
+inline bool split_ok(const NnopsGemmQ41Args& g)
+{
+    return !g.a_f16 && g.trans_b && !g.b_soa && g.k % 64 == 0 && !skinny_ok(g) && !use_gemv(g) &&
+           4 * g.m * g.k < INT32_MAX && 32 * g.ldb_bytes < INT32_MAX;
+}
+
+inline size_t split_ws_bytes(const NnopsGemmQ41Args& g)
+{
+    return align_up((size_t)g.m * (size_t)g.k * 4) + align_up((size_t)g.m * 4);
+}
+
 // the prepacked planes' block-column pitches: nibbles in bytes, d|m in dwords
 inline int64_t prepack_q41_nib_pitch(int64_t k) { return (k + 7) / 8 * 128; }
 inline int64_t prepack_q41_dm_pitch(int64_t k) { return (k + 63) / 64 * 64; }
@@ -2802,6 +2876,9 @@ using namespace nnops_amd;
 
 extern "C" size_t nnops_hip_gemm_q4_1_workspace_size(const NnopsGemmQ41Args* g)
 {
+    if (g != nullptr && split_ok(*g)) {
+        return split_ws_bytes(*g);
+    }
     if (g == nullptr || g->trans_b || !use_gemv(*g) || bcm_ok(*g)) {
         return 0;
     }
@@ -2998,6 +3075,26 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                 NNOPS_LAUNCH((gemv_q4_1_bcm<8, 8, 2>), dim3((unsigned)nbn), dim3(512), 0, s, kk);
             }
             m0 += mt;
+        }
+    } else if (split_ok(*g)) {
+        if (((uintptr_t)workspace & 15) != 0) {
+            return NNOPS_INVALID_ARGUMENT;
+        }
+        _Float16* hi = static_cast<_Float16*>(workspace);
+        _Float16* lo = hi + (int64_t)g->m * g->k;
+        float* rs = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up((size_t)g->m * (size_t)g->k * 4));
+        NNOPS_LAUNCH(split_a_f32, dim3((unsigned)g->m), dim3(256), 0, s, static_cast<const float*>(g->a), g->lda,
+                     (int)g->k, hi, lo, rs);
+        Q41Kern kk = k;
+        kk.a = hi;
+        kk.lda = g->k;
+        kk.plane = g->m * g->k * 2;
+        kk.row_scale = rs;
+        const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
+        if (k.out_f16) {
+            NNOPS_LAUNCH((gemm_q4_1_ring<true, 3, 1, 8, false, true>), dim3(tiles), dim3(512), 0, s, kk);
+        } else {
+            NNOPS_LAUNCH((gemm_q4_1_ring<false, 3, 1, 8, false, true>), dim3(tiles), dim3(512), 0, s, kk);
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

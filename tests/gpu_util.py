@@ -32,6 +32,17 @@ def announce(msg):
     sys.stdout.flush()
 
 
+def q41_f16_weights(M, K, f16, trans_b=True):
+    """Whether the Q4_1 route for M x K decodes its weights to f16 (the oracle's
+    w_round_f16): f16 A past M = 2, and f32 A on the split-f16 ring (blocks
+    along K, K % 64 == 0, past the GEMV rows M <= 16 and the skinny rows M <=
+    48 with K % 256 == 0)."""
+    if f16:
+        return M > 2
+    skinny = 3 <= M <= 48 and K % 256 == 0
+    return trans_b and K % 64 == 0 and M > 16 and not skinny
+
+
 def norm_err(got, want):
     """max |got - want| / max(|want|, rms(want)), elementwise: a relative error
     that stays meaningful at outputs that cancel to ~0 (the tolerance metric of

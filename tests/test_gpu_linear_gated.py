@@ -7,7 +7,8 @@ Bar: the Q4_1 tolerance (BASELINE: 2e-3) as a normalized error,
 max_i |g_i - w_i| / max(|w_i|, rms(w)), for f32 and f16 destinations (an f16
 rounding flip is 2^-10 of the value). Past M = 2 an f16 X takes the ring GEMM,
 which decodes the weight to f16 as nnops' packed route does for half operands
-(its small-M route decodes in f32); the oracle follows (w_round_f16)."""
+(its small-M route decodes in f32), and so does an f32 X past the skinny
+rows (the split-f16 ring); the oracle follows (w_round_f16, q41_f16_weights)."""
 from __future__ import annotations
 
 import math
@@ -18,7 +19,7 @@ import pytest
 import oracle
 import datagen as dg
 import nnops_amd as na
-from gpu_util import dev, host, announce, norm_err, oracle_rows
+from gpu_util import dev, host, announce, norm_err, oracle_rows, q41_f16_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -91,7 +92,8 @@ def test_gated_variants(f16, M, K, N2, kw):
     bias = dg.normal(N2 + 1, (N2,)).astype(dt)
     old = dg.normal(N2 + 2, (M, N2 // 2)).astype(dt) if kw.get("add_to") else None
     got = run_linear(x, blk, N2, gated=True, bias=bias, old=old, **kw)
-    want = oracle.q4_1_linear(x, blk, N2, w_round_f16=f16 and M > 2, gated=True, out_f16=f16, bias=bias, out=old,
+    want = oracle.q4_1_linear(x, blk, N2, w_round_f16=q41_f16_weights(M, K, f16), gated=True, out_f16=f16, bias=bias,
+                              out=old,
                               gate_act=GATE[kw["gate_activation"]], gate_alpha=kw.get("gate_alpha", 1.0),
                               gate_beta=kw.get("gate_beta", 0.0), gate_limit=kw.get("gate_limit", math.inf),
                               act={None: oracle.ACT_NONE, na.EP_RELU: oracle.ACT_RELU,
@@ -126,7 +128,8 @@ def test_q4_1_linear_bias_epilogue_residual(f16, M, K, N, kw):
            na.EP_RELU: oracle.ACT_RELU, na.EP_SIGMOID: oracle.ACT_SIGMOID}[kw.get("act")]
     active = act != oracle.ACT_NONE or "min_clip" in kw
     pre = kw.get("add_to", False) and (kw.get("residual_pre_activation", False) or not active)
-    want = oracle.q4_1_linear(x, blk, N, w_round_f16=f16 and M > 2, out_f16=f16, bias=bias, out=old, act=act,
+    want = oracle.q4_1_linear(x, blk, N, w_round_f16=q41_f16_weights(M, K, f16), out_f16=f16, bias=bias, out=old,
+                              act=act,
                               min_clip=kw.get("min_clip", -math.inf), max_clip=kw.get("max_clip", math.inf),
                               add_to=kw.get("add_to", False), residual_pre=pre).astype(np.float32)
     err = norm_err(got, want)
@@ -185,7 +188,7 @@ def test_q4_1_matmul_alpha_beta(f16, M, trans_b, kw):
         ins.append(na.tensor(dev(bias)))
     assert op.compute([na.tensor(y)], ins) == na.OK
     torch.cuda.synchronize()
-    acc = oracle.gemm_q4_1(x, blk, N, trans_b=trans_b, w_round_f16=f16 and M > 2)
+    acc = oracle.gemm_q4_1(x, blk, N, trans_b=trans_b, w_round_f16=q41_f16_weights(M, K, f16, trans_b))
     want = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, act=MM_ACT[kw.get("act")],
                               matmul_order=True, alpha=kw["alpha"], beta=kw["beta"],
                               residual_pre=kw.get("residual_pre", False)).astype(np.float32)

@@ -92,20 +92,57 @@ def test_q4_1_skinny_f32_a(M, K, N):
     assert norm_err(got, want) <= 1e-4
 
 
+def split_route(M, K, trans_b):
+    """The f32-A shapes that take the split-f16 ring: blocks along K, K % 64
+    == 0, past the GEMV (M <= 16) and skinny (M <= 48, K % 256 == 0) rows."""
+    skinny = 3 <= M <= 48 and K % 256 == 0
+    return trans_b and K % 64 == 0 and M > 16 and not skinny
+
+
 @pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40)])
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_q4_1_f32_a_gemm(M, K, N, trans_b):
     """f32 A past the GEMV rows: the f32 MFMA GEMM (ragged M, N and K tiles)
     against the f64-accumulated oracle within 1e-4 (normalized; an f32 sum of
     K = 4096 products carries ~1e-5); M = 16 is the GEMV loop's last row
-    count."""
+    count. The split-f16 ring (blocks along K, K % 64 == 0) decodes each
+    weight to f16 as the f16-A routes do: within 1e-4 of the oracle with the
+    weights so rounded (A's two f16 parts carry 22 bits), within BASELINE's
+    2e-3 of the exact one."""
     announce(f"q4_1 f32 A GEMM {M}x{K}x{N} trans_b={trans_b}")
     seed = 3 * M + K + N + int(trans_b)
     a = dg.normal(seed, (M, K))
     blk = dg.q4_1_blocks(seed + 1, N, K) if trans_b else dg.q4_1_blocks(seed + 2, K, N)
     got = run_gpu(a, blk, N, trans_b=trans_b)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
-    assert norm_err(got, want) <= 1e-4
+    if split_route(M, K, trans_b):
+        assert norm_err(got, oracle.gemm_q4_1(a, blk, N, trans_b=trans_b, w_round_f16=True)) <= 1e-4
+        assert norm_err(got, want) <= TOL
+    else:
+        assert norm_err(got, want) <= 1e-4
+
+
+def test_q4_1_f32_a_split_row_scales():
+    """The split-f16 ring's per-row power-of-two scaling: rows far outside
+    f16's range (1e6 and 1e-7 times N(0,1), one row with a single 1e5 among
+    N(0,1), an all-zero row, a row of 2^-130 subnormals) stay within 1e-4 of
+    the oracle with f16-rounded weights, row by row."""
+    import torch
+    M, K, N = 64, 512, 256
+    announce(f"q4_1 f32 A split scales {M}x{K}x{N}")
+    a = dg.normal(77, (M, K))
+    a[0] *= 1e6
+    a[1] *= 1e-7
+    a[2, 5] = 1e5
+    a[3] = 0.0
+    a[4] = np.float32(2.0 ** -130) * np.sign(a[4])
+    blk = dg.q4_1_blocks(78, N, K)
+    assert split_route(M, K, True)
+    got = run_gpu(a, blk, N, trans_b=True)
+    want = oracle.gemm_q4_1(a, blk, N, trans_b=True, w_round_f16=True)
+    assert np.all(got[3] == 0.0)
+    for m in (0, 1, 2, 4, 5, 63):
+        assert norm_err(got[m], want[m]) <= 1e-4, m
 
 
 @pytest.mark.parametrize("M", [1, 40])
