@@ -935,7 +935,7 @@ LINE_TRAFFIC = {
     "cfg4_q4_1_gemm_m512_f32a": ["split_a_f32_cfg4_m512", "gemm_q4_1_ring_split_cfg4_m512"],
     "cfg4_q4_1_gemv_m1_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m1_packed"],
     "cfg4_q4_1_gemm_m512_kn_prepacked": ["gemm_q4_1_kn_ring_cfg4_m512_packed"],
-    "cfg4_q4_1_m8_decode_batch_kn_prepacked": ["gemv_q4_1_bcm_cfg4_m8_packed"],
+    "cfg4_q4_1_m8_decode_batch_kn_prepacked": ["gemv_q4_1_bcm_mfma_cfg4_m8_packed"],
     "gated_ffn_swiglu_m1": ["gemv_q4_1_pipe_gated_m1"],
     "gated_ffn_swiglu_m512": ["gemm_q4_1_ring_gated_m512"],
     "cfg5_s8_addto_gelu": ["gemm_i8_ring_cfg5", "gemm_i8_reduce_cfg5"],

@@ -1477,6 +1477,148 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_bcm(Q41Kern p)
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM over the prepacked blocks-along-N planes: f16 A with 3 <= M <=
+// 16 rows per launch, K % 256 == 0. Workgroup j owns block column j (32
+// columns); its 4 waves take K quarters, each through its own DMA ring in LDS
+// (NS stages of 64 k: the 8 nibble groups, 1 KiB; the 64 d|m dwords, 256
+// bytes; A's 16 rows x 128 bytes with row r's 16-byte chunk c in slot c ^ ((r
+// >> 1) & 7), so the 16 rows a fragment read serves hit 16 bank groups), so a
+// wave waits only on its own loads, never at a barrier. Per 32-k slice lane l
+// decodes the slice's rows 8 (l / 16) .. + 7 at columns l % 16 (low nibbles)
+// and 16 + l % 16 (high nibbles): byte l % 4 of the rows' nibble dword (l %
+// 16) / 4 (a 32-byte LDS read that 4 lanes share), 1024 + q by v_and_or_b32
+// under exponent byte 0x64, v_pk_add_f16 removes 1024 exactly and
+// v_pk_fma_f16 rounds d * q + m once (the f16 weights of the ring GEMMs); then
+// two v_mfma_f32_16x16x32_f16 with A's fragment (row l % 16, the same 8 k).
+// The quarters meet in LDS in wave order (deterministic). Bound: HBM.
+// ---------------------------------------------------------------------------
+template <int NS>
+__global__ __launch_bounds__(256) void gemv_q4_1_bcm_mfma(Q41Kern p)
+{
+    constexpr int W = 4;
+    constexpr int kNib = 1024, kDm = 256, kAt = 2048, kSt = kNib + kDm + kAt;
+    constexpr int L = 4;                              // DMA instructions per stage
+    static_assert((NS - 1) * L < 64, "vmcnt range");
+    static_assert(W * NS * kSt >= (W - 1) * 2 * 64 * 16, "the quarters' sums fit the ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[W * NS * kSt];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t j = blockIdx.x;
+    const uint8_t* nib = p.b + j * p.ldb;
+    const uint8_t* dmc = reinterpret_cast<const uint8_t*>(p.bdm + j * p.ldbdm);
+    const _Float16* A = static_cast<const _Float16*>(p.a);
+    const int kq = p.k / W;
+    const int kbeg = wave * kq;
+    const int nst = kq / 64;
+    uint8_t* my = ring + wave * NS * kSt;
+    // A rows staged by lane: instruction q holds rows 8 q .. 8 q + 7
+    const _Float16* a_src[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int r = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        a_src[q] = A + (int64_t)min(r, p.m - 1) * p.lda + kbeg + 8 * c;
+    }
+    auto issue = [&](int st) {
+        uint8_t* base = my + (st % NS) * kSt;
+        const int k0 = kbeg + 64 * st;
+        __builtin_amdgcn_global_load_lds(NNOPS_GPTR(nib + (int64_t)(k0 / 8) * 128 + 16 * lane), NNOPS_LPTR(base), 16,
+                                         0, 2);
+        if (lane < 16) {
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(dmc + (int64_t)k0 * 4 + 16 * lane),
+                                             NNOPS_LPTR(base + kNib), 16, 0, 2);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            __builtin_amdgcn_global_load_lds(NNOPS_GPTR(a_src[q] + 64 * st), NNOPS_LPTR(base + kNib + kDm + 1024 * q),
+                                             16, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) {
+        if (st < nst) {
+            issue(st);
+        }
+    }
+    const int ar = lane & 15, g = lane >> 4;          // A row; k group of the slice
+    const int col = lane & 15;
+    const uint32_t sel = 0x0c000c00u | (uint32_t)(4 + (col & 3)) << 16 | (uint32_t)(col & 3);
+    v4f acc0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const v2h k1024 = __builtin_bit_cast(v2h, 0x64006400u);
+    for (int st = 0; st < nst; ++st) {
+        if (st + NS - 1 < nst) {
+            issue(st + NS - 1);
+            wait_vmcnt<(NS - 1) * L>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        asm volatile("" ::: "memory");
+        const uint8_t* base = my + (st % NS) * kSt;
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+            const int cf = 4 * sl + g;                    // A chunk of the lane's 8 k
+            const v8h af = *reinterpret_cast<const v8h*>(base + kNib + kDm + ar * 128 + ((cf ^ ((ar >> 1) & 7)) << 4));
+            const uint8_t* gp = base + (4 * sl + g) * 128 + 32 * (col >> 2);
+            const v4i n0 = *reinterpret_cast<const v4i*>(gp);
+            const v4i n1 = *reinterpret_cast<const v4i*>(gp + 16);
+            const uint8_t* dp = base + kNib + (32 * sl + 8 * g) * 4;
+            const v4i d0 = *reinterpret_cast<const v4i*>(dp);
+            const v4i d1 = *reinterpret_cast<const v4i*>(dp + 16);
+            const uint32_t nw[8] = {(uint32_t)n0.x, (uint32_t)n0.y, (uint32_t)n0.z, (uint32_t)n0.w,
+                                    (uint32_t)n1.x, (uint32_t)n1.y, (uint32_t)n1.z, (uint32_t)n1.w};
+            const uint32_t dw[8] = {(uint32_t)d0.x, (uint32_t)d0.y, (uint32_t)d0.z, (uint32_t)d0.w,
+                                    (uint32_t)d1.x, (uint32_t)d1.y, (uint32_t)d1.z, (uint32_t)d1.w};
+            uint32_t wl[4], wh[4];
+#pragma unroll
+            for (int rp = 0; rp < 4; ++rp) {
+                const uint32_t t = __builtin_amdgcn_perm(nw[2 * rp + 1], nw[2 * rp], sel);
+                const v2h ql = __builtin_bit_cast(v2h, and_or_u32(t, 0x000f000fu, 0x64006400u)) - k1024;
+                const v2h qh = __builtin_bit_cast(v2h, and_or_u32(t >> 4, 0x000f000fu, 0x64006400u)) - k1024;
+                const v2h d2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dw[2 * rp + 1], dw[2 * rp], 0x05040100u));
+                const v2h m2 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(dw[2 * rp + 1], dw[2 * rp], 0x07060302u));
+                wl[rp] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(ql, d2, m2));
+                wh[rp] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(qh, d2, m2));
+            }
+            const v8h bl = __builtin_bit_cast(v8h, v4i{(int)wl[0], (int)wl[1], (int)wl[2], (int)wl[3]});
+            const v8h bh = __builtin_bit_cast(v8h, v4i{(int)wh[0], (int)wh[1], (int)wh[2], (int)wh[3]});
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bl, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bh, acc1, 0, 0, 0);
+        }
+    }
+    // the quarters meet in wave order: rows 4 (lane / 16) + r of columns
+    // lane % 16 (acc0) and 16 + lane % 16 (acc1)
+    __syncthreads();
+    v4f* red = reinterpret_cast<v4f*>(ring);
+    if (wave > 0) {
+        red[((wave - 1) * 2 + 0) * 64 + lane] = acc0;
+        red[((wave - 1) * 2 + 1) * 64 + lane] = acc1;
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+        acc0 += red[(w * 2 + 0) * 64 + lane];
+        acc1 += red[(w * 2 + 1) * 64 + lane];
+    }
+    const int n = (int)j * 32 + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * g + r;
+        if (m < p.m) {
+            if (n < p.n) {
+                store_out(p, m, n, acc0[r]);
+            }
+            if (n + 16 < p.n) {
+                store_out(p, m, n + 16, acc1[r]);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Skinny GEMM, blocks along K ([N][K/32]), f16 A with 3 <= M <= 16 rows per
 // launch (more rows: one launch per 16), K % 256 == 0: the weight streams
@@ -2832,8 +2974,10 @@ inline bool skinny_ok(const NnopsGemmQ41Args& g)
 }
 
 // rows of A up to which the prepacked planes take the GEMV passes rather than
-// the ring (M = 12: 65 us against 77)
+// the ring (M = 12: 65 us against 77), and (K % 256 == 0) the skinny MFMA
+// form, one launch per 16 rows
 constexpr int64_t kBcmMaxM = 12;
+constexpr int64_t kBcmMfmaMaxM = 48;
 
 // The one-launch GEMV over the prepacked planes (gemv_q4_1_bcm): f16 A with
 // 16-byte-aligned rows, K % 8 == 0.
@@ -3054,6 +3198,16 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
                     NNOPS_LAUNCH(reduce_q4_1<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kk);
                 }
             }
+        }
+    } else if (bcm_ok(*g) && g->m >= 3 && g->m <= kBcmMfmaMaxM && g->k % 256 == 0) {
+        // a few rows of A over the prepacked planes on the matrix cores, the
+        // weight streamed once per 16 rows
+        for (int m0 = 0; m0 < k.m; m0 += 16) {
+            Q41Kern kk = k;
+            kk.m = std::min(16, k.m - m0);
+            kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
+            kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
+            NNOPS_LAUNCH((gemv_q4_1_bcm_mfma<4>), dim3((unsigned)nbn), dim3(256), 0, s, kk);
         }
     } else if (bcm_ok(*g) && g->m <= kBcmMaxM) {
         // a few rows of A over the prepacked planes: the one-launch GEMV, up

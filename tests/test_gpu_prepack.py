@@ -6,7 +6,7 @@ through the fp-activation and dequantizing routes; and the packed q4_1
 weight with blocks along N (two planes) gives bit-for-bit the raw weight's
 result on the ring route, the same up to f32 summation order on the GEMV
 (which walks the planes in groups of 8 rows), within the Q4_1 tolerance
-elsewhere."""
+elsewhere (the skinny MFMA route of 3..48 rows)."""
 from __future__ import annotations
 
 import numpy as np
@@ -15,9 +15,14 @@ import pytest
 import oracle
 import datagen as dg
 import nnops_amd as na
-from gpu_util import dev, host, announce
+from gpu_util import dev, host, announce, norm_err
 
 pytestmark = pytest.mark.gpu
+
+
+def packed_skinny(M, K, a_f16):
+    """The packed q4_1 planes' skinny MFMA route: f16 A, 3 <= M <= 48, K % 256 == 0."""
+    return a_f16 and 3 <= M <= 48 and K % 256 == 0
 
 
 def run(op, a_t, w_t, out_dtype, shape):
@@ -119,7 +124,7 @@ def test_matmul_q4_1_prepacked_matches_raw(M, K, N, a_f16):
     at = na.tensor(dev(a))
     got_p = run(op, at, packed, torch.float32, (M, N))
     got_r = run(op, at, wt, torch.float32, (M, N))
-    if (M > 2 and a_f16) or M > 16:
+    if ((M > 2 and a_f16) or M > 16) and not packed_skinny(M, K, a_f16):
         # the f16 ring or the f32 MFMA GEMM: same decode, same order
         np.testing.assert_array_equal(got_p, got_r)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=False)
@@ -185,8 +190,8 @@ def test_matmul_q4_1_prepacked_config4_kn():
 @pytest.mark.parametrize("M", [2, 40])
 def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
     """f16 A -> f16 C (nnops: the output follows A) through the packed
-    planes, equal to the raw weight's result on the ring (M=40) route and,
-    like it, within the Q4_1 bar on the GEMV (M=2) route; and a batched A
+    planes (the GEMV at M=2, the skinny MFMA GEMM at M=40) and the raw
+    weight (the GEMV, the ring), each within the Q4_1 bar; and a batched A
     [2, M, K] against the one packed weight."""
     import torch
     announce(f"prepack q4_1 f16 out / batched M={M}")
@@ -199,7 +204,7 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
     at = na.tensor(dev(a))
     got_p = run(op, at, packed, torch.float16, (2, M, N))
     got_r = run(op, at, wt, torch.float16, (2, M, N))
-    if M > 2:
+    if M > 2 and not packed_skinny(M, K, True):
         np.testing.assert_array_equal(got_p.view(np.uint16), got_r.view(np.uint16))
     for bi in range(2):
         want = oracle.gemm_q4_1(a[bi], blk, N, trans_b=False, w_round_f16=True, c_f16=True).astype(np.float32)
@@ -211,16 +216,19 @@ def test_matmul_q4_1_prepacked_f16_out_and_batched_a(M):
 
 
 @pytest.mark.parametrize("f16_out", [False, True])
-@pytest.mark.parametrize("M", [3, 5, 8, 12])
-def test_matmul_q4_1_prepacked_few_rows(M, f16_out):
-    """3 <= M <= 12 rows of f16 A over the packed planes take the one-launch
-    GEMV in passes of up to 8 rows (products a * d split exactly, like the M
-    <= 2 passes): within the Q4_1 bar of the f32 dequant oracle, rows of
-    every pass checked, f32 and f16 destinations, N ragged (not a multiple of
-    the 32-column block)."""
+@pytest.mark.parametrize("M,K", [(3, 2048), (5, 2048), (8, 2048), (12, 2048), (16, 4096), (33, 1024), (48, 2048),
+                                 (5, 1000), (12, 1000)])
+def test_matmul_q4_1_prepacked_few_rows(M, K, f16_out):
+    """3 <= M <= 48 rows of f16 A over the packed planes: K % 256 == 0 takes
+    the skinny MFMA GEMM (weights decoded to f16, one launch per 16 rows:
+    within 1e-4 of the oracle with f16-rounded weights), else the one-launch
+    GEMV in passes of up to 8 rows (M <= 12; products a * d split exactly).
+    Both within the Q4_1 bar of the f32 dequant oracle, every row checked,
+    f32 and f16 destinations, N ragged (not a multiple of the 32-column
+    block)."""
     import torch
     announce(f"prepack q4_1 few rows M={M} f16_out={f16_out}")
-    K, N = 2048, 1000
+    N = 1000
     a = dg.normal(950 + M, (M, K)).astype(np.float16)
     blk = dg.q4_1_blocks(951 + M, K, N)
     op = na.MatMul(transpose_b=False)
@@ -233,6 +241,8 @@ def test_matmul_q4_1_prepacked_few_rows(M, f16_out):
     scale = max(np.max(np.abs(want)), np.sqrt(np.mean(want ** 2)))
     err = float(np.max(np.abs(got.astype(np.float32) - want)) / scale)
     assert err <= 2e-3, err
+    if packed_skinny(M, K, True) and not f16_out:
+        assert norm_err(got, oracle.gemm_q4_1(a, blk, N, trans_b=False, w_round_f16=True)) <= 1e-4
 
 
 @pytest.mark.parametrize("K,N", [(64, 200), (96, 1024), (37, 72)])
