@@ -3207,7 +3207,10 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
             kk.m = std::min(16, k.m - m0);
             kk.a = static_cast<const char*>(g->a) + (int64_t)m0 * g->lda * 2;
             kk.c = static_cast<char*>(g->c) + (int64_t)m0 * g->ldc * (k.out_f16 ? 2 : 4);
-            NNOPS_LAUNCH((gemv_q4_1_bcm_mfma<4>), dim3((unsigned)nbn), dim3(256), 0, s, kk);
+            // 3 stages of 64 k in flight per wave (2 and 4 measured the same or slower;
+            // so did A fragments loaded straight from L2, 8 waves per column, and
+            // rotated K start points per workgroup: 12.6-19 us at M = 8)
+            NNOPS_LAUNCH((gemv_q4_1_bcm_mfma<3>), dim3((unsigned)nbn), dim3(256), 0, s, kk);
         }
     } else if (bcm_ok(*g) && g->m <= kBcmMaxM) {
         // a few rows of A over the prepacked planes: the one-launch GEMV, up
