@@ -2263,9 +2263,19 @@ __global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, 
     __shared__ float red[4];
     const int m = blockIdx.x;
     const float* row = a + (int64_t)m * lda;
+    // 16-byte loads where the row allows (k % 4 == 0 always: k % 64 == 0)
+    const bool vec = ((uintptr_t)row & 15) == 0;
     float mx = 0.0f;
-    for (int i = threadIdx.x; i < k; i += 256) {
-        mx = fmaxf(mx, __builtin_fabsf(row[i]));
+    if (vec) {
+        for (int i = 4 * (int)threadIdx.x; i < k; i += 1024) {
+            const v4f x = *reinterpret_cast<const v4f*>(row + i);
+            mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[0])), __builtin_fabsf(x[1]));
+            mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[2])), __builtin_fabsf(x[3]));
+        }
+    } else {
+        for (int i = threadIdx.x; i < k; i += 256) {
+            mx = fmaxf(mx, __builtin_fabsf(row[i]));
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -2288,11 +2298,26 @@ __global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, 
     }
     _Float16* h_row = hi + (int64_t)m * k;
     _Float16* l_row = lo + (int64_t)m * k;
-    for (int i = threadIdx.x; i < k; i += 256) {
-        const float x = row[i] * down;
-        const _Float16 h = (_Float16)x;
-        h_row[i] = h;
-        l_row[i] = (_Float16)(x - (float)h);
+    // 4 values per thread and step: the row is still in this CU's cache
+    for (int i = 4 * (int)threadIdx.x; i < k; i += 1024) {
+        v4f x;
+        if (vec) {
+            x = *reinterpret_cast<const v4f*>(row + i);
+        } else {
+            x = v4f{row[i], row[i + 1], row[i + 2], row[i + 3]};
+        }
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float y = x[q] * down;
+            h[q] = (_Float16)y;
+            l[q] = (_Float16)(y - (float)h[q]);
+        }
+        uint2 hw, lw;
+        __builtin_memcpy(&hw, h, 8);
+        __builtin_memcpy(&lw, l, 8);
+        *reinterpret_cast<uint2*>(h_row + i) = hw;
+        *reinterpret_cast<uint2*>(l_row + i) = lw;
     }
 }
 
@@ -2339,17 +2364,18 @@ __device__ __forceinline__ v8h decode8_f16(uint32_t lo0, uint32_t lo1, v2h d2, v
 // activation -- measured slower than the separate pass: 108 against 98 us at
 // 512 x 14336 x 4096, the pass's arithmetic then running with the matrix
 // cores idle; the gated form saves the larger staging: 196 -> 184 us.)
-template <bool OUT16, int NS, int WM, int WN = 4, bool GATED = false, bool SPLIT = false>
+template <bool OUT16, int NS, int WM, int WN = 4, bool GATED = false, bool SPLIT = false, int BM = 128, int BN = 256>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 {
-    static_assert(!GATED || (WM == 1 && WN == 8), "gated: one wave per 32 columns, halves 4 waves apart");
+    static_assert(!GATED || (WM == 1 && WN == 8 && BM == 128 && BN == 256),
+                  "gated: one wave per 32 columns, halves 4 waves apart");
     static_assert(!SPLIT || (!GATED && WM == 1), "split A: one wave row");
     constexpr int W = WM * WN;                      // waves: WM along M x WN along N
     constexpr int AP = SPLIT ? 2 : 1;               // planes of A (SPLIT: hi and lo f16 parts)
-    constexpr int QA = 16 * AP / W, QB = 16 / W;    // 1 KiB pieces per wave per stage
+    constexpr int QA = AP * BM / (8 * W), QB = BN / (16 * W);   // 1 KiB pieces per wave per stage
+    static_assert(QA * 8 * W == AP * BM && QB * 16 * W == BN, "whole pieces per wave");
     constexpr int L = QA + QB;
     static_assert(NS >= 3 && (NS - 2) * L < 64, "stages");
-    constexpr int BM = 128, BN = 256;
     constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     constexpr int kA = AP * BM * 128, kB = BN * 64, kStage = kA + kB;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
