@@ -726,6 +726,9 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     // latency then hides behind the first stage's) where the LDS holds them
     constexpr bool kSbl = (MODE == RING_S8 || MODE == RING_FP) && NS * kStage + BN * 4 <= 160 * 1024;
     __shared__ __attribute__((aligned(16))) float sbl[kSbl ? BN : 4];
+    // RING_FP: the bias in the destination's type, widened to f32, likewise
+    constexpr bool kBl = MODE == RING_FP && kSbl && NS * kStage + BN * 8 <= 160 * 1024;
+    __shared__ __attribute__((aligned(16))) float biasl[kBl ? BN : 4];
 
     int tm, tn, sp;
     ring_coords(ceil_div(p.m, BM), ceil_div(p.n, BN), tm, tn, sp);
@@ -924,6 +927,22 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                 v = *reinterpret_cast<const v4f*>(p.ep.s_b + n);
             }
             *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = v;
+        }
+    }
+    if constexpr (kBl) {
+        if (threadIdx.x >= BN / 4 && threadIdx.x < BN / 2) {
+            const int t = (int)threadIdx.x - BN / 4;
+            const int n = n0 + 4 * t;
+            v4f v = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (p.ep.bias_fp != nullptr && n < p.n) {
+                if (p.ep.out_kind == NNOPS_OUT_F16) {
+                    const _Float16* b16 = static_cast<const _Float16*>(p.ep.bias_fp) + n;
+                    v = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
+                } else {
+                    v = *reinterpret_cast<const v4f*>(static_cast<const float*>(p.ep.bias_fp) + n);
+                }
+            }
+            *reinterpret_cast<v4f*>(&biasl[4 * t]) = v;
         }
     }
     if (kt >= NS - 1) {
@@ -1134,7 +1153,9 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             cp.n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
             cp.sb = sbp[j][g];
             cp.bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (cp.n < p.n && ep.bias_fp != nullptr) {
+            if constexpr (kBl) {
+                cp.bias = *reinterpret_cast<const v4f*>(&biasl[cp.n - n0]);
+            } else if (cp.n < p.n && ep.bias_fp != nullptr) {
                 if (f16) {
                     const _Float16* b16 = static_cast<const _Float16*>(ep.bias_fp) + cp.n;
                     cp.bias = v4f{(float)b16[0], (float)b16[1], (float)b16[2], (float)b16[3]};
@@ -1146,7 +1167,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         };
         // the 4 values of (i, j, g) for this lane: row wm0 + 32 i + (lane & 31),
         // columns cp.n .. + 3
-        auto values = [&](int i, int j, int g, const ColFp& cp, float sa) {
+        // CLIP: a finite clip range (the default -inf / +inf clip is the
+        // identity for every value, NaN included, and is left out)
+        auto values = [&](int i, int j, int g, const ColFp& cp, float sa, auto clip_c) {
+            constexpr bool kClip = decltype(clip_c)::value;
             const int n = cp.n;
             const int m = m0 + wm0 + i * 32 + (lane & 31);
             v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1172,8 +1196,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                 if (pre) {
                     f = __fadd_rn(f, old[e]);
                 }
-                f = f < ep.min_clip ? ep.min_clip : f;
-                f = ep.max_clip < f ? ep.max_clip : f;
+                if constexpr (kClip) {
+                    f = f < ep.min_clip ? ep.min_clip : f;
+                    f = ep.max_clip < f ? ep.max_clip : f;
+                }
                 if (relu) {
                     f = f > 0.0f ? f : 0.0f;
                 }
@@ -1199,7 +1225,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             // [TM][128-byte] tile of one slab of columns (32 f32 or 64 f16),
             // entries of 4 columns at slot q ^ (row % groups) in the row.
             int8_t* tile = ring + wave * (TM * 128);
-            auto slab = [&](auto esz_c) {
+            auto slab = [&](auto esz_c, auto clip_c) {
                 constexpr int ESZ = decltype(esz_c)::value;          // output element bytes
                 constexpr int SC = (TN < 128 / ESZ) ? TN : 128 / ESZ; // columns per slab
                 constexpr int GPS = SC / 4;                          // 4-column entries per slab row
@@ -1218,7 +1244,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
                             for (int i = 0; i < FM; ++i) {
                                 const int r = i * 32 + (lane & 31);
-                                const v4f o = values(i, j, g, cp, sa_i[i]);
+                                const v4f o = values(i, j, g, cp, sa_i[i], clip_c);
                                 int8_t* dst = tile + r * RB + ((q ^ (r % GPS)) * E);
                                 if constexpr (ESZ == 4) {
                                     *reinterpret_cast<v4f*>(dst) = o;
@@ -1260,10 +1286,17 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 }
             };
-            if (f16) {
-                slab(std::integral_constant<int, 2>{});
+            using TrueC = std::integral_constant<bool, true>;
+            using FalseC = std::integral_constant<bool, false>;
+            const bool clip = !(ep.min_clip == -__builtin_inff() && ep.max_clip == __builtin_inff());
+            if (f16 && clip) {
+                slab(std::integral_constant<int, 2>{}, TrueC{});
+            } else if (f16) {
+                slab(std::integral_constant<int, 2>{}, FalseC{});
+            } else if (clip) {
+                slab(std::integral_constant<int, 4>{}, TrueC{});
             } else {
-                slab(std::integral_constant<int, 4>{});
+                slab(std::integral_constant<int, 4>{}, FalseC{});
             }
         } else {
 #pragma unroll
@@ -1278,7 +1311,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                         if (m >= p.m || n >= p.n) {
                             continue;
                         }
-                        const v4f o = values(i, j, g, cp, sa_i[i]);
+                        const v4f o = values(i, j, g, cp, sa_i[i], std::integral_constant<bool, true>{});
                         char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
                         if (f16) {
                             _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
@@ -1530,6 +1563,7 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit 
     const bool even = ep.round_even != 0;
     const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
     const float inv_out = __fdiv_rn(1.0f, ep.s_out);
+    const bool clip = !(ep.min_clip == -__builtin_inff() && ep.max_clip == __builtin_inff());
     uint32_t outw = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1551,8 +1585,10 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit 
                     f = __fadd_rn(f, res);
                 }
             }
-            f = f < ep.min_clip ? ep.min_clip : f;
-            f = ep.max_clip < f ? ep.max_clip : f;
+            if (clip) {   // the default -inf / +inf clip is the identity
+                f = f < ep.min_clip ? ep.min_clip : f;
+                f = ep.max_clip < f ? ep.max_clip : f;
+            }
             if constexpr (ACT == NNOPS_ACT_RELU) {
                 f = f > 0.0f ? f : 0.0f;
             } else if constexpr (ACT == NNOPS_ACT_GELU) {
