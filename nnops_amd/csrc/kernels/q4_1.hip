@@ -2631,10 +2631,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
 // d|m bytes (2 pieces, waves 0 and 1), both with the slot-row order above
 // (rows k and k + 8 then sit 32 banks apart in the nibbles and 8 in d|m).
 // ---------------------------------------------------------------------------
-template <bool OUT16, int NS, bool SOA>
+template <bool OUT16, int NS, bool SOA, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 {
-    constexpr int W = 8, QA = 2;                    // A: 2 KiB pieces per wave per stage
+    constexpr int AP = SPLIT ? 2 : 1;               // planes of A (SPLIT: hi and lo f16 parts)
+    constexpr int W = 8, QA = 2 * AP;               // A: 2 KiB pieces per wave per stage and plane
     constexpr int BM = 128, BN = 256, FM = 4;
     constexpr int kRow = BN / 32 * 20;              // 160 bytes of B per k row
     // slot-row pitch of the d|m dwords and of the nibble dwords, and where the
@@ -2645,7 +2646,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     // (2 ks and 2 ks + 1) sit 4 banks apart; the d|m rows follow
     constexpr int kGrp = 1040;
     constexpr int kDmAt = SOA ? 8 * kGrp : 0;
-    constexpr int kA = BM * 128, kB = SOA ? kDmAt + 64 * kRowD : 64 * kRow, kStage = kA + kB;
+    constexpr int kA = AP * BM * 128, kB = SOA ? kDmAt + 64 * kRowD : 64 * kRow, kStage = kA + kB;
     constexpr int kBPieces = kB / 1024;             // 10 x 1 KiB: waves 0, 1 issue two
     static_assert(NS >= 3 && kBPieces > W && kBPieces <= 2 * W, "stages");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStage];
@@ -2679,9 +2680,10 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     int a_off[QA], b_off[2];
 #pragma unroll
     for (int i = 0; i < QA; ++i) {
+        // SPLIT: staged rows 128..255 are the lo plane's rows 0..127
         const int ra = 8 * (QA * wave + i) + (lane >> 3);
         const int ca = (lane & 7) ^ ((ra >> 1) & 7);
-        a_off[i] = min(ra, p.m - 1 - m0) * (int)p.lda * 2 + ca * 16;
+        a_off[i] = min(ra & (BM - 1), p.m - 1 - m0) * (int)p.lda * 2 + ca * 16 + (ra >= BM ? (int)p.plane : 0);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -2734,7 +2736,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
 
     const int fr = lane & 31, kh = lane >> 5;
     auto a_frag = [&](const uint8_t* st, int i, int ks) {
-        const int r = i * 32 + fr;
+        const int r = (i >= FM ? BM : 0) + (i % FM) * 32 + fr;
         const int c = (2 * ks + kh) ^ ((r >> 1) & 7);
         return *reinterpret_cast<const v8h*>(st + r * 128 + c * 16);
     };
@@ -2819,17 +2821,21 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
     wait_ring(kt < NS - 1);
     __syncthreads();
 
-    v8h fa0[FM], fa1[FM], fb0, fb1;
-    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[FM]) {
+    v8h fa0[AP * FM], fa1[AP * FM], fb0, fb1;
+    auto load_a = [&](const uint8_t* st, int ks, v8h (&fa)[AP * FM]) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < AP * FM; ++i) {
             fa[i] = a_frag(st, i, ks);
         }
     };
-    auto mfma_slice = [&](const v8h (&fa)[FM], const v8h& fb) {
+    // SPLIT: the hi parts' products, then the lo parts' into the same accumulators
+    auto mfma_slice = [&](const v8h (&fa)[AP * FM], const v8h& fb) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb, acc[i], 0, 0, 0);
+        for (int h = 0; h < AP; ++h) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[h * FM + i], fb, acc[i], 0, 0, 0);
+            }
         }
     };
     for (int t = 0; t < kt; ++t) {
@@ -2869,10 +2875,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
                 if (m < p.m) {
+                    // SPLIT: the row's power-of-two factor (exact)
+                    const float v = SPLIT ? acc[i][r] * p.row_scale[m] : acc[i][r];
                     if constexpr (OUT16) {
-                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)acc[i][r];
+                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
                     } else {
-                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = acc[i][r];
+                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
                     }
                 }
             }
@@ -3020,14 +3028,23 @@ inline bool kn_ring_ok(const NnopsGemmQ41Args& g)
 }
 
 
-// f32 A past the skinny and GEMV shapes, blocks along K, K % 64 == 0: split
-// into two f16 planes in the workspace (split_a_f32) and run the SPLIT ring
-// (two f16 MFMAs per decoded weight fragment) instead of the f32 MFMA GEMM
-// (config 4's shape at M = 512: 555 us on the f32 matrix cores).
+// f32 A past the skinny and GEMV shapes, K % 64 == 0, either weight form
+// (blocks along K: the ring; along N, raw rows or the prepacked planes: the
+// kn ring): split into two f16 planes in the workspace (split_a_f32) and run
+// the ring's SPLIT form (two f16 MFMAs per decoded weight fragment) instead
+// of the f32 MFMA GEMM (config 4's shape at M = 512: 555 us on the f32
+// matrix cores, 152 us split).
 inline bool split_ok(const NnopsGemmQ41Args& g)
 {
-    return !g.a_f16 && g.trans_b && !g.b_soa && g.k % 64 == 0 && !skinny_ok(g) && !use_gemv(g) &&
-           4 * g.m * g.k < INT32_MAX && 32 * g.ldb_bytes < INT32_MAX;
+    if (g.a_f16 || g.k % 64 != 0 || skinny_ok(g) || use_gemv(g) || 4 * g.m * g.k >= INT32_MAX) {
+        return false;
+    }
+    if (g.trans_b) {
+        return !g.b_soa && 32 * g.ldb_bytes < INT32_MAX;
+    }
+    // blocks along N: the kn ring's weight conditions (its A is the planes)
+    return (g.ldb_bytes % 16) == 0 && ((uintptr_t)g.b & 15) == 0 &&
+           (g.b_soa ? 8 * g.ldb_bytes < INT32_MAX && 8 * g.ldb_dm * 4 < INT32_MAX : g.k * g.ldb_bytes < INT32_MAX);
 }
 
 inline size_t split_ws_bytes(const NnopsGemmQ41Args& g)
@@ -3274,10 +3291,18 @@ extern "C" int nnops_hip_gemm_q4_1(const NnopsGemmQ41Args* g, void* workspace, s
         kk.plane = g->m * g->k * 2;
         kk.row_scale = rs;
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 255) / 256));
-        if (k.out_f16) {
+        if (g->trans_b && k.out_f16) {
             NNOPS_LAUNCH((gemm_q4_1_ring<true, 3, 1, 8, false, true>), dim3(tiles), dim3(512), 0, s, kk);
-        } else {
+        } else if (g->trans_b) {
             NNOPS_LAUNCH((gemm_q4_1_ring<false, 3, 1, 8, false, true>), dim3(tiles), dim3(512), 0, s, kk);
+        } else if (soa && k.out_f16) {
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<true, 3, true, true>), dim3(tiles), dim3(512), 0, s, kk);
+        } else if (soa) {
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<false, 3, true, true>), dim3(tiles), dim3(512), 0, s, kk);
+        } else if (k.out_f16) {
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<true, 3, false, true>), dim3(tiles), dim3(512), 0, s, kk);
+        } else {
+            NNOPS_LAUNCH((gemm_q4_1_kn_ring<false, 3, false, true>), dim3(tiles), dim3(512), 0, s, kk);
         }
     } else if (!g->a_f16) {
         const unsigned tiles = (unsigned)(((g->m + 127) / 128) * ((g->n + 127) / 128));

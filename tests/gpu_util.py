@@ -32,15 +32,19 @@ def announce(msg):
     sys.stdout.flush()
 
 
-def q41_f16_weights(M, K, f16, trans_b=True):
+def q41_f16_weights(M, K, f16, trans_b=True, N=None, packed=False):
     """Whether the Q4_1 route for M x K decodes its weights to f16 (the oracle's
-    w_round_f16): f16 A past M = 2, and f32 A on the split-f16 ring (blocks
-    along K, K % 64 == 0, past the GEMV rows M <= 16 and the skinny rows M <=
-    48 with K % 256 == 0)."""
+    w_round_f16): f16 A past M = 2, and f32 A on the split-f16 rings (K % 64
+    == 0, past the GEMV rows M <= 16; blocks along K past the skinny rows M <=
+    48 with K % 256 == 0; blocks along N with 16-byte weight rows, i.e. N a
+    multiple of 128, or the prepacked planes)."""
     if f16:
         return M > 2
-    skinny = 3 <= M <= 48 and K % 256 == 0
-    return trans_b and K % 64 == 0 and M > 16 and not skinny
+    if K % 64 or M <= 16:
+        return False
+    if trans_b:
+        return not (M <= 48 and K % 256 == 0)
+    return packed or ((N + 31) // 32 * 20) % 16 == 0
 
 
 def norm_err(got, want):

@@ -188,7 +188,7 @@ def test_q4_1_matmul_alpha_beta(f16, M, trans_b, kw):
         ins.append(na.tensor(dev(bias)))
     assert op.compute([na.tensor(y)], ins) == na.OK
     torch.cuda.synchronize()
-    acc = oracle.gemm_q4_1(x, blk, N, trans_b=trans_b, w_round_f16=q41_f16_weights(M, K, f16, trans_b))
+    acc = oracle.gemm_q4_1(x, blk, N, trans_b=trans_b, w_round_f16=q41_f16_weights(M, K, f16, trans_b, N))
     want = oracle.fp_out_pass(acc, N, out=old, out_f16=f16, bias=bias, act=MM_ACT[kw.get("act")],
                               matmul_order=True, alpha=kw["alpha"], beta=kw["beta"],
                               residual_pre=kw.get("residual_pre", False)).astype(np.float32)

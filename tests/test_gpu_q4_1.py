@@ -12,7 +12,7 @@ import pytest
 import oracle
 import datagen as dg
 import nnops_amd as na
-from gpu_util import dev, host, announce, norm_err, oracle_rows
+from gpu_util import dev, host, announce, norm_err, oracle_rows, q41_f16_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -92,20 +92,19 @@ def test_q4_1_skinny_f32_a(M, K, N):
     assert norm_err(got, want) <= 1e-4
 
 
-def split_route(M, K, trans_b):
-    """The f32-A shapes that take the split-f16 ring: blocks along K, K % 64
-    == 0, past the GEMV (M <= 16) and skinny (M <= 48, K % 256 == 0) rows."""
-    skinny = 3 <= M <= 48 and K % 256 == 0
-    return trans_b and K % 64 == 0 and M > 16 and not skinny
+def split_route(M, K, trans_b, N):
+    """The f32-A shapes that take a split-f16 ring (gpu_util.q41_f16_weights)."""
+    return q41_f16_weights(M, K, False, trans_b, N)
 
 
-@pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40)])
+@pytest.mark.parametrize("M,K,N", [(17, 640, 96), (130, 1000, 200), (300, 4096, 520), (16, 96, 40),
+                                   (64, 512, 256), (130, 1024, 1000)])
 @pytest.mark.parametrize("trans_b", [True, False])
 def test_q4_1_f32_a_gemm(M, K, N, trans_b):
     """f32 A past the GEMV rows: the f32 MFMA GEMM (ragged M, N and K tiles)
     against the f64-accumulated oracle within 1e-4 (normalized; an f32 sum of
     K = 4096 products carries ~1e-5); M = 16 is the GEMV loop's last row
-    count. The split-f16 ring (blocks along K, K % 64 == 0) decodes each
+    count. The split-f16 rings (K % 64 == 0, either weight form) decode each
     weight to f16 as the f16-A routes do: within 1e-4 of the oracle with the
     weights so rounded (A's two f16 parts carry 22 bits), within BASELINE's
     2e-3 of the exact one."""
@@ -115,7 +114,7 @@ def test_q4_1_f32_a_gemm(M, K, N, trans_b):
     blk = dg.q4_1_blocks(seed + 1, N, K) if trans_b else dg.q4_1_blocks(seed + 2, K, N)
     got = run_gpu(a, blk, N, trans_b=trans_b)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=trans_b)
-    if split_route(M, K, trans_b):
+    if split_route(M, K, trans_b, N):
         assert norm_err(got, oracle.gemm_q4_1(a, blk, N, trans_b=trans_b, w_round_f16=True)) <= 1e-4
         assert norm_err(got, want) <= TOL
     else:
@@ -137,7 +136,7 @@ def test_q4_1_f32_a_split_row_scales():
     a[3] = 0.0
     a[4] = np.float32(2.0 ** -130) * np.sign(a[4])
     blk = dg.q4_1_blocks(78, N, K)
-    assert split_route(M, K, True)
+    assert split_route(M, K, True, N)
     got = run_gpu(a, blk, N, trans_b=True)
     want = oracle.gemm_q4_1(a, blk, N, trans_b=True, w_round_f16=True)
     assert np.all(got[3] == 0.0)
