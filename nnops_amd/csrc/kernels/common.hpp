@@ -190,8 +190,9 @@ __device__ __forceinline__ int32_t requant_clamped(float x, int32_t zp, bool u8,
     const float zpf = (float)zp;
     const float lo = __fsub_rn(u8 ? 0.0f : -128.0f, zpf);
     const float hi = __fsub_rn(u8 ? 255.0f : 127.0f, zpf);
-    x = x < lo ? lo : x;
-    x = hi < x ? hi : x;
+    // clamp to [lo, hi] (lo < hi) in one v_med3_f32: the same value as the
+    // two compares for every number x (the int8 passes never hand it a NaN)
+    x = __builtin_amdgcn_fmed3f(x, lo, hi);
     const float rr = even ? __builtin_rintf(x) : round_half_away(x);
     return (int32_t)rr + zp;
 }
@@ -202,10 +203,11 @@ __device__ __forceinline__ int32_t requant_clamped(float x, int32_t zp, bool u8,
 // correctly rounded +,-,*,/ and floor, so the host evaluates the same bits.
 __device__ __forceinline__ float tanh_cw(float x)
 {
-    const float ax = __builtin_fabsf(x);
-    if (!(ax < 9.0f)) {
-        return (x != x) ? x : __builtin_copysignf(1.0f, x);
-    }
+    // |x| >= 9 (and NaN) is selected at the end rather than branched to: the
+    // reduction runs on min(|x|, 9), the same operations for every |x| < 9
+    const float ax0 = __builtin_fabsf(x);
+    const bool big = !(ax0 < 9.0f);
+    const float ax = big ? 9.0f : ax0;
     const float y = __fadd_rn(ax, ax);
     const float n = __builtin_floorf(__fadd_rn(__fmul_rn(y, 1.44269504088896341f), 0.5f));
     const float r = __fsub_rn(__fsub_rn(y, __fmul_rn(n, 0.693145751953125f)),
@@ -223,7 +225,7 @@ __device__ __forceinline__ float tanh_cw(float x)
     const float scale = __int_as_float((127 - ni) << 23);
     const float t = __fmul_rn(q, scale);
     const float th = __fdiv_rn(__fsub_rn(1.0f, t), __fadd_rn(1.0f, t));
-    return __builtin_copysignf(th, x);
+    return big ? ((x != x) ? x : __builtin_copysignf(1.0f, x)) : __builtin_copysignf(th, x);
 }
 
 // GELU, tanh form, in nnops' operation order: 0.5x(1 + tanh(c(x + 0.044715x^3))).

@@ -2260,22 +2260,31 @@ __global__ __launch_bounds__(256, 1) void gemm_q4_1_f32(Q41Kern p)
 __global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, int k, _Float16* hi, _Float16* lo,
                                                    float* row_scale)
 {
+    constexpr int kHold = 8;                 // 4-value groups a thread keeps between the passes (k <= 8192)
     __shared__ float red[4];
     const int m = blockIdx.x;
     const float* row = a + (int64_t)m * lda;
     // 16-byte loads where the row allows (k % 4 == 0 always: k % 64 == 0)
     const bool vec = ((uintptr_t)row & 15) == 0;
+    auto load4 = [&](int i) {
+        return vec ? *reinterpret_cast<const v4f*>(row + i) : v4f{row[i], row[i + 1], row[i + 2], row[i + 3]};
+    };
+    v4f held[kHold];
     float mx = 0.0f;
-    if (vec) {
-        for (int i = 4 * (int)threadIdx.x; i < k; i += 1024) {
-            const v4f x = *reinterpret_cast<const v4f*>(row + i);
-            mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[0])), __builtin_fabsf(x[1]));
-            mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[2])), __builtin_fabsf(x[3]));
-        }
-    } else {
-        for (int i = threadIdx.x; i < k; i += 256) {
-            mx = fmaxf(mx, __builtin_fabsf(row[i]));
-        }
+#pragma unroll
+    for (int u = 0; u < kHold; ++u) {
+        const int i = 4 * (int)threadIdx.x + 1024 * u;
+        held[u] = i < k ? load4(i) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < kHold; ++u) {
+        mx = fmaxf(fmaxf(mx, __builtin_fabsf(held[u][0])), __builtin_fabsf(held[u][1]));
+        mx = fmaxf(fmaxf(mx, __builtin_fabsf(held[u][2])), __builtin_fabsf(held[u][3]));
+    }
+    for (int i = 4 * (int)threadIdx.x + 1024 * kHold; i < k; i += 1024) {
+        const v4f x = load4(i);
+        mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[0])), __builtin_fabsf(x[1]));
+        mx = fmaxf(fmaxf(mx, __builtin_fabsf(x[2])), __builtin_fabsf(x[3]));
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -2298,14 +2307,7 @@ __global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, 
     }
     _Float16* h_row = hi + (int64_t)m * k;
     _Float16* l_row = lo + (int64_t)m * k;
-    // 4 values per thread and step: the row is still in this CU's cache
-    for (int i = 4 * (int)threadIdx.x; i < k; i += 1024) {
-        v4f x;
-        if (vec) {
-            x = *reinterpret_cast<const v4f*>(row + i);
-        } else {
-            x = v4f{row[i], row[i + 1], row[i + 2], row[i + 3]};
-        }
+    auto put4 = [&](int i, const v4f& x) {
         _Float16 h[4], l[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -2318,6 +2320,16 @@ __global__ __launch_bounds__(256) void split_a_f32(const float* a, int64_t lda, 
         __builtin_memcpy(&lw, l, 8);
         *reinterpret_cast<uint2*>(h_row + i) = hw;
         *reinterpret_cast<uint2*>(l_row + i) = lw;
+    };
+#pragma unroll
+    for (int u = 0; u < kHold; ++u) {
+        const int i = 4 * (int)threadIdx.x + 1024 * u;
+        if (i < k) {
+            put4(i, held[u]);
+        }
+    }
+    for (int i = 4 * (int)threadIdx.x + 1024 * kHold; i < k; i += 1024) {
+        put4(i, load4(i));
     }
 }
 
