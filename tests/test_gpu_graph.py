@@ -58,15 +58,18 @@ def test_int8_routes_under_graph_replay(M, K, N, out, trans_b):
 
 
 @pytest.mark.parametrize("trans_b", [True, False])
-def test_q4_1_under_graph_replay(trans_b):
+@pytest.mark.parametrize("a_dt", ["f16", "f32"])
+def test_q4_1_under_graph_replay(trans_b, a_dt):
     """Both Q4_1 layouts; blocks along N at M <= 2 is the one-launch GEMV whose
-    arrival counters carry the launch epoch baked into the graph."""
+    arrival counters carry the launch epoch baked into the graph; M=8 with
+    blocks along K is the matrix-core GEMV; f32 activations at M=256 are
+    split into two f16 parts in the workspace before the ring."""
     import torch
-    announce(f"graph q4_1 trans_b={trans_b}")
+    announce(f"graph q4_1 trans_b={trans_b} a={a_dt}")
     K, N = 4096, 2048
     blk = dev(dg.q4_1_blocks(5, N, K) if trans_b else dg.q4_1_blocks(5, K, N))
-    for M in (1, 2, 256):
-        a = dev(dg.normal(6 + M, (M, K)).astype(np.float16))
+    for M in (1, 2, 8, 256):
+        a = dev(dg.normal(6 + M, (M, K)).astype(np.float16 if a_dt == "f16" else np.float32))
         c = torch.zeros((M, N), dtype=torch.float32, device="cuda")
         ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
 
