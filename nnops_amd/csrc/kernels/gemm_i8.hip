@@ -651,6 +651,8 @@ struct RingSplit {
     int splits;        // K ranges per output tile
     int kt_per;        // staged k steps per split (the last split takes the rest)
     int32_t* part;     // RING_PART: [splits][M][N] raw accumulators
+    float row_k;       // gemm_i8_reduce_q: RN(s_a / s_out) and RN(1 / s_out), the
+    float inv_out;     // host's correctly rounded f32 quotients (the device's bits)
 };
 
 __device__ __forceinline__ void block_barrier()
@@ -1524,84 +1526,84 @@ __global__ __launch_bounds__(256) void gemm_i8_reduce(GemmI8Kern p, RingSplit sk
 // float epilogue and residual order fixed at compile time: every load a
 // thread needs (its splits' partial groups, the column tables and the
 // residual word) is issued before the first is used, and the arithmetic is
-// straight-line. One thread per 4-column group; element for element the
-// operations of epi_value, so the bytes equal gemm_i8_reduce's.
+// straight-line. One thread per 4-column group, grid.y walking the rows (no
+// per-thread division for the row); element for element the operations of
+// epi_value, so the bytes equal gemm_i8_reduce's.
 template <int ACT, bool FEP, bool ADD, bool PRE>
 __global__ __launch_bounds__(256) void gemm_i8_reduce_q(GemmI8Kern p, RingSplit sk)
 {
     const EpiParams& ep = p.ep;
-    const int groups = p.n >> 2;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= (int64_t)p.m * groups) {
+    const int nb = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    if (nb >= p.n) {
         return;
-    }
-    const int m = (int)(gid / groups);
-    const int nb = (int)(gid - (int64_t)m * groups) * 4;
-    const int64_t slab = (int64_t)p.m * p.n;
-    const int32_t* src = sk.part + (int64_t)m * p.n + nb;
-    v4i raw = v4i{0, 0, 0, 0};
-    int s = 0;
-    for (; s + 3 < sk.splits; s += 4) {
-        const v4i x0 = *reinterpret_cast<const v4i*>(src + s * slab);
-        const v4i x1 = *reinterpret_cast<const v4i*>(src + (s + 1) * slab);
-        const v4i x2 = *reinterpret_cast<const v4i*>(src + (s + 2) * slab);
-        const v4i x3 = *reinterpret_cast<const v4i*>(src + (s + 3) * slab);
-        raw += (x0 + x1) + (x2 + x3);
-    }
-    for (; s < sk.splits; ++s) {
-        raw += *reinterpret_cast<const v4i*>(src + s * slab);
-    }
-    int8_t* c8 = static_cast<int8_t*>(p.c) + (int64_t)m * p.ldc_bytes + nb;
-    uint32_t oldw = 0;
-    if constexpr (ADD) {
-        oldw = *reinterpret_cast<const uint32_t*>(c8);
     }
     const v4f sb = ep.s_b != nullptr ? *reinterpret_cast<const v4f*>(ep.s_b + nb)
                                      : v4f{ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar, ep.s_b_scalar};
     const v4i bias = ep.bias != nullptr ? *reinterpret_cast<const v4i*>(ep.bias + nb) : v4i{0, 0, 0, 0};
     const bool u8 = ep.out_kind == NNOPS_OUT_U8;
     const bool even = ep.round_even != 0;
-    const float row_k = __fdiv_rn(ep.s_a_scalar, ep.s_out);
-    const float inv_out = __fdiv_rn(1.0f, ep.s_out);
+    const float row_k = sk.row_k;
+    const float inv_out = sk.inv_out;
     const bool clip = !(ep.min_clip == -__builtin_inff() && ep.max_clip == __builtin_inff());
-    uint32_t outw = 0;
+    const int64_t slab = (int64_t)p.m * p.n;
+    for (int m = (int)blockIdx.y; m < p.m; m += (int)gridDim.y) {
+        const int32_t* src = sk.part + (int64_t)m * p.n + nb;
+        v4i raw = v4i{0, 0, 0, 0};
+        int s = 0;
+        for (; s + 3 < sk.splits; s += 4) {
+            const v4i x0 = *reinterpret_cast<const v4i*>(src + s * slab);
+            const v4i x1 = *reinterpret_cast<const v4i*>(src + (s + 1) * slab);
+            const v4i x2 = *reinterpret_cast<const v4i*>(src + (s + 2) * slab);
+            const v4i x3 = *reinterpret_cast<const v4i*>(src + (s + 3) * slab);
+            raw += (x0 + x1) + (x2 + x3);
+        }
+        for (; s < sk.splits; ++s) {
+            raw += *reinterpret_cast<const v4i*>(src + s * slab);
+        }
+        int8_t* c8 = static_cast<int8_t*>(p.c) + (int64_t)m * p.ldc_bytes + nb;
+        uint32_t oldw = 0;
+        if constexpr (ADD) {
+            oldw = *reinterpret_cast<const uint32_t*>(c8);
+        }
+        uint32_t outw = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        int32_t v = raw[e] + bias[e];
-        int32_t q;
-        if constexpr (!FEP) {
-            if constexpr (ACT == NNOPS_ACT_RELU) {
-                v = v < 0 ? 0 : v;
-            }
-            q = requant_clamped(__fmul_rn((float)v, __fmul_rn(row_k, sb[e])), ep.zp_out, u8, even);
-        } else {
-            float f = __fmul_rn((float)v, __fmul_rn(ep.s_a_scalar, sb[e]));
-            float res = 0.0f;
-            if constexpr (ADD) {
-                const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
-                const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
-                res = __fmul_rn((float)(old - ep.zp_out), ep.s_out);
-                if constexpr (PRE) {
+        for (int e = 0; e < 4; ++e) {
+            int32_t v = raw[e] + bias[e];
+            int32_t q;
+            if constexpr (!FEP) {
+                if constexpr (ACT == NNOPS_ACT_RELU) {
+                    v = v < 0 ? 0 : v;
+                }
+                q = requant_clamped(__fmul_rn((float)v, __fmul_rn(row_k, sb[e])), ep.zp_out, u8, even);
+            } else {
+                float f = __fmul_rn((float)v, __fmul_rn(ep.s_a_scalar, sb[e]));
+                float res = 0.0f;
+                if constexpr (ADD) {
+                    const uint32_t ob = (oldw >> (8 * e)) & 0xffu;
+                    const int32_t old = u8 ? (int32_t)ob : (int32_t)(int8_t)ob;
+                    res = __fmul_rn((float)(old - ep.zp_out), ep.s_out);
+                    if constexpr (PRE) {
+                        f = __fadd_rn(f, res);
+                    }
+                }
+                if (clip) {   // the default -inf / +inf clip is the identity
+                    f = f < ep.min_clip ? ep.min_clip : f;
+                    f = ep.max_clip < f ? ep.max_clip : f;
+                }
+                if constexpr (ACT == NNOPS_ACT_RELU) {
+                    f = f > 0.0f ? f : 0.0f;
+                } else if constexpr (ACT == NNOPS_ACT_GELU) {
+                    f = gelu_tanh(f);
+                }
+                if constexpr (ADD && !PRE) {
                     f = __fadd_rn(f, res);
                 }
+                q = requant_clamped(div_by_fixed(f, ep.s_out, inv_out), ep.zp_out, u8, even);
             }
-            if (clip) {   // the default -inf / +inf clip is the identity
-                f = f < ep.min_clip ? ep.min_clip : f;
-                f = ep.max_clip < f ? ep.max_clip : f;
-            }
-            if constexpr (ACT == NNOPS_ACT_RELU) {
-                f = f > 0.0f ? f : 0.0f;
-            } else if constexpr (ACT == NNOPS_ACT_GELU) {
-                f = gelu_tanh(f);
-            }
-            if constexpr (ADD && !PRE) {
-                f = __fadd_rn(f, res);
-            }
-            q = requant_clamped(div_by_fixed(f, ep.s_out, inv_out), ep.zp_out, u8, even);
+            outw |= ((uint32_t)q & 0xffu) << (8 * e);
         }
-        outw |= ((uint32_t)q & 0xffu) << (8 * e);
+        *reinterpret_cast<uint32_t*>(c8) = outw;
     }
-    *reinterpret_cast<uint32_t*>(c8) = outw;
 }
 
 // ---------------------------------------------------------------------------
@@ -2706,13 +2708,16 @@ void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
 {
     const int64_t groups = (int64_t)k.m * (k.n / 4);
     if (sk.splits <= 8 && reduce_q_ok(k)) {
-        const dim3 grid((unsigned)((groups + 255) / 256));
+        const dim3 grid((unsigned)((k.n / 4 + 255) / 256), (unsigned)std::min<int64_t>(k.m, 65535));
+        RingSplit q = sk;
+        q.row_k = k.ep.s_a_scalar / k.ep.s_out;
+        q.inv_out = 1.0f / k.ep.s_out;
         if (k.ep.act == NNOPS_ACT_GELU) {
-            launch_reduce_q_act<NNOPS_ACT_GELU>(k, sk, grid, s);
+            launch_reduce_q_act<NNOPS_ACT_GELU>(k, q, grid, s);
         } else if (k.ep.act == NNOPS_ACT_RELU) {
-            launch_reduce_q_act<NNOPS_ACT_RELU>(k, sk, grid, s);
+            launch_reduce_q_act<NNOPS_ACT_RELU>(k, q, grid, s);
         } else {
-            launch_reduce_q_act<NNOPS_ACT_NONE>(k, sk, grid, s);
+            launch_reduce_q_act<NNOPS_ACT_NONE>(k, q, grid, s);
         }
         return;
     }
