@@ -1708,6 +1708,24 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_lds(GemmI8Kern p)
     const int8_t* a_row = p.a + (int64_t)(a_live ? arow : 0) * p.lda;
     const int kq = (lane >> 4) * 16;
     int8_t* st = stage[wave];
+    // A plain int32 destination (no zero-point terms) takes only the bias and
+    // Relu; its bias word is loaded now, off the output pass's critical path
+    const bool plain32 = p.ep.out_kind == NNOPS_OUT_S32 && !p.ep.compensate;
+    const int n_out = n0 + (lane & 15);
+    int32_t bias_n = 0;
+    if (plain32 && wave == 0 && p.ep.bias != nullptr && n_out < p.n) {
+        bias_n = p.ep.bias[n_out];
+    }
+    // the general output pass's column and row constants, likewise up front
+    EpiCol col{};
+    EpiRow rws[4]{};
+    if (!plain32 && wave == 0 && n_out < p.n) {
+        col = epi_col(p.ep, n_out);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            rws[r] = epi_row(p.ep, min(4 * (lane >> 4) + r, p.m - 1));
+        }
+    }
 
     v4i acc = {0, 0, 0, 0};
     for (int kb = wave * KW; kb < p.k; kb += W * KW) {
@@ -1744,18 +1762,29 @@ __global__ __launch_bounds__(W * 64) void gemv_i8_lds(GemmI8Kern p)
         acc += red[w][lane];
     }
     // 16x16 layout: lane holds column (lane & 15), rows 4*(lane/16) + r.
-    const int n = n0 + (lane & 15);
+    const int n = n_out;
     if (n >= p.n) {
         return;
     }
-    const EpiCol c = epi_col(p.ep, n);
+    if (plain32) {
+        const bool relu = p.ep.act == NNOPS_ACT_RELU;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * (lane >> 4) + r;
+            if (m < p.m) {
+                const int32_t v = acc[r] + bias_n;
+                reinterpret_cast<int32_t*>(static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes)[n] =
+                    (relu && v < 0) ? 0 : v;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int m = 4 * (lane >> 4) + r;
         if (m < p.m) {
-            const EpiRow row = epi_row(p.ep, m);
             char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
-            epi_store(p.ep, row, c, acc[r], crow, n);
+            epi_store(p.ep, rws[r], col, acc[r], crow, n);
         }
     }
 }
