@@ -645,6 +645,47 @@ __device__ __forceinline__ void buffer_load_lds16(BufRsrc r, int8_t* lds, int vo
 #endif
 }
 
+// Stores and loads with the sc1 cache policy: coherent at device scope (the
+// lowering of an agent-scope atomic store / load) without a cache-wide fence;
+// how the K splits of a one-launch kernel hand their partial sums over.
+__device__ __forceinline__ void buffer_store4_sc1(BufRsrc r, int32_t v, int voff)
+{
+#if __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, 0, 16);
+#else
+    (void)r, (void)v, (void)voff;
+#endif
+}
+
+__device__ __forceinline__ void buffer_store8_sc1(BufRsrc r, uint64_t v, int voff)
+{
+#if __HIP_DEVICE_COMPILE__
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i, v), r, voff, 0, 16);
+#else
+    (void)r, (void)v, (void)voff;
+#endif
+}
+
+__device__ __forceinline__ uint64_t buffer_load8_sc1(BufRsrc r, int voff)
+{
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 16));
+#else
+    (void)r, (void)voff;
+    return 0;
+#endif
+}
+
+__device__ __forceinline__ v4i buffer_load16_sc1(BufRsrc r, int voff)
+{
+#if __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16);
+#else
+    (void)r, (void)voff;
+    return v4i{0, 0, 0, 0};
+#endif
+}
+
 enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2, RING_FP = 3 };
 
 struct RingSplit {
@@ -653,6 +694,8 @@ struct RingSplit {
     int32_t* part;     // RING_PART: [splits][M][N] raw accumulators
     float row_k;       // gemm_i8_reduce_q: RN(s_a / s_out) and RN(1 / s_out), the
     float inv_out;     // host's correctly rounded f32 quotients (the device's bits)
+    uint64_t* flag;    // gemv_i8_kn_tr: [column groups][splits] split-completion flags
+    uint64_t epoch;    // the launch's flag value (graph replays repeat it), never 0
 };
 
 __device__ __forceinline__ void block_barrier()
@@ -1955,9 +1998,14 @@ __device__ __forceinline__ void transpose4x4_bytes(uint32_t r0, uint32_t r1, uin
 // wave w streams its own contiguous run of 64-row steps (16 CB bytes per
 // row, whole cache lines, in 1 KiB DMA instructions) through an NSW-slot
 // ring of its own, with the step's A fragments (16 bytes per lane, from L2)
-// loaded beside it. The waves meet in LDS and the workgroup
-// writes its int32 partials [split][M][N]; gemm_i8_reduce sums the splits
-// and runs the output pass.
+// loaded beside it. The waves meet in LDS. With one K range the workgroup
+// runs the output pass; with several it writes its int32 partials
+// [split][M][N] (device-coherent sc1 stores), then its flag (the launch
+// epoch), then reads every split's flag: a workgroup that finds them all set
+// sums the column group's splits in split order and runs the output pass --
+// the last to arrive always does, and one that reads the flags at the same
+// moment writes the same bits -- then clears the flags, so a replayed graph
+// (same epoch) finds them clear. No second launch.
 // ---------------------------------------------------------------------------
 template <int NSW, int CB>
 __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk, int groups)
@@ -2066,32 +2114,104 @@ __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk,
         }
     }
     __syncthreads();
-    if (wave != 0) {
-        return;
-    }
-    // 16x16 layout: lane holds column (lane & 15) of the block, rows 4 (lane >> 4) + r;
-    // one K range: the output pass here, else the partials for gemm_i8_reduce
-    int32_t* part = sk.part + (int64_t)sp * p.m * p.n;
+    // 16x16 layout: lane holds column (lane & 15) of the block, rows 4 (lane >> 4) + r
+    if (sk.splits == 1) {
+        if (wave != 0) {
+            return;
+        }
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-        v4i v = acc[cb] + red[(0 * CB + cb) * 64 + lane] + red[(1 * CB + cb) * 64 + lane] +
-                red[(2 * CB + cb) * 64 + lane];
-        const int n = n0 + 16 * cb + (lane & 15);
-        if (n < p.n) {
-            const EpiCol c = epi_col(p.ep, n);
+        for (int cb = 0; cb < CB; ++cb) {
+            const v4i v = acc[cb] + red[(0 * CB + cb) * 64 + lane] + red[(1 * CB + cb) * 64 + lane] +
+                          red[(2 * CB + cb) * 64 + lane];
+            const int n = n0 + 16 * cb + (lane & 15);
+            if (n < p.n) {
+                const EpiCol c = epi_col(p.ep, n);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = 4 * (lane >> 4) + r;
-                if (m < p.m) {
-                    if (sk.splits == 1) {
-                        epi_store(p.ep, epi_row(p.ep, m), c, v[r], static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes,
-                                  n);
-                    } else {
-                        part[(int64_t)m * p.n + n] = v[r];
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 4 * (lane >> 4) + r;
+                    if (m < p.m) {
+                        epi_store(p.ep, epi_row(p.ep, m), c, v[r],
+                                  static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes, n);
                     }
                 }
             }
         }
+        return;
+    }
+    // the split's partials (byte offsets fit 32 bits: splits * M * N * 4 <
+    // 2^31, checked by the plan), then its flag
+    const BufRsrc rpart = buffer_rsrc(sk.part);
+    const BufRsrc rflag = buffer_rsrc(sk.flag + (int64_t)cg * sk.splits);
+    __shared__ int s_all;
+    if (wave == 0) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const v4i v = acc[cb] + red[(0 * CB + cb) * 64 + lane] + red[(1 * CB + cb) * 64 + lane] +
+                          red[(2 * CB + cb) * 64 + lane];
+            const int n = n0 + 16 * cb + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * (lane >> 4) + r;
+                if (n < p.n && m < p.m) {
+                    buffer_store4_sc1(rpart, v[r], ((sp * p.m + m) * p.n + n) * 4);
+                }
+            }
+        }
+        wait_vmcnt<0>();
+        if (lane == 0) {
+            buffer_store8_sc1(rflag, sk.epoch, sp * 8);
+        }
+        wait_vmcnt<0>();
+        const uint64_t f = lane < sk.splits ? buffer_load8_sc1(rflag, lane * 8) : sk.epoch;
+        const bool all = __builtin_amdgcn_ballot_w64(f != sk.epoch) == 0;
+        if (lane == 0) {
+            s_all = all;
+        }
+    }
+    __syncthreads();
+    if (!s_all) {
+        return;
+    }
+    // every split has published: 4 consecutive columns of one row per
+    // thread, the splits summed in split order (exact: integers)
+    const int q = threadIdx.x & (CW / 4 - 1);
+    const int n = n0 + 4 * q;
+    if (n < p.n) {
+        const EpiCol c[4] = {epi_col(p.ep, n), epi_col(p.ep, n + 1), epi_col(p.ep, n + 2), epi_col(p.ep, n + 3)};
+        const bool plain32 = p.ep.out_kind == NNOPS_OUT_S32 && !p.ep.compensate;
+        for (int m = threadIdx.x / (CW / 4); m < p.m; m += 256 / (CW / 4)) {
+            // four splits' loads in flight at a time
+            v4i sum = v4i{0, 0, 0, 0};
+            int sp2 = 0;
+            for (; sp2 + 3 < sk.splits; sp2 += 4) {
+                const int o = ((sp2 * p.m + m) * p.n + n) * 4, st = p.m * p.n * 4;
+                const v4i x0 = buffer_load16_sc1(rpart, o), x1 = buffer_load16_sc1(rpart, o + st);
+                const v4i x2 = buffer_load16_sc1(rpart, o + 2 * st), x3 = buffer_load16_sc1(rpart, o + 3 * st);
+                sum += (x0 + x1) + (x2 + x3);
+            }
+            for (; sp2 < sk.splits; ++sp2) {
+                sum += buffer_load16_sc1(rpart, ((sp2 * p.m + m) * p.n + n) * 4);
+            }
+            char* crow = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes;
+            if (plain32) {
+                // an int32 destination without zero-point terms: bias and Relu
+                const bool relu = p.ep.act == NNOPS_ACT_RELU;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int32_t v = sum[e] + c[e].bias;
+                    reinterpret_cast<int32_t*>(crow)[n + e] = (relu && v < 0) ? 0 : v;
+                }
+                continue;
+            }
+            const EpiRow row = epi_row(p.ep, m);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                epi_store(p.ep, row, c[e], sum[e], crow, n + e);
+            }
+        }
+    }
+    if ((int)threadIdx.x < sk.splits) {
+        buffer_store8_sc1(rflag, 0ull, (int)threadIdx.x * 8);
     }
 }
 
@@ -2406,7 +2526,7 @@ struct KnPlan {
 inline int kn_mt(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 struct WsPlan {
-    size_t r_a = 0, r_b = 0, a_t = 0, b_t = 0, part = 0, total = 0;
+    size_t r_a = 0, r_b = 0, a_t = 0, b_t = 0, part = 0, flag = 0, total = 0;
     int64_t kp = 0;
     RingPlan ring;
     KnPlan kn;
@@ -2566,6 +2686,10 @@ WsPlan plan_workspace(const NnopsGemmI8Args& g)
     w.kn = plan_kn(g);
     if (w.kn.cpl != 0) {
         w.part = off; off += align_up((size_t)w.kn.splits * (size_t)g.m * (size_t)g.n * 4);
+        if (w.kn.tr && w.kn.splits > 1) {
+            // the splits' completion flags (gemv_i8_kn_tr meets them in place)
+            w.flag = off; off += align_up((size_t)w.kn.chunks * (size_t)w.kn.splits * 8);
+        }
         w.total = off;
         return w;
     }
@@ -2757,18 +2881,17 @@ void launch_reduce(const GemmI8Kern& k, const RingSplit& sk, hipStream_t s)
     }
 }
 
-void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, hipStream_t s)
+void launch_kn(const GemmI8Kern& k, const KnPlan& r, int32_t* part, uint64_t* flag, hipStream_t s)
 {
-    RingSplit sk;
+    RingSplit sk{};
     sk.splits = r.splits;
     sk.kt_per = 0;
     sk.part = part;
     if (r.tr) {
+        sk.flag = flag;
+        sk.epoch = next_launch_epoch();
         NNOPS_LAUNCH((gemv_i8_kn_tr<2, 8>), dim3((unsigned)(r.chunks * r.splits)), dim3(256), 0, s, k, sk,
                      r.chunks);
-        if (r.splits > 1) {
-            launch_reduce(k, sk, s);
-        }
         return;
     }
     KnSplit ks;
@@ -3040,7 +3163,7 @@ extern "C" int nnops_hip_gemm_i8(const NnopsGemmI8Args* g, void* workspace, size
     const bool fullk = aligned && (g->k % 64 == 0);
     const int epi = choose_epi(*g, e);
     if (w.kn.cpl != 0) {
-        launch_kn(k, w.kn, reinterpret_cast<int32_t*>(ws + w.part), s);
+        launch_kn(k, w.kn, reinterpret_cast<int32_t*>(ws + w.part), reinterpret_cast<uint64_t*>(ws + w.flag), s);
     } else if (g->m <= 16 && aligned && g->k % 64 == 0 && gemv_lds_ok(*g)) {
         NNOPS_LAUNCH((gemv_i8_lds<4>), dim3((unsigned)((g->n + 15) / 16)), dim3(256), 0, s, k);
     } else if (g->m <= 4 && aligned) {

@@ -281,6 +281,33 @@ def test_kn_gemv_weight_zero_point_and_tables(M):
     np.testing.assert_array_equal(got, oracle.gemm_i8(a, b, zp_b=zpb))
 
 
+def test_kn_split_meeting_reuses_one_workspace():
+    """The [K,N] skinny route meets its K splits inside the launch through
+    completion flags in the workspace: a workspace filled with 0xff bytes
+    (flag words that are not the launch's epoch), then the same workspace
+    again (the flags left cleared), then a smaller call over it, each bit for
+    bit against the oracle, s32 and s8 destinations."""
+    import torch
+    ws = torch.full((32 << 20,), 0xff, dtype=torch.uint8, device="cuda")
+    for M, K, N, out in [(16, 4096, 2048, "s32"), (16, 4096, 2048, "s8"), (5, 1024, 1000, "s32"),
+                         (12, 2048, 4096, "s8")]:
+        announce(f"[K,N] split meeting {M}x{K}x{N} {out}")
+        a = dg.act_s8(700 + M, (M, K))
+        b = dg.ints(701 + N, (K, N), -127, 127)
+        sb = dg.uniform(702, (N,), 0.002, 0.01)
+        bias = dg.ints(703, (N,), -3000, 3000, np.int32)
+        kind = na.OUT_S32 if out == "s32" else na.OUT_S8
+        c = torch.zeros((M, N), dtype=torch.int32 if out == "s32" else torch.int8, device="cuda")
+        for rep in range(2):
+            c.zero_()
+            na.gemm_i8(dev(a), dev(b), c, trans_b=False, out_kind=kind, bias=dev(bias), s_a=0.02, s_b=dev(sb),
+                       s_out=0.05, act=na.ACT_RELU, workspace=ws)
+            torch.cuda.synchronize()
+            want = oracle.gemm_i8(a, b, bias=bias, out_kind=oracle.OUT_S32 if out == "s32" else oracle.OUT_S8,
+                                  s_a=0.02, s_b=sb, s_out=0.05, act=oracle.ACT_RELU)
+            np.testing.assert_array_equal(host(c), want, err_msg=f"call {rep}")
+
+
 @pytest.mark.parametrize("trans_b", [False, True])
 @pytest.mark.parametrize("s_out", [0.05, 2.0])
 def test_config5_full_workload_every_row(trans_b, s_out):
