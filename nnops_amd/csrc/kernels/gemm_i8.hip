@@ -2162,8 +2162,11 @@ __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk,
             buffer_store8_sc1(rflag, sk.epoch, sp * 8);
         }
         wait_vmcnt<0>();
-        const uint64_t f = lane < sk.splits ? buffer_load8_sc1(rflag, lane * 8) : sk.epoch;
-        const bool all = __builtin_amdgcn_ballot_w64(f != sk.epoch) == 0;
+        bool all = true;
+        for (int f0 = 0; f0 < sk.splits; f0 += 64) {
+            const uint64_t f = f0 + lane < sk.splits ? buffer_load8_sc1(rflag, (f0 + lane) * 8) : sk.epoch;
+            all = all && __builtin_amdgcn_ballot_w64(f != sk.epoch) == 0;
+        }
         if (lane == 0) {
             s_all = all;
         }
@@ -2210,8 +2213,8 @@ __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk,
             }
         }
     }
-    if ((int)threadIdx.x < sk.splits) {
-        buffer_store8_sc1(rflag, 0ull, (int)threadIdx.x * 8);
+    for (int f = (int)threadIdx.x; f < sk.splits; f += (int)blockDim.x) {
+        buffer_store8_sc1(rflag, 0ull, f * 8);
     }
 }
 
@@ -2687,7 +2690,7 @@ WsPlan plan_workspace(const NnopsGemmI8Args& g)
     if (w.kn.cpl != 0) {
         w.part = off; off += align_up((size_t)w.kn.splits * (size_t)g.m * (size_t)g.n * 4);
         if (w.kn.tr && w.kn.splits > 1) {
-            // the splits' completion flags (gemv_i8_kn_tr meets them in place)
+            // the splits' completion flags (gemv_i8_kn_tr meets them in the launch)
             w.flag = off; off += align_up((size_t)w.kn.chunks * (size_t)w.kn.splits * 8);
         }
         w.total = off;

@@ -282,15 +282,17 @@ def test_kn_gemv_weight_zero_point_and_tables(M):
 
 
 def test_kn_split_meeting_reuses_one_workspace():
-    """The [K,N] skinny route meets its K splits inside the launch through
-    completion flags in the workspace: a workspace filled with 0xff bytes
+    """The [K,N] MFMA GEMV (3 <= M <= 16) meets its K splits inside the
+    launch through completion flags in the workspace (the column GEMV at
+    M <= 2, which sums its splits in a second launch, rides along): a workspace filled with 0xff bytes
     (flag words that are not the launch's epoch), then the same workspace
     again (the flags left cleared), then a smaller call over it, each bit for
     bit against the oracle, s32 and s8 destinations."""
     import torch
     ws = torch.full((32 << 20,), 0xff, dtype=torch.uint8, device="cuda")
     for M, K, N, out in [(16, 4096, 2048, "s32"), (16, 4096, 2048, "s8"), (5, 1024, 1000, "s32"),
-                         (12, 2048, 4096, "s8")]:
+                         (12, 2048, 4096, "s8"), (1, 4096, 11008, "s32"), (2, 1024, 8256, "s8"),
+                         (1, 2048, 1040, "s8")]:
         announce(f"[K,N] split meeting {M}x{K}x{N} {out}")
         a = dg.act_s8(700 + M, (M, K))
         b = dg.ints(701 + N, (K, N), -127, 127)
