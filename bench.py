@@ -925,10 +925,10 @@ LINE_TRAFFIC = {
     "cfg1_s32_128x1024x1024": ["gemm_i8_ring_cfg1"],
     "cfg3_int8_gemv_m1_kn_s32": ["gemv_i8_kn_cfg3_m1", "gemm_i8_reduce_cfg3_m1"],
     "cfg3_int8_gemv_m1_kn_s8": ["gemv_i8_kn_cfg3_m1", "gemm_i8_reduce_cfg3_m1"],
-    "cfg3_int8_gemv_m4_kn_s32": ["gemv_i8_kn_tr_cfg3_m4_m16", "gemm_i8_reduce_cfg3_m4"],
-    "cfg3_int8_gemv_m4_kn_s8": ["gemv_i8_kn_tr_cfg3_m4_m16", "gemm_i8_reduce_q_cfg3_m4"],
-    "cfg3_int8_gemv_m16_kn_s32": ["gemv_i8_kn_tr_cfg3_m4_m16", "gemm_i8_reduce_cfg3_m16"],
-    "cfg3_int8_gemv_m16_kn_s8": ["gemv_i8_kn_tr_cfg3_m4_m16", "gemm_i8_reduce_q_cfg3_m16"],
+    "cfg3_int8_gemv_m4_kn_s32": ["gemv_i8_kn_tr_cfg3_m4_m16"],
+    "cfg3_int8_gemv_m4_kn_s8": ["gemv_i8_kn_tr_cfg3_m4_m16"],
+    "cfg3_int8_gemv_m16_kn_s32": ["gemv_i8_kn_tr_cfg3_m4_m16"],
+    "cfg3_int8_gemv_m16_kn_s8": ["gemv_i8_kn_tr_cfg3_m4_m16"],
     "cfg3_int8_gemv_m1_nk_s32": ["gemv_i8_rows_cfg3_m1"],
     "cfg3_int8_gemv_m4_nk_s32": ["gemv_i8_rows_cfg3_m4"],
     "cfg3_int8_gemv_m16_nk_s32": ["gemv_i8_lds_cfg3_m16"],
