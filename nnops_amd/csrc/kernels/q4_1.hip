@@ -1298,6 +1298,46 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
         return;
     }
     // 1024 columns x MT rows: 4 consecutive columns per thread and row
+    if constexpr (MT == 1 && W == 8) {
+        // one row: two threads per column quad, each summing its half of the
+        // splits in split order with every load in flight at once (half 0
+        // takes splits 0 .. 15, half 1 the rest), then half 0 adds half 1's sum
+        static_assert(kKnNS * kKnStage >= 256 * 16, "the halves meet in the ring");
+        const int half = tid >> 8, q = tid & 255;
+        const int nq = cg * 1024 + 4 * q;
+        const int sa = half ? 16 : 0, sb = half ? kd.splits : min(16, kd.splits);
+        v4f sum = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = sa; s0 < sb; s0 += 16) {
+            v4f part[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int s2 = min(s0 + u, sb - 1);
+                part[u] = __builtin_bit_cast(v4f, q_buffer_load16_sc1(rp, s2 * MT * 4096 + q * 16));
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (s0 + u < sb) {
+                    sum += part[u];
+                }
+            }
+        }
+        v4f* xs = reinterpret_cast<v4f*>(ring);
+        if (half == 1) {
+            xs[q] = sum;
+        }
+        __syncthreads();
+        if (half == 0 && nq < p.n) {
+            if (kd.splits > 16) {
+                sum += xs[q];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (nq + e < p.n) {
+                    store_out(p, 0, nq + e, sum[e]);
+                }
+            }
+        }
+    } else {
     const int n = cg * 1024 + 4 * tid;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -1326,6 +1366,7 @@ __global__ __launch_bounds__(W * 64) void gemv_q4_1_kn_dma(Q41Kern p, KnDma kd)
                 store_out(p, m, n + e, sum[e]);
             }
         }
+    }
     }
     // clear the flags for the next launch on this workspace (a replayed graph
     // reuses the epoch); every split has published by now
