@@ -680,6 +680,20 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
     if (n0 >= nout) {
         return;
     }
+    // GATED: lane r * MT + m finishes output (m, n0 + r); its two bias values
+    // and (add_to) the destination's current value are loaded first, so the
+    // combine after the stream waits on no memory
+    float pre_bg = 0.0f, pre_bu = 0.0f, pre_old = 0.0f;
+    if constexpr (GATED) {
+        const int r = lane / MT, m = lane % MT;
+        if (r < R / 2 && n0 + r < nout && m < p.m) {
+            const FpOut& fo = p.fo;
+            const char* orow = static_cast<const char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
+            pre_old = fp_out_old(fo, orow, n0 + r);
+            pre_bg = bias_at(fo, n0 + r);
+            pre_bu = bias_at(fo, nout + n0 + r);
+        }
+    }
     // A first: its loads retire before the DMA pieces queued behind them
     const uint32_t* A = static_cast<const uint32_t*>(p.a);   // f16 pairs
     uint32_t ah[2][MT][16];
@@ -795,17 +809,34 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
         }
     }
     if constexpr (GATED) {
-        // lanes (r, m) each finish one output: gate product acc[r], value acc[2 + r]
+        // lane r * MT + m finishes output (m, n0 + r) (gate product acc[r],
+        // value acc[R/2 + r]; every lane holds the sums); lane m then writes
+        // row m's pair as one 4-byte word where f16 allows: a 2-byte store
+        // per output costs a read-modify-write each (1.2 us of the launch)
+        static_assert(R / 2 == 2, "one f16 pair per row");
         const FpOut& fo = p.fo;
+        const int r = lane / MT, m = lane % MT;
+        float y = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R / 2; ++r) {
+        for (int rr = 0; rr < R / 2; ++rr) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                const int n = n0 + r;
-                if (lane == r * MT + m && n < nout && m < p.m) {
-                    char* orow = static_cast<char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
-                    fp_out_store(fo, orow, n, fp_out_value(fo, acc[r][m], acc[R / 2 + r][m], fp_out_old(fo, orow, n),
-                                                           bias_at(fo, n), bias_at(fo, nout + n)));
+            for (int mm = 0; mm < MT; ++mm) {
+                if (lane == rr * MT + mm) {
+                    y = fp_out_value(fo, acc[rr][mm], acc[R / 2 + rr][mm], pre_old, pre_bg, pre_bu);
+                }
+            }
+        }
+        const float y1 = __shfl(y, lane + MT, 64);       // lane m: output (m, n0 + 1)
+        if (r == 0 && m < p.m && n0 < nout) {
+            char* orow = static_cast<char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
+            _Float16* h = reinterpret_cast<_Float16*>(orow) + n0;
+            if (n0 + 1 < nout && fo.out_f16 && ((uintptr_t)h & 3) == 0) {
+                const _Float16 pr[2] = {(_Float16)y, (_Float16)y1};
+                *reinterpret_cast<uint32_t*>(h) = __builtin_bit_cast(uint32_t, pr);
+            } else {
+                fp_out_store(fo, orow, n0, y);
+                if (n0 + 1 < nout) {
+                    fp_out_store(fo, orow, n0 + 1, y1);
                 }
             }
         }

@@ -71,6 +71,31 @@ def test_gated_ffn_config4_shape(M, gate):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("M,N", [(1, 1001), (2, 1001), (2, 512)])
+@pytest.mark.parametrize("kw", [dict(gate_activation=na.EP_SILU), dict(gate_activation=na.EP_GELU, add_to=True)])
+def test_gated_gemv_fused_edges(M, N, kw):
+    """The one-launch gated GEMV (K = 4096, M <= 2, f16 X and destination)
+    against the oracle: an odd output count (the last wave's column pair has
+    one member), M = 2 (two rows per wave), the f16 pairs written as one
+    word, and add_to (the destination read before the stream). Its f32
+    destination is compared bit for bit with the two-step form in
+    test_gpu_fused_pass.py."""
+    announce(f"gated gemv M={M} N={N} {kw}")
+    K = 4096
+    f16 = True
+    dt = np.float16
+    x = dg.normal(900 + M, (M, K)).astype(np.float16)
+    blk = dg.q4_1_blocks(901 + N, 2 * N, K)
+    bias = (0.1 * dg.normal(902, (2 * N,))).astype(np.float16 if f16 else np.float32)
+    old = dg.normal(903, (M, N)).astype(dt) if kw.get("add_to") else None
+    got = run_linear(x, blk, 2 * N, gated=True, bias=bias, old=old, f16_out=f16, **kw)
+    want = oracle.q4_1_linear(x, blk, 2 * N, w_round_f16=False, gated=True, out_f16=f16, bias=bias, out=old,
+                              gate_act=GATE[kw["gate_activation"]],
+                              add_to=kw.get("add_to", False)).astype(np.float32)
+    err = norm_err(got, want)
+    assert err <= TOL, err
+
+
 GATED_VARIANTS = [
     dict(gate_activation=na.EP_SILU, gate_alpha=1.702, gate_beta=1.0, gate_limit=7.0),
     dict(gate_activation=na.EP_GELU, gate_beta=0.5, gate_limit=1.5, act=na.EP_RELU),
