@@ -181,6 +181,97 @@ __global__ __launch_bounds__(256) void quantize_kernel(QdqKern p)
     }
 }
 
+// The common shape, an f16 side and one parameter per row (per tensor or per
+// token) with 1024 | cols and 16-byte aligned rows: a wave owns 1024
+// consecutive elements of one row and lane l the elements 8 l .. 8 l + 7 and
+// 512 + 8 l .. + 7, so every vector load and store instruction of the wave
+// covers one contiguous span (1 KiB of f16, 512 bytes of int8), where the
+// general kernels' 16-element chunks per lane touch each line twice, half of
+// it per instruction. The same operations per element as quant_one /
+// dequantize's vector body (fma(q, s, -zp * s): 16 | cols makes every element
+// a body element).
+__host__ __device__ __forceinline__ bool qdq_row_param(const QdqKern& p)
+{
+    return p.dim <= 1 || (p.inner == p.cols && p.dim == p.rows);
+}
+
+__global__ __launch_bounds__(256) void quantize_rows_f16(QdqKern p)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t wblk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t per_row = p.cols / 1024;
+    if (wblk >= p.rows * per_row) {
+        return;
+    }
+    const int64_t r = wblk / per_row;
+    const int64_t c0 = (wblk - r * per_row) * 1024;
+    const int64_t j = p.dim <= 1 ? 0 : r;
+    const float inv = __fdiv_rn(1.0f, qdq_scale(p, j));
+    const float zf = (float)qdq_zero(p, j);
+    const bool u8 = p.y_kind == NNOPS_OUT_U8;
+    const int32_t qmin = u8 ? 0 : -128, qmax = u8 ? 255 : 127;
+    const _Float16* xr = static_cast<const _Float16*>(p.x) + r * p.ld_x + c0;
+    int8_t* yr = static_cast<int8_t*>(p.y) + r * p.ld_y + c0;
+    v4i w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        w[h] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(xr + 512 * h + 8 * lane));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const _Float16* e = reinterpret_cast<const _Float16*>(&w[h]);
+        uint32_t o[2] = {0u, 0u};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            o[q / 4] |= ((uint32_t)quant_one((float)e[q], inv, zf, qmin, qmax) & 0xffu) << (8 * (q % 4));
+        }
+        __builtin_nontemporal_store((uint64_t)o[0] | ((uint64_t)o[1] << 32),
+                                    reinterpret_cast<uint64_t*>(yr + 512 * h + 8 * lane));
+    }
+}
+
+__global__ __launch_bounds__(256) void dequantize_rows_f16(QdqKern p)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t wblk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t per_row = p.cols / 1024;
+    if (wblk >= p.rows * per_row) {
+        return;
+    }
+    const int64_t r = wblk / per_row;
+    const int64_t c0 = (wblk - r * per_row) * 1024;
+    const int64_t j = p.dim <= 1 ? 0 : r;
+    const float sc = qdq_scale(p, j);
+    const float zf = (float)qdq_zero(p, j);
+    const float nzs = __fmul_rn(-zf, sc);
+    const bool u8 = p.x_kind == NNOPS_OUT_U8;
+    const int8_t* xr = static_cast<const int8_t*>(p.x) + r * p.ld_x + c0;
+    _Float16* yr = static_cast<_Float16*>(p.y) + r * p.ld_y + c0;
+    uint64_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        w[h] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(xr + 512 * h + 8 * lane));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        _Float16 e8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t b = (uint32_t)(w[h] >> (8 * q)) & 0xffu;
+            const int32_t v = u8 ? (int32_t)b : (int32_t)(int8_t)b;
+            // the f32 result first, then its f16 rounding (two roundings, as
+            // the reference): the asm keeps the compiler from fusing the pair
+            // into one mixed-precision fma that rounds once
+            float f = __builtin_fmaf((float)v, sc, nzs);
+            asm volatile("" : "+v"(f));
+            e8[q] = (_Float16)f;
+        }
+        v4i o;
+        __builtin_memcpy(&o, e8, 16);
+        __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(yr + 512 * h + 8 * lane));
+    }
+}
+
 // fma(q, s, -zp * s) over each segment's whole 16-element blocks, (q - zp) * s
 // over its last segment % 16 elements.
 __device__ __forceinline__ float dequant_one(const QdqKern& p, int64_t i, int32_t q, float s, float zf)
@@ -235,7 +326,9 @@ __global__ __launch_bounds__(256) void dequantize_kernel(QdqKern p)
                 _Float16 e8[8];
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
-                    e8[q] = (_Float16)y[8 * h + q];
+                    float f = y[8 * h + q];
+                    asm volatile("" : "+v"(f));   // f32 first, then f16 (see dequantize_rows_f16)
+                    e8[q] = (_Float16)f;
                 }
                 v4i o;
                 __builtin_memcpy(&o, e8, 16);
@@ -312,6 +405,20 @@ QdqKern qdq_kern(const NnopsQdqArgs* g)
     return k;
 }
 
+// The rows kernels' conditions: the f16 side, one parameter per row, 1024 |
+// cols, 16-byte aligned f16 rows and 8-byte aligned int8 rows, and for the
+// dequantize the segment a multiple of 16 (every element in a vector body).
+bool rows_fast(const QdqKern& k, bool quantize)
+{
+    const bool f16 = quantize ? k.x_kind == NNOPS_OUT_F16 : k.y_kind == NNOPS_OUT_F16;
+    const void* h = quantize ? k.x : k.y;
+    const void* b = quantize ? k.y : k.x;
+    const int64_t ldh = quantize ? k.ld_x : k.ld_y, ldb = quantize ? k.ld_y : k.ld_x;
+    return f16 && qdq_row_param(k) && k.cols % 1024 == 0 && k.cols > 0 && ((uintptr_t)h % 16) == 0 &&
+           (ldh * 2) % 16 == 0 && ((uintptr_t)b % 8) == 0 && ldb % 8 == 0 &&
+           (quantize || k.segment % 16 == 0) && k.rows * (k.cols / 1024) <= 4 * (int64_t)UINT32_MAX;
+}
+
 }  // namespace
 }  // namespace nnops_amd
 
@@ -324,9 +431,16 @@ extern "C" int nnops_hip_quantize_linear(const NnopsQdqArgs* g, void* stream)
     if (rc >= 0) {
         return rc;
     }
+    const QdqKern k = qdq_kern(g);
+    if (rows_fast(k, true)) {
+        const int64_t waves = g->rows * (g->cols / 1024);
+        NNOPS_LAUNCH(quantize_rows_f16, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), k);
+        return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+    }
     const int64_t threads = g->rows * ((g->cols + 15) / 16);
     NNOPS_LAUNCH(quantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), qdq_kern(g));
+                       static_cast<hipStream_t>(stream), k);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }
 
@@ -337,8 +451,15 @@ extern "C" int nnops_hip_dequantize_linear(const NnopsQdqArgs* g, void* stream)
     if (rc >= 0) {
         return rc;
     }
+    const QdqKern k = qdq_kern(g);
+    if (rows_fast(k, false)) {
+        const int64_t waves = g->rows * (g->cols / 1024);
+        NNOPS_LAUNCH(dequantize_rows_f16, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), k);
+        return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
+    }
     const int64_t threads = g->rows * ((g->cols + 15) / 16);
     NNOPS_LAUNCH(dequantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), qdq_kern(g));
+                       static_cast<hipStream_t>(stream), k);
     return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
 }

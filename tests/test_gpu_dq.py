@@ -314,6 +314,29 @@ def test_quantize_dequantize_linear(shape, n_params, axis, f16, u8):
     assert np.array_equal(gy.view(ui), want_y.view(ui)), np.argwhere(gy.view(ui) != want_y.view(ui))[:5]
 
 
+@pytest.mark.parametrize("cols", [1024, 1000])
+def test_dequantize_f16_rounds_twice(cols):
+    """y = fma(q, s, -zp * s) is rounded to f32 and then to f16, as the
+    reference does: q = -128, s = 0.11721731722354889, zp = 3 gives an f32
+    value whose single rounding to f16 lands one ulp away (a fused
+    mixed-precision fma would). The rows kernel (1024 | cols) and the
+    general one (cols = 1000)."""
+    import torch
+    announce(f"dequantize f16 double rounding cols={cols}")
+    rows = 8
+    q = np.full((rows, cols), -128, np.int8)
+    q[:, 1::2] = dg.ints(77, (rows, cols // 2), -128, 127, np.int8)
+    scale = np.full((rows,), 0.11721731722354889, np.float32)
+    zp = np.full((rows,), 3, np.int8)
+    y = torch.zeros((rows, cols), dtype=torch.float16, device="cuda")
+    dop = na.DequantizeLinear(axis=-1, output_dtype=na.DT_F16)
+    assert dop.compute([na.tensor(y)], [na.tensor(dev(q)), na.tensor(dev(scale)), na.tensor(dev(zp))]) == na.OK
+    torch.cuda.synchronize()
+    want = oracle.dequantize_linear(q, scale, zp.astype(np.int32), out_dtype=np.float16, axis=-1)
+    assert want[0, 0].view(np.uint16) == 0xcbae
+    np.testing.assert_array_equal(host(y).view(np.uint16), want.view(np.uint16))
+
+
 def test_quant_linear_rejects():
     import torch
     announce("qdq rejects")
