@@ -1957,14 +1957,14 @@ __global__ __launch_bounds__(WPB * 64) void gemv_i8_rows(GemmI8Kern p)
 // ---------------------------------------------------------------------------
 // Column GEMV, M <= 16, B n-contiguous ([K][N], the MatMul weight without
 // transpose_b), consumed in place. Lane l of a wave owns CPL consecutive
-// columns (CPL = 16: one 16-byte load per row; CPL = 4: one 4-byte load per
-// row), so every wave load streams 64 * CPL contiguous bytes of one row. Four
+// columns (the launch takes CPL = 4: one 4-byte load per row; the template
+// also takes 16), so every wave load streams 64 * CPL contiguous bytes of one row. Four
 // rows k..k+3 are transposed in registers (two v_perm per column) into one
 // dword of 4 k-bytes per column, which v_dot4 multiplies with A[m][k..k+3]
 // read through the scalar cache (A is uniform across the wave). Split s of S
 // takes k-quads [s Q / S, (s + 1) Q / S) of a column chunk, and the W waves of
-// its workgroup equal parts of that range, summed by LDS atomic adds (W = 16 for
-// 16-column groups; 4 or 8 for 4-column groups); the workgroups write raw
+// its workgroup equal parts of that range, summed by LDS atomic adds (W = 4
+// or 8); the workgroups write raw
 // int32 partials that gemm_i8_reduce sums and passes through the output pass.
 // (Meeting the splits inside the kernel, the last-arriving split summing the
 // others through device-coherent loads, measured slower: the handoff costs
@@ -2568,7 +2568,7 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
         }
         return r;
     }
-    const int cpl = g.m <= 2 ? 16 : 4;
+    const int cpl = 4;
     if (g.n % cpl != 0 || g.n % 4 != 0 || ((uintptr_t)g.b % cpl) != 0 || (g.ldb % cpl) != 0 ||
         ((uintptr_t)g.a % 4) != 0 || (g.lda % 4) != 0) {
         return r;
@@ -2576,18 +2576,14 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
     const int mt = kn_mt(g.m);
     r.cpl = cpl;
     r.chunks = (int)((g.n + 64 * cpl - 1) / (64 * cpl));
-    // 1024-column chunks for M <= 2 (every load a full 1 KiB row segment, the
-    // shape that streams HBM at full rate), 256 columns beyond. K is split so
-    // the workgroups fill the CUs once (no second round whose tail is
-    // exposed), each split at least 16 rows per wave. (Config 3, M = 1: 11
-    // chunks x 23 splits; 16 splits and 46 splits of 8 waves measured the
-    // same or slower.)
-    if (cpl == 16) {
-        r.w = 16;
-    } else {
-        r.w = (mt * cpl >= 64) ? 4 : 8;
-    }
-    const int per_cu = cpl == 16 ? 1 : 2;
+    // 256-column chunks (4 columns per lane: every wave load is 256 bytes of
+    // one row, two whole lines). K is split so the workgroups fill the CUs
+    // about twice, each split at least 16 rows per wave. (Config 3, M = 1:
+    // 43 chunks x 11 splits, 13.0 us per call; 1024-column chunks of 16-byte
+    // lanes, 11 chunks x 23 splits of 16 waves, ran 13.6 at M = 1 and 15.1
+    // against 13.5 at M = 2.)
+    r.w = (mt * cpl >= 64) ? 4 : 8;
+    const int per_cu = 2;
     const int64_t max_splits = std::max<int64_t>(1, g.k / (16 * r.w));
     r.splits = (int)std::min<int64_t>(max_splits, std::max(1, 256 * per_cu / r.chunks));
     if ((int64_t)r.splits * g.m * g.n * 4 >= INT32_MAX) {
@@ -2819,11 +2815,8 @@ template <int MT>
 void launch_kn_mt(const GemmI8Kern& k, const RingSplit& sk, const KnSplit& ks, int cpl, int w, hipStream_t s)
 {
     const dim3 grid((unsigned)(ks.chunks * sk.splits));
-    if (cpl == 16) {
-        if constexpr (MT <= 2) {
-            NNOPS_LAUNCH((gemv_i8_kn<MT, 16, 16, 4>), grid, dim3(1024), 0, s, k, sk, ks);
-        }
-    } else if (w == 4) {
+    (void)cpl;                              // the plan takes 4 columns per lane
+    if (w == 4) {
         NNOPS_LAUNCH((gemv_i8_kn<MT, 4, 4, 4>), grid, dim3(256), 0, s, k, sk, ks);
     } else {
         NNOPS_LAUNCH((gemv_i8_kn<MT, 4, 8, 4>), grid, dim3(512), 0, s, k, sk, ks);
