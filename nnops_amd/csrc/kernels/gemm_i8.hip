@@ -2555,7 +2555,9 @@ KnPlan plan_kn(const NnopsGemmI8Args& g)
     // row segments and ~512 workgroups 15.2 / 16.6 us at M = 4 / 16; 256-byte
     // segments 18.7 / 20.0 (256 workgroups) and 21.8 / 27.0 (512); no K split
     // (86 workgroups) 37.8 / 38.5; at M = 1..2 the column GEMV stays faster,
-    // 13.8 against 14.9 us)
+    // 13.8 against 14.9 us). With the splits meeting in the launch: 14.6 /
+    // 16.5 us at 5 splits, the same at 4, 16.6 / 18.8 at 3, 19.7 / 21.8 at 6
+    // (516 workgroups: a second round), 17.3 / 18.8 at 8.
     if (g.m >= 3 && g.k % 64 == 0 && g.n % 4 == 0 && aligned16(g.b, g.ldb) &&
         aligned16(static_cast<const int8_t*>(g.a), g.lda) && g.k * g.ldb + g.n < (int64_t)INT32_MAX) {
         r.tr = true;
