@@ -666,7 +666,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_lds(Q41Kern p)
 // and value rows p.fo.n + n0, p.fo.n + n0 + 1 (two 5 KiB spans) and combines
 // its two outputs with fp_out_value, from the same f32 products the two-step
 // form stages, so the bits are the two-step form's.
-template <int MT, int R, bool GATED = false>
+template <int MT, int R, bool GATED = false, bool OUT16 = false>
 __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
 {
     constexpr int kRow = 128 * 20;
@@ -679,20 +679,6 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
     const int n0 = (blockIdx.x * 4 + wave) * (GATED ? R / 2 : R);
     if (n0 >= nout) {
         return;
-    }
-    // GATED: lane r * MT + m finishes output (m, n0 + r); its two bias values
-    // and (add_to) the destination's current value are loaded first, so the
-    // combine after the stream waits on no memory
-    float pre_bg = 0.0f, pre_bu = 0.0f, pre_old = 0.0f;
-    if constexpr (GATED) {
-        const int r = lane / MT, m = lane % MT;
-        if (r < R / 2 && n0 + r < nout && m < p.m) {
-            const FpOut& fo = p.fo;
-            const char* orow = static_cast<const char*>(fo.out) + (int64_t)m * fo.ld_out * (fo.out_f16 ? 2 : 4);
-            pre_old = fp_out_old(fo, orow, n0 + r);
-            pre_bg = bias_at(fo, n0 + r);
-            pre_bu = bias_at(fo, nout + n0 + r);
-        }
     }
     // A first: its loads retire before the DMA pieces queued behind them
     const uint32_t* A = static_cast<const uint32_t*>(p.a);   // f16 pairs
@@ -736,6 +722,26 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
                                              NNOPS_LPTR(&stage[wave][q * 1024]), 16, 0, 2);
         }
     }
+    // GATED: lane r * MT + m finishes output (m, n0 + r). Its two bias values
+    // and the destination's current value (add_to) are loaded now, behind
+    // the DMA pieces: three loads every lane issues, at clamped or stand-in
+    // addresses where a value is absent, so the counts the waits below
+    // allow for are fixed (XL), and widened only in the combine.
+    constexpr int XL = GATED ? 3 : 0;
+    using OutBits = std::conditional_t<OUT16, uint16_t, uint32_t>;
+    OutBits x_bg{}, x_bu{}, x_old{};
+    if constexpr (GATED) {
+        const FpOut& fo = p.fo;
+        const int r = lane / MT, m = min(lane % MT, p.m - 1);
+        const int n = min(n0 + min(r, R / 2 - 1), nout - 1);
+        const OutBits* orow = reinterpret_cast<const OutBits*>(static_cast<const char*>(fo.out) +
+                                                                (int64_t)m * fo.ld_out * sizeof(OutBits));
+        const OutBits* bb = fo.bias != nullptr ? static_cast<const OutBits*>(fo.bias) : orow;
+        const int nb = fo.bias != nullptr ? n : 0;
+        x_bg = bb[nb];
+        x_bu = bb[fo.bias != nullptr ? nout + n : 0];
+        x_old = orow[n];
+    }
     const v2h one = __builtin_bit_cast(v2h, 0x3c003c00u);
     float asum[2][MT];
 #pragma unroll
@@ -761,7 +767,7 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
     auto phase = [&]<int RR, int U>() {
         // last byte this (row, half) needs, and the piece holding it
         constexpr int last = RR * kRow + (64 * U + 63) * 20 + 19;
-        wait_vmcnt<C - 1 - last / 1024>();
+        wait_vmcnt<C - 1 - last / 1024 + XL>();
         asm volatile("" ::: "memory");
         const uint32_t* bp = reinterpret_cast<const uint32_t*>(&stage[wave][RR * kRow + (lane + 64 * U) * 20]);
         uint32_t raw[5];
@@ -816,6 +822,18 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
         static_assert(R / 2 == 2, "one f16 pair per row");
         const FpOut& fo = p.fo;
         const int r = lane / MT, m = lane % MT;
+        // the early loads' bits as bias_at / fp_out_old read them (0 when absent)
+        wait_vmcnt<0>();
+        auto widen = [](OutBits v) {
+            if constexpr (OUT16) {
+                return (float)__builtin_bit_cast(_Float16, v);
+            } else {
+                return __builtin_bit_cast(float, v);
+            }
+        };
+        const float pre_bg = fo.bias != nullptr ? widen(x_bg) : 0.0f;
+        const float pre_bu = fo.bias != nullptr ? widen(x_bu) : 0.0f;
+        const float pre_old = fp_out_reads_old(fo) ? widen(x_old) : 0.0f;
         float y = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < R / 2; ++rr) {
@@ -3484,9 +3502,17 @@ extern "C" int nnops_hip_gemm_q4_1_fused(const NnopsGemmQ41Args* g, const NnopsF
         // two outputs per wave, four waves per workgroup
         const unsigned rb = (unsigned)((pass->n + 7) / 8);
         if (g->m == 1) {
-            NNOPS_LAUNCH((gemv_q4_1_pipe<1, 4, true>), dim3(rb), dim3(256), 0, s, k);
+            if (fo.out_f16) {
+                NNOPS_LAUNCH((gemv_q4_1_pipe<1, 4, true, true>), dim3(rb), dim3(256), 0, s, k);
+            } else {
+                NNOPS_LAUNCH((gemv_q4_1_pipe<1, 4, true, false>), dim3(rb), dim3(256), 0, s, k);
+            }
         } else {
-            NNOPS_LAUNCH((gemv_q4_1_pipe<2, 4, true>), dim3(rb), dim3(256), 0, s, k);
+            if (fo.out_f16) {
+                NNOPS_LAUNCH((gemv_q4_1_pipe<2, 4, true, true>), dim3(rb), dim3(256), 0, s, k);
+            } else {
+                NNOPS_LAUNCH((gemv_q4_1_pipe<2, 4, true, false>), dim3(rb), dim3(256), 0, s, k);
+            }
         }
         return hipGetLastError() == hipSuccess ? NNOPS_OK : NNOPS_INTERNAL;
     }
