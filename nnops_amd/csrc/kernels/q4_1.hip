@@ -731,6 +731,8 @@ __global__ __launch_bounds__(256) void gemv_q4_1_pipe(Q41Kern p)
     using OutBits = std::conditional_t<OUT16, uint16_t, uint32_t>;
     OutBits x_bg{}, x_bu{}, x_old{};
     if constexpr (GATED) {
+        // the waits count these loads as issued after the pieces: keep them there
+        asm volatile("" ::: "memory");
         const FpOut& fo = p.fo;
         const int r = lane / MT, m = min(lane % MT, p.m - 1);
         const int n = min(n0 + min(r, R / 2 - 1), nout - 1);
