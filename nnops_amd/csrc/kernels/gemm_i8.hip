@@ -618,6 +618,41 @@ __device__ __forceinline__ v2i lds_read_tr8(const int8_t* p)
 #endif
 }
 
+// The same read as inline assembly, for loops whose LDS stages arrive by DMA:
+// the compiler cannot tell the intrinsic's reads from the stages still in
+// flight and puts a full vmcnt(0) before them, which drains the DMA ring every
+// stage. The assembly is not tracked, so its results are pending until
+// lds_tr8_ready ties them to an explicit lgkmcnt(0).
+__device__ __forceinline__ v2i lds_read_tr8_asm(const int8_t* p)
+{
+    v2i r;
+#if __HIP_DEVICE_COMPILE__
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)(p);
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(a) : "memory");
+#else
+    (void)p;
+    r = v2i{0, 0};
+#endif
+    return r;
+}
+
+// Waits for every outstanding LDS read of the wave and makes the 16 values
+// read by lds_read_tr8_asm depend on that wait, so no use moves above it.
+__device__ __forceinline__ void lds_tr8_ready(v2i (&lo)[8], v2i (&hi)[8])
+{
+#if __HIP_DEVICE_COMPILE__
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(lo[4]), "+v"(lo[5]), "+v"(lo[6]),
+                   "+v"(lo[7]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]), "+v"(hi[3]), "+v"(hi[4]), "+v"(hi[5]),
+                   "+v"(hi[6]), "+v"(hi[7])
+                 :
+                 : "memory");
+#else
+    (void)lo;
+    (void)hi;
+#endif
+}
+
 // Exchanges x's lanes 32..63 with y's lanes 0..31 (v_permlane32_swap): with
 // x = a word of lane half h = 0 / 1 and y the same for another word, lane
 // l < 32 ends with (x, y) = (x_l, x_{l+32}) and lane l + 32 with
@@ -687,6 +722,10 @@ __device__ __forceinline__ v4i buffer_load16_sc1(BufRsrc r, int voff)
 }
 
 enum { RING_S8 = 0, RING_S32 = 1, RING_PART = 2, RING_FP = 3 };
+
+// 16 zero bytes in global memory (never written): the address a lane loads
+// from when its table value is absent, so the load needs no branch.
+static __device__ __attribute__((aligned(16))) int32_t kZero16[4];
 
 struct RingSplit {
     int splits;        // K ranges per output tile
@@ -921,6 +960,38 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     };
 
+    // The output pass's column tables (bias[n], whose values start the
+    // accumulators of the fused modes, and the staged s_b) are loaded
+    // before the first stages are issued and used after: loaded behind the
+    // stages, their first use would wait for every stage in flight
+    // (loads retire in issue order), holding the first matrix work until
+    // the whole prologue had landed.
+    // Every lane loads unconditionally (a 16-byte zero stand-in where a
+    // value is absent) and selects at the use: a load under a branch is
+    // waited for where the branch joins, before the stages would go out.
+    const int32_t* const zero16 = kZero16;
+    v4i bpre[F16 ? 1 : FN][4];
+#pragma unroll
+    for (int j = 0; j < FN && !F16; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            bpre[j][g] = v4i{0, 0, 0, 0};
+            if constexpr (MODE != RING_PART) {
+                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                const bool live = p.ep.bias != nullptr && n < p.n;
+                bpre[j][g] = *reinterpret_cast<const v4i*>(live ? p.ep.bias + n : zero16);
+            }
+        }
+    }
+    const int nsb = n0 + 4 * (int)threadIdx.x;
+    const bool sb_live = kSbl && threadIdx.x < BN / 4 && p.ep.s_b != nullptr && nsb < p.n;
+    v4f sbpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kSbl) {
+        sbpre = *reinterpret_cast<const v4f*>(sb_live ? p.ep.s_b + nsb : reinterpret_cast<const float*>(zero16));
+    }
+    // keep those loads ahead of the stages
+    asm volatile("" ::: "memory");
+
     // Ring: stage s goes to slot s % NS; nothing is issued past this split's
     // last stage, so the vmcnt waits count only the stages really in flight.
 #pragma unroll
@@ -929,8 +1000,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             issue(s);
         }
     }
-    // Accumulators (transposed layout); the fused modes start from bias[n],
-    // whose loads go out after the first stages' so their latencies overlap.
+    // Accumulators (transposed layout); the fused modes start from bias[n].
 #pragma unroll
     for (int j = 0; j < FN && F16; ++j) {
 #pragma unroll
@@ -940,41 +1010,22 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     }
 #pragma unroll
     for (int j = 0; j < FN && !F16; ++j) {
-        int32_t b0[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v4i bv = v4i{0, 0, 0, 0};
-            if constexpr (MODE != RING_PART) {
-                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-                if (p.ep.bias != nullptr && n < p.n) {
-                    bv = *reinterpret_cast<const v4i*>(p.ep.bias + n);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                b0[4 * g + e] = bv[e];
-            }
-        }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                acc[i][j][r] = b0[r];
+                acc[i][j][r] = bpre[j][r / 4][r % 4];
             }
         }
     }
-
     if constexpr (kSbl) {
         if (threadIdx.x < BN / 4) {
-            const int n = n0 + 4 * (int)threadIdx.x;
-            v4f v = v4f{p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar};
-            if (p.ep.s_b != nullptr && n < p.n) {
-                v = *reinterpret_cast<const v4f*>(p.ep.s_b + n);
-            }
-            *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = v;
+            const float sc = p.ep.s_b_scalar;
+            *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = sb_live ? sbpre : v4f{sc, sc, sc, sc};
         }
     }
     if constexpr (kBl) {
+        // the fp bias (2 or 4 bytes per column) is rarer: loaded here
         if (threadIdx.x >= BN / 4 && threadIdx.x < BN / 2) {
             const int t = (int)threadIdx.x - BN / 4;
             const int n = n0 + 4 * t;
@@ -2015,7 +2066,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk,
     constexpr int Q = STEP / 1024;          // DMA instructions per step
     constexpr int RPQ = 1024 / CW;          // rows per DMA instruction
     constexpr int L = Q + 1;                // vector-memory ops per step: the DMA + 1 A load
-    static_assert(CB == 8 || CB == 16, "128- or 256-byte row segments");
+    static_assert(CB == 8, "128-byte row segments (lds_tr8_ready ties 8 column blocks)");
     static_assert(NSW >= 1 && (NSW - 1) * L < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) int8_t ring[4][NSW][STEP];
     static_assert(3 * CB * 64 * 16 <= 4 * NSW * STEP, "the waves' partial tiles fit the ring");
@@ -2087,14 +2138,19 @@ __global__ __launch_bounds__(256) void gemv_i8_kn_tr(GemmI8Kern p, RingSplit sk,
                 }
                 asm volatile("" ::: "memory");
                 const int8_t* st = ring[wave][u];
+                v2i lo[CB], hi[CB];
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) {
                     // the column block is chunk cb of the staged row
                     const int k0 = tr_k;
-                    const v2i lo = lds_read_tr8(st + k0 * CW + ((cb ^ swz(k0)) << 4) + tr_b);
-                    const v2i hi = lds_read_tr8(st + (k0 + 8) * CW + ((cb ^ swz(k0 + 8)) << 4) + tr_b);
-                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u], v4i{lo.x, lo.y, hi.x, hi.y}, acc[cb], 0,
-                                                                   0, 0);
+                    lo[cb] = lds_read_tr8_asm(st + k0 * CW + ((cb ^ swz(k0)) << 4) + tr_b);
+                    hi[cb] = lds_read_tr8_asm(st + (k0 + 8) * CW + ((cb ^ swz(k0 + 8)) << 4) + tr_b);
+                }
+                lds_tr8_ready(lo, hi);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u], v4i{lo[cb].x, lo[cb].y, hi[cb].x, hi[cb].y},
+                                                                   acc[cb], 0, 0, 0);
                 }
                 // the slot's reads are done before the next step's DMA reuses it
                 __builtin_amdgcn_s_waitcnt(0xc07f);
