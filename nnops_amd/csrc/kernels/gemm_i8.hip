@@ -636,6 +636,39 @@ __device__ __forceinline__ v2i lds_read_tr8_asm(const int8_t* p)
     return r;
 }
 
+// lgkmcnt(0) with the fragments built from lds_read_tr8_asm as in/out
+// operands: their uses cannot move above it.
+template <int N>
+__device__ __forceinline__ void lds_tr8_ready_frags(v4i (&f)[N])
+{
+    static_assert(N == 1 || N == 2, "one or two fragments");
+#if __HIP_DEVICE_COMPILE__
+    if constexpr (N == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]) : : "memory");
+    } else {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]) : : "memory");
+    }
+#else
+    (void)f;
+#endif
+}
+
+// Waits until at most S stages of L vector-memory operations each are in
+// flight (S wave-uniform, clamped to MAXS).
+template <int L, int MAXS>
+__device__ __forceinline__ void wait_stages(int s)
+{
+    if constexpr (MAXS <= 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (s >= MAXS) {
+            wait_vmcnt<MAXS * L>();
+        } else {
+            wait_stages<L, MAXS - 1>(s);
+        }
+    }
+}
+
 // Waits for every outstanding LDS read of the wave and makes the 16 values
 // read by lds_read_tr8_asm depend on that wait, so no use moves above it.
 __device__ __forceinline__ void lds_tr8_ready(v2i (&lo)[8], v2i (&hi)[8])
@@ -791,6 +824,12 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     constexpr int QA = BM / RPI / W;              // load instructions per wave per stage (A)
     constexpr int QB = BN / RPI / W;
     constexpr int L = QA + QB;                    // vector-memory ops per wave per stage
+    // TRB rings of 128 rows and more: the transposed reads as untracked
+    // assembly, per-stage counted waits to the end and step 0 peeled, so no
+    // full vmcnt(0) drains the ring (4096^3: 73 -> 69 us; 333 x 4096 x
+    // 14336: 46 -> 40 us). The 64 x 64 tiles (a handful of stages, latency
+    // bound) and the [N,K] rings measured faster without.
+    constexpr bool kTrAsm = TRB && BM >= 128;
     constexpr int S = BK / 32;                    // 32-k MFMA slices per stage
     constexpr int kStage = (BM + BN) * BK;
     constexpr int kPitch8 = TN + 16;              // staged byte row pitch: 2-way bank conflicts at most
@@ -894,9 +933,18 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     auto frag_tr = [&](const int8_t* stb, int col, int ks) {
         const int k0 = 32 * ks + tr_k;
         const int c = col + tr_c;
-        const v2i lo = lds_read_tr8(stb + k0 * BN + (((c >> 4) ^ swzb(k0)) << 4) + (c & 15));
-        const v2i hi = lds_read_tr8(stb + (k0 + 8) * BN + (((c >> 4) ^ swzb(k0 + 8)) << 4) + (c & 15));
-        return v4i{lo.x, lo.y, hi.x, hi.y};
+        const int8_t* plo = stb + k0 * BN + (((c >> 4) ^ swzb(k0)) << 4) + (c & 15);
+        const int8_t* phi = stb + (k0 + 8) * BN + (((c >> 4) ^ swzb(k0 + 8)) << 4) + (c & 15);
+        if constexpr (kTrAsm) {
+            // untracked reads: step() ties them to an lgkmcnt(0) before their use
+            const v2i lo = lds_read_tr8_asm(plo);
+            const v2i hi = lds_read_tr8_asm(phi);
+            return v4i{lo.x, lo.y, hi.x, hi.y};
+        } else {
+            const v2i lo = lds_read_tr8(plo);
+            const v2i hi = lds_read_tr8(phi);
+            return v4i{lo.x, lo.y, hi.x, hi.y};
+        }
     };
     auto read_frags = [&](const int8_t* st, int ks, v4i (&fa)[FM], v4i (&fb)[FN]) {
         if constexpr (TRB) {
@@ -960,37 +1008,38 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         }
     };
 
-    // The output pass's column tables (bias[n], whose values start the
-    // accumulators of the fused modes, and the staged s_b) are loaded
-    // before the first stages are issued and used after: loaded behind the
-    // stages, their first use would wait for every stage in flight
-    // (loads retire in issue order), holding the first matrix work until
-    // the whole prologue had landed.
-    // Every lane loads unconditionally (a 16-byte zero stand-in where a
-    // value is absent) and selects at the use: a load under a branch is
-    // waited for where the branch joins, before the stages would go out.
+    // The output pass's column tables: bias[n] (whose values start the
+    // accumulators of the fused modes), the staged s_b and fp bias.
+    // kTrAsm: bias[n] and s_b are loaded before the first stages are issued
+    // and used after (with step 0 peeled the first use then waits for these
+    // loads alone); every lane loads unconditionally, from a 16-byte zero
+    // stand-in where a value is absent, since a load under a branch is waited
+    // for where the branch joins. Elsewhere they follow the first stages
+    // (measured as fast or faster there).
     const int32_t* const zero16 = kZero16;
-    v4i bpre[F16 ? 1 : FN][4];
+    v4i bpre[kTrAsm ? FN : 1][4];
+    const int nsb = n0 + 4 * (int)threadIdx.x;
+    const bool sb_live = kTrAsm && kSbl && threadIdx.x < BN / 4 && p.ep.s_b != nullptr && nsb < p.n;
+    v4f sbpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kTrAsm) {
 #pragma unroll
-    for (int j = 0; j < FN && !F16; ++j) {
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            bpre[j][g] = v4i{0, 0, 0, 0};
-            if constexpr (MODE != RING_PART) {
-                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
-                const bool live = p.ep.bias != nullptr && n < p.n;
-                bpre[j][g] = *reinterpret_cast<const v4i*>(live ? p.ep.bias + n : zero16);
+            for (int g = 0; g < 4; ++g) {
+                bpre[j][g] = v4i{0, 0, 0, 0};
+                if constexpr (MODE != RING_PART) {
+                    const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                    const bool live = p.ep.bias != nullptr && n < p.n;
+                    bpre[j][g] = *reinterpret_cast<const v4i*>(live ? p.ep.bias + n : zero16);
+                }
             }
         }
+        if constexpr (kSbl) {
+            sbpre = *reinterpret_cast<const v4f*>(sb_live ? p.ep.s_b + nsb : reinterpret_cast<const float*>(zero16));
+        }
+        // keep those loads ahead of the stages
+        asm volatile("" ::: "memory");
     }
-    const int nsb = n0 + 4 * (int)threadIdx.x;
-    const bool sb_live = kSbl && threadIdx.x < BN / 4 && p.ep.s_b != nullptr && nsb < p.n;
-    v4f sbpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (kSbl) {
-        sbpre = *reinterpret_cast<const v4f*>(sb_live ? p.ep.s_b + nsb : reinterpret_cast<const float*>(zero16));
-    }
-    // keep those loads ahead of the stages
-    asm volatile("" ::: "memory");
 
     // Ring: stage s goes to slot s % NS; nothing is issued past this split's
     // last stage, so the vmcnt waits count only the stages really in flight.
@@ -1010,22 +1059,46 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
     }
 #pragma unroll
     for (int j = 0; j < FN && !F16; ++j) {
+        int32_t b0[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i bv = v4i{0, 0, 0, 0};
+            if constexpr (kTrAsm) {
+                bv = bpre[j][g];
+            } else if constexpr (MODE != RING_PART) {
+                const int n = n0 + wn0 + j * 32 + 8 * g + 4 * (lane >> 5);
+                if (p.ep.bias != nullptr && n < p.n) {
+                    bv = *reinterpret_cast<const v4i*>(p.ep.bias + n);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b0[4 * g + e] = bv[e];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                acc[i][j][r] = bpre[j][r / 4][r % 4];
+                acc[i][j][r] = b0[r];
             }
         }
     }
     if constexpr (kSbl) {
         if (threadIdx.x < BN / 4) {
-            const float sc = p.ep.s_b_scalar;
-            *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = sb_live ? sbpre : v4f{sc, sc, sc, sc};
+            const int n = n0 + 4 * (int)threadIdx.x;
+            v4f v = v4f{p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar, p.ep.s_b_scalar};
+            if constexpr (kTrAsm) {
+                if (sb_live) {
+                    v = sbpre;
+                }
+            } else if (p.ep.s_b != nullptr && n < p.n) {
+                v = *reinterpret_cast<const v4f*>(p.ep.s_b + n);
+            }
+            *reinterpret_cast<v4f*>(&sbl[4 * threadIdx.x]) = v;
         }
     }
     if constexpr (kBl) {
-        // the fp bias (2 or 4 bytes per column) is rarer: loaded here
         if (threadIdx.x >= BN / 4 && threadIdx.x < BN / 2) {
             const int t = (int)threadIdx.x - BN / 4;
             const int n = n0 + 4 * t;
@@ -1041,8 +1114,11 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             *reinterpret_cast<v4f*>(&biasl[4 * t]) = v;
         }
     }
-    if (kt >= NS - 1) {
-        wait_vmcnt<(NS - 2) * L>();   // stage 0 landed, stages 1..NS-2 may be in flight
+    // stage 0 landed; the others issued (up to NS - 2) may stay in flight
+    if constexpr (kTrAsm) {
+        wait_stages<L, NS - 2>(min(kt, NS - 1) - 1);
+    } else if (kt >= NS - 1) {
+        wait_vmcnt<(NS - 2) * L>();
     } else {
         wait_vmcnt<0>();
     }
@@ -1067,13 +1143,20 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             v4i (&cb)[FN] = (ks & 1) ? f1b : f0b;
             v4i (&na)[FM] = (ks & 1) ? f0a : f1a;
             v4i (&nb)[FN] = (ks & 1) ? f0b : f1b;
+            if constexpr (kTrAsm) {
+                lds_tr8_ready_frags(cb);
+            }
             if (ks + 1 < S) {
                 read_frags(st, ks + 1, na, nb);
                 mfma_all(ca, cb);
                 schedule(false);
             } else {
                 mfma_all(ca, cb);
-                if (more) {
+                if constexpr (kTrAsm) {
+                    // stage t + 1 landed; the ones after it may stay in
+                    // flight (all issued: kt - 2 - t of them)
+                    wait_stages<L, NS - 2>(more ? NS - 2 : kt - 2 - t);
+                } else if (more) {
                     wait_vmcnt<(NS - 2) * L>();
                 } else {
                     wait_vmcnt<0>();
@@ -1086,7 +1169,17 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             }
         }
     };
-    for (int t = 0; t < kt; ++t) {
+    // kTrAsm: step 0 outside the loop (the accumulators start from loaded
+    // values, and a loop that uses loaded values while issuing loads of its
+    // own gets a full vmcnt(0) before it)
+    int t0 = 0;
+    if constexpr (kTrAsm) {
+        if (kt > 0) {
+            step(0);
+        }
+        t0 = 1;
+    }
+    for (int t = t0; t < kt; ++t) {
         step(t);
     }
     // The output pass's per-column scales: from the LDS copy staged at the
