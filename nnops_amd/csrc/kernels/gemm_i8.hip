@@ -1358,8 +1358,11 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         // columns cp.n .. + 3
         // CLIP: a finite clip range (the default -inf / +inf clip is the
         // identity for every value, NaN included, and is left out)
-        auto values = [&](int i, int j, int g, const ColFp& cp, float sa, auto clip_c) {
+        // PLAIN: no residual, no fp bias, no Relu and no clip (host-known):
+        // the value is v * (s_a * s_b[n]) alone, with no per-element branches
+        auto values = [&](int i, int j, int g, const ColFp& cp, float sa, auto clip_c, auto plain_c) {
             constexpr bool kClip = decltype(clip_c)::value;
+            constexpr bool kPlain = decltype(plain_c)::value;
             const int n = cp.n;
             const int m = m0 + wm0 + i * 32 + (lane & 31);
             v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1367,7 +1370,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                 return o;
             }
             v4f old = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (ep.add_to) {
+            if (!kPlain && ep.add_to) {
                 const char* cptr = static_cast<const char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
                 if (f16) {
                     const _Float16* o16 = reinterpret_cast<const _Float16*>(cptr);
@@ -1379,6 +1382,10 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float f = __fmul_rn((float)acc[i][j][4 * g + e], __fmul_rn(sa, cp.sb[e]));
+                if constexpr (kPlain) {
+                    o[e] = f;
+                    continue;
+                }
                 if (ep.bias_fp != nullptr) {
                     f = __fadd_rn(f, cp.bias[e]);
                 }
@@ -1414,7 +1421,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             // [TM][128-byte] tile of one slab of columns (32 f32 or 64 f16),
             // entries of 4 columns at slot q ^ (row % groups) in the row.
             int8_t* tile = ring + wave * (TM * 128);
-            auto slab = [&](auto esz_c, auto clip_c) {
+            auto slab = [&](auto esz_c, auto clip_c, auto plain_c) {
                 constexpr int ESZ = decltype(esz_c)::value;          // output element bytes
                 constexpr int SC = (TN < 128 / ESZ) ? TN : 128 / ESZ; // columns per slab
                 constexpr int GPS = SC / 4;                          // 4-column entries per slab row
@@ -1433,7 +1440,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
                             for (int i = 0; i < FM; ++i) {
                                 const int r = i * 32 + (lane & 31);
-                                const v4f o = values(i, j, g, cp, sa_i[i], clip_c);
+                                const v4f o = values(i, j, g, cp, sa_i[i], clip_c, plain_c);
                                 int8_t* dst = tile + r * RB + ((q ^ (r % GPS)) * E);
                                 if constexpr (ESZ == 4) {
                                     *reinterpret_cast<v4f*>(dst) = o;
@@ -1464,7 +1471,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                         if (m < p.m && n < p.n) {
                             char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * ESZ;
                             if (n + 16 / ESZ <= p.n) {
-                                *reinterpret_cast<v4i*>(cptr) = v;
+                                __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(cptr));
                             } else {
                                 // a row's last group of 4 columns (N % 8 == 4, f16)
                                 *reinterpret_cast<uint2*>(cptr) = uint2{(uint32_t)v.x, (uint32_t)v.y};
@@ -1478,14 +1485,19 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             using TrueC = std::integral_constant<bool, true>;
             using FalseC = std::integral_constant<bool, false>;
             const bool clip = !(ep.min_clip == -__builtin_inff() && ep.max_clip == __builtin_inff());
-            if (f16 && clip) {
-                slab(std::integral_constant<int, 2>{}, TrueC{});
+            const bool plain = !clip && !relu && !ep.add_to && ep.bias_fp == nullptr;
+            if (f16 && plain) {
+                slab(std::integral_constant<int, 2>{}, FalseC{}, TrueC{});
+            } else if (f16 && clip) {
+                slab(std::integral_constant<int, 2>{}, TrueC{}, FalseC{});
             } else if (f16) {
-                slab(std::integral_constant<int, 2>{}, FalseC{});
+                slab(std::integral_constant<int, 2>{}, FalseC{}, FalseC{});
+            } else if (plain) {
+                slab(std::integral_constant<int, 4>{}, FalseC{}, TrueC{});
             } else if (clip) {
-                slab(std::integral_constant<int, 4>{}, TrueC{});
+                slab(std::integral_constant<int, 4>{}, TrueC{}, FalseC{});
             } else {
-                slab(std::integral_constant<int, 4>{}, FalseC{});
+                slab(std::integral_constant<int, 4>{}, FalseC{}, FalseC{});
             }
         } else {
 #pragma unroll
@@ -1500,7 +1512,8 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                         if (m >= p.m || n >= p.n) {
                             continue;
                         }
-                        const v4f o = values(i, j, g, cp, sa_i[i], std::integral_constant<bool, true>{});
+                        const v4f o = values(i, j, g, cp, sa_i[i], std::integral_constant<bool, true>{},
+                                             std::integral_constant<bool, false>{});
                         char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
                         if (f16) {
                             _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
