@@ -97,9 +97,9 @@ __device__ __forceinline__ float load_a(const Q41Kern& p, int m, int k)
 __device__ __forceinline__ void store_out(const Q41Kern& p, int m, int n, float v)
 {
     if (p.out_f16) {
-        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
+        __builtin_nontemporal_store((_Float16)v, static_cast<_Float16*>(p.c) + (int64_t)m * p.ldc + n);
     } else {
-        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
+        __builtin_nontemporal_store(v, static_cast<float*>(p.c) + (int64_t)m * p.ldc + n);
     }
 }
 
@@ -2704,9 +2704,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_q4_1_ring(Q41Kern p)
                     // SPLIT: the row's power-of-two factor (exact)
                     const float v = SPLIT ? acc[i][j][r] * p.row_scale[m] : acc[i][j][r];
                     if constexpr (OUT16) {
-                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
+                        __builtin_nontemporal_store((_Float16)v, static_cast<_Float16*>(p.c) + (int64_t)m * p.ldc + n);
                     } else {
-                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
+                        __builtin_nontemporal_store(v, static_cast<float*>(p.c) + (int64_t)m * p.ldc + n);
                     }
                 }
             }
@@ -2982,9 +2982,9 @@ __global__ __launch_bounds__(512, 1) void gemm_q4_1_kn_ring(Q41Kern p)
                     // SPLIT: the row's power-of-two factor (exact)
                     const float v = SPLIT ? acc[i][r] * p.row_scale[m] : acc[i][r];
                     if constexpr (OUT16) {
-                        static_cast<_Float16*>(p.c)[(int64_t)m * p.ldc + n] = (_Float16)v;
+                        __builtin_nontemporal_store((_Float16)v, static_cast<_Float16*>(p.c) + (int64_t)m * p.ldc + n);
                     } else {
-                        static_cast<float*>(p.c)[(int64_t)m * p.ldc + n] = v;
+                        __builtin_nontemporal_store(v, static_cast<float*>(p.c) + (int64_t)m * p.ldc + n);
                     }
                 }
             }
