@@ -1358,11 +1358,14 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
         // columns cp.n .. + 3
         // CLIP: a finite clip range (the default -inf / +inf clip is the
         // identity for every value, NaN included, and is left out)
-        // PLAIN: no residual, no fp bias, no Relu and no clip (host-known):
-        // the value is v * (s_a * s_b[n]) alone, with no per-element branches
-        auto values = [&](int i, int j, int g, const ColFp& cp, float sa, auto clip_c, auto plain_c) {
+        // FORM (host-known) > 0: no residual and no clip, so the value is
+        // v * (s_a * s_b[n]) [+ bias[n]] [Relu] with no per-element branches
+        // (1: neither, 2: bias, 3: Relu, 4: both), the general order's
+        // operations; 0: the general pass
+        auto values = [&](int i, int j, int g, const ColFp& cp, float sa, auto clip_c, auto form_c) {
             constexpr bool kClip = decltype(clip_c)::value;
-            constexpr bool kPlain = decltype(plain_c)::value;
+            constexpr int kForm = decltype(form_c)::value;
+            constexpr bool kPlain = kForm > 0;
             const int n = cp.n;
             const int m = m0 + wm0 + i * 32 + (lane & 31);
             v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1383,6 +1386,12 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             for (int e = 0; e < 4; ++e) {
                 float f = __fmul_rn((float)acc[i][j][4 * g + e], __fmul_rn(sa, cp.sb[e]));
                 if constexpr (kPlain) {
+                    if constexpr (kForm == 2 || kForm == 4) {
+                        f = __fadd_rn(f, cp.bias[e]);
+                    }
+                    if constexpr (kForm == 3 || kForm == 4) {
+                        f = f > 0.0f ? f : 0.0f;
+                    }
                     o[e] = f;
                     continue;
                 }
@@ -1421,7 +1430,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             // [TM][128-byte] tile of one slab of columns (32 f32 or 64 f16),
             // entries of 4 columns at slot q ^ (row % groups) in the row.
             int8_t* tile = ring + wave * (TM * 128);
-            auto slab = [&](auto esz_c, auto clip_c, auto plain_c) {
+            auto slab = [&](auto esz_c, auto clip_c, auto form_c) {
                 constexpr int ESZ = decltype(esz_c)::value;          // output element bytes
                 constexpr int SC = (TN < 128 / ESZ) ? TN : 128 / ESZ; // columns per slab
                 constexpr int GPS = SC / 4;                          // 4-column entries per slab row
@@ -1440,7 +1449,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
 #pragma unroll
                             for (int i = 0; i < FM; ++i) {
                                 const int r = i * 32 + (lane & 31);
-                                const v4f o = values(i, j, g, cp, sa_i[i], clip_c, plain_c);
+                                const v4f o = values(i, j, g, cp, sa_i[i], clip_c, form_c);
                                 int8_t* dst = tile + r * RB + ((q ^ (r % GPS)) * E);
                                 if constexpr (ESZ == 4) {
                                     *reinterpret_cast<v4f*>(dst) = o;
@@ -1485,19 +1494,28 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
             using TrueC = std::integral_constant<bool, true>;
             using FalseC = std::integral_constant<bool, false>;
             const bool clip = !(ep.min_clip == -__builtin_inff() && ep.max_clip == __builtin_inff());
-            const bool plain = !clip && !relu && !ep.add_to && ep.bias_fp == nullptr;
-            if (f16 && plain) {
-                slab(std::integral_constant<int, 2>{}, FalseC{}, TrueC{});
-            } else if (f16 && clip) {
-                slab(std::integral_constant<int, 2>{}, TrueC{}, FalseC{});
-            } else if (f16) {
-                slab(std::integral_constant<int, 2>{}, FalseC{}, FalseC{});
-            } else if (plain) {
-                slab(std::integral_constant<int, 4>{}, FalseC{}, TrueC{});
-            } else if (clip) {
-                slab(std::integral_constant<int, 4>{}, TrueC{}, FalseC{});
+            using F0 = std::integral_constant<int, 0>;
+            const bool fast = !clip && !ep.add_to;
+            const int form = !fast ? 0 : 1 + (ep.bias_fp != nullptr ? 1 : 0) + (relu ? 2 : 0);
+            auto run = [&](auto esz_c) {
+                if (form == 1) {
+                    slab(esz_c, FalseC{}, std::integral_constant<int, 1>{});
+                } else if (form == 2) {
+                    slab(esz_c, FalseC{}, std::integral_constant<int, 2>{});
+                } else if (form == 3) {
+                    slab(esz_c, FalseC{}, std::integral_constant<int, 3>{});
+                } else if (form == 4) {
+                    slab(esz_c, FalseC{}, std::integral_constant<int, 4>{});
+                } else if (clip) {
+                    slab(esz_c, TrueC{}, F0{});
+                } else {
+                    slab(esz_c, FalseC{}, F0{});
+                }
+            };
+            if (f16) {
+                run(std::integral_constant<int, 2>{});
             } else {
-                slab(std::integral_constant<int, 4>{}, FalseC{}, FalseC{});
+                run(std::integral_constant<int, 4>{});
             }
         } else {
 #pragma unroll
@@ -1513,7 +1531,7 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                             continue;
                         }
                         const v4f o = values(i, j, g, cp, sa_i[i], std::integral_constant<bool, true>{},
-                                             std::integral_constant<bool, false>{});
+                                             std::integral_constant<int, 0>{});
                         char* cptr = static_cast<char*>(p.c) + (int64_t)m * p.ldc_bytes + (int64_t)n * (f16 ? 2 : 4);
                         if (f16) {
                             _Float16 h[4] = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
