@@ -1607,7 +1607,13 @@ void gemm_i8_ring(GemmI8Kern p, RingSplit sk)
                 const int n = n0 + cc * 4;
                 const v4i v = *reinterpret_cast<const v4i*>(ring + sr * kRowB + cc * 16);
                 if (m < p.m && n < p.n) {
-                    *reinterpret_cast<v4i*>(cbase + (int64_t)m * ld + (int64_t)n * 4) = v;
+                    // the int32 destination is written once; the partials are
+                    // read back by the reduce, so they keep the default policy
+                    if constexpr (MODE == RING_S32) {
+                        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(cbase + (int64_t)m * ld + (int64_t)n * 4));
+                    } else {
+                        *reinterpret_cast<v4i*>(cbase + (int64_t)m * ld + (int64_t)n * 4) = v;
+                    }
                 }
             }
             if (pass + 1 < FM / PI) {
